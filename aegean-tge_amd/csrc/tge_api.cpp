@@ -1,0 +1,646 @@
+// C ABI of the gfx950 paged-KV path: backend bring-up, page pools, per-step
+// batch plans and the kernel entry points. See include/tge_kv.h.
+#include "tge_kv.h"
+
+#include <hip/hip_runtime.h>
+
+#include <algorithm>
+#include <cmath>
+#include <cstdlib>
+#include <cstring>
+#include <functional>
+#include <mutex>
+#include <stdexcept>
+#include <string>
+#include <vector>
+
+#include "tge_common.h"
+#include "tge_error.h"
+#include "tge_kernels.h"
+
+namespace {
+
+thread_local std::string g_last_error;
+
+int fail(int status, const std::string& msg) {
+  g_last_error = msg;
+  return status;
+}
+
+}  // namespace
+
+void tge::set_last_error(const std::string& message) { g_last_error = message; }
+
+namespace {
+
+#define TGE_HIP(call)                                                          \
+  do {                                                                         \
+    const hipError_t e_ = (call);                                              \
+    if (e_ != hipSuccess)                                                      \
+      return fail(TGE_ERR_DEVICE, std::string(#call ": ") + hipGetErrorString(e_)); \
+  } while (0)
+
+struct Backend {
+  std::once_flag once;
+  int status = TGE_ERR_UNAVAILABLE;
+  std::string arch;
+};
+Backend g_backend;
+
+int backend_ready() {
+  std::call_once(g_backend.once, [] {
+    const char* force = std::getenv("TGE_FORCE_UNAVAILABLE");
+    if (force && force[0] && std::strcmp(force, "0") != 0) {
+      g_backend.status = TGE_ERR_UNAVAILABLE;
+      return;
+    }
+    int n = 0;
+    if (hipGetDeviceCount(&n) != hipSuccess || n <= 0) return;
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess) return;
+    hipDeviceProp_t prop;
+    if (hipGetDeviceProperties(&prop, dev) != hipSuccess) return;
+    g_backend.arch = prop.gcnArchName;
+    if (g_backend.arch.rfind("gfx950", 0) == 0) g_backend.status = TGE_OK;
+  });
+  return g_backend.status;
+}
+
+size_t align256(size_t x) { return (x + 255) & ~size_t(255); }
+
+}  // namespace
+
+struct tge_kv_pool {
+  tge_kv_pool_desc desc{};
+  void* k = nullptr;
+  void* v = nullptr;
+  void* ks = nullptr;
+  void* vs = nullptr;
+  size_t kv_block_bytes = 0;    // one page block of K (or V)
+  size_t scale_block_bytes = 0;
+  size_t layer_blocks = 0;      // pages * kv_heads
+  size_t bytes = 0;
+};
+
+// Work lists of one attention kind (decode or prefill) for the current plan.
+struct AttnPlan {
+  std::vector<tge::WorkRec> work;
+  std::vector<tge::ReduceRec> reduce;
+  int row_groups = 1;
+  int parts = 0;
+  int max_splits = 0;
+  bool built = false;
+  // device image: work | reduce
+  char* dev = nullptr;
+  size_t dev_bytes = 0;
+  size_t off_reduce = 0;
+  char* host = nullptr;
+  size_t host_bytes = 0;
+  hipEvent_t staged = nullptr;
+  float* part_o = nullptr;
+  float* part_ml = nullptr;
+  size_t part_floats = 0;
+
+  ~AttnPlan() {
+    if (dev) (void)hipFree(dev);
+    if (host) (void)hipHostFree(host);
+    if (staged) (void)hipEventDestroy(staged);
+    if (part_o) (void)hipFree(part_o);
+    if (part_ml) (void)hipFree(part_ml);
+  }
+};
+
+struct tge_batch {
+  // Host copy of the plan.
+  std::vector<tge::SessionRec> sessions;
+  std::vector<int> tables;
+  std::vector<tge::RowRec> rows;
+  int kv_heads = 0, head_dim = 0, q_heads = 0, pages = 0, group = 1;
+  int max_rows = 0;  // largest n_new * group
+  bool planned = false;
+  AttnPlan decode, prefill;
+
+  // Device image: sessions | tables | rows (one allocation), pinned staging.
+  char* dev = nullptr;
+  size_t dev_bytes = 0;
+  char* host = nullptr;
+  size_t host_bytes = 0;
+  hipEvent_t staged = nullptr;
+  size_t off_sessions = 0, off_tables = 0, off_rows = 0;
+
+  ~tge_batch() {
+    if (dev) (void)hipFree(dev);
+    if (host) (void)hipHostFree(host);
+    if (staged) (void)hipEventDestroy(staged);
+  }
+};
+
+extern "C" {
+
+const char* tge_status_string(int status) {
+  switch (status) {
+    case TGE_OK: return "ok";
+    case TGE_ERR_INVALID: return "invalid argument";
+    case TGE_ERR_RUNTIME: return "runtime error";
+    case TGE_ERR_UNAVAILABLE: return "backend unavailable";
+    case TGE_ERR_DEVICE: return "device error";
+    case TGE_ERR_CAPACITY: return "capacity exceeded";
+    default: return "unknown status";
+  }
+}
+
+const char* tge_last_error(void) { return g_last_error.c_str(); }
+
+int tge_backend_init(void) {
+  const int s = backend_ready();
+  if (s != TGE_OK) return fail(s, "no gfx950 device available");
+  return TGE_OK;
+}
+
+const char* tge_backend_arch(void) {
+  backend_ready();
+  return g_backend.arch.c_str();
+}
+
+int tge_kv_k_index(int token, int dim) { return tge::k_index(token, dim); }
+int tge_kv_v_index(int token, int dim) { return tge::v_index(token, dim); }
+
+// ---------------------------------------------------------------------------
+// Pool
+// ---------------------------------------------------------------------------
+int tge_kv_pool_create(const tge_kv_pool_desc* desc, tge_kv_pool** out) {
+  if (!desc || !out) return fail(TGE_ERR_INVALID, "kv_pool_create: null argument");
+  const tge_kv_pool_desc& d = *desc;
+  if (d.layers <= 0 || d.pages <= 0 || d.kv_heads <= 0)
+    return fail(TGE_ERR_INVALID, "kv_pool_create: non-positive size");
+  if (d.head_dim != 64 && d.head_dim != 128)
+    return fail(TGE_ERR_INVALID, "kv_pool_create: head_dim must be 64 or 128");
+  if (d.format != TGE_KV_F16 && d.format != TGE_KV_I8)
+    return fail(TGE_ERR_INVALID, "kv_pool_create: unknown format");
+  if (d.format == TGE_KV_I8 && d.scale_format != TGE_SCALE_F16 &&
+      d.scale_format != TGE_SCALE_F32)
+    return fail(TGE_ERR_INVALID, "kv_pool_create: unknown scale format");
+  const int s = backend_ready();
+  if (s != TGE_OK) return fail(s, "kv_pool_create: backend unavailable");
+
+  auto* p = new tge_kv_pool;
+  p->desc = d;
+  const size_t elem = d.format == TGE_KV_F16 ? 2 : 1;
+  p->kv_block_bytes = (size_t)16 * d.head_dim * elem;
+  p->scale_block_bytes =
+      d.format == TGE_KV_I8 ? (size_t)16 * (d.head_dim / 32) * (d.scale_format == TGE_SCALE_F32 ? 4 : 2)
+                            : 0;
+  p->layer_blocks = (size_t)d.pages * d.kv_heads;
+  const size_t kv_total = p->kv_block_bytes * p->layer_blocks * d.layers;
+  const size_t sc_total = p->scale_block_bytes * p->layer_blocks * d.layers;
+  hipError_t e = hipMalloc(&p->k, kv_total);
+  if (e == hipSuccess) e = hipMalloc(&p->v, kv_total);
+  if (e == hipSuccess && sc_total) e = hipMalloc(&p->ks, sc_total);
+  if (e == hipSuccess && sc_total) e = hipMalloc(&p->vs, sc_total);
+  if (e == hipSuccess) e = hipMemset(p->k, 0, kv_total);
+  if (e == hipSuccess) e = hipMemset(p->v, 0, kv_total);
+  if (e == hipSuccess && sc_total) e = hipMemset(p->ks, 0, sc_total);
+  if (e == hipSuccess && sc_total) e = hipMemset(p->vs, 0, sc_total);
+  if (e != hipSuccess) {
+    tge_kv_pool_destroy(p);
+    return fail(e == hipErrorOutOfMemory ? TGE_ERR_CAPACITY : TGE_ERR_DEVICE,
+                std::string("kv_pool_create: ") + hipGetErrorString(e));
+  }
+  p->bytes = 2 * kv_total + 2 * sc_total;
+  *out = p;
+  return TGE_OK;
+}
+
+void tge_kv_pool_destroy(tge_kv_pool* p) {
+  if (!p) return;
+  if (p->k) (void)hipFree(p->k);
+  if (p->v) (void)hipFree(p->v);
+  if (p->ks) (void)hipFree(p->ks);
+  if (p->vs) (void)hipFree(p->vs);
+  delete p;
+}
+
+size_t tge_kv_pool_bytes(const tge_kv_pool* p) { return p ? p->bytes : 0; }
+
+int tge_kv_pool_layer(const tge_kv_pool* p, int layer, tge_kv_layer_view* out) {
+  if (!p || !out) return fail(TGE_ERR_INVALID, "kv_pool_layer: null argument");
+  if (layer < 0 || layer >= p->desc.layers)
+    return fail(TGE_ERR_INVALID, "kv_pool_layer: layer out of range");
+  const size_t kv = p->kv_block_bytes * p->layer_blocks * layer;
+  const size_t sc = p->scale_block_bytes * p->layer_blocks * layer;
+  out->k = static_cast<char*>(p->k) + kv;
+  out->v = static_cast<char*>(p->v) + kv;
+  out->k_scales = p->ks ? static_cast<char*>(p->ks) + sc : nullptr;
+  out->v_scales = p->vs ? static_cast<char*>(p->vs) + sc : nullptr;
+  out->kv_block_bytes = p->kv_block_bytes;
+  out->scale_block_bytes = p->scale_block_bytes;
+  return TGE_OK;
+}
+
+// ---------------------------------------------------------------------------
+// Batch plan
+// ---------------------------------------------------------------------------
+int tge_batch_create(tge_batch** out) {
+  if (!out) return fail(TGE_ERR_INVALID, "batch_create: null argument");
+  *out = new tge_batch;
+  return TGE_OK;
+}
+
+void tge_batch_destroy(tge_batch* b) { delete b; }
+
+namespace {
+
+// Pages per decode unit: enough units to cover the 256 CUs several times
+// over, at least 8 pages (2 per wave) so a unit amortises its Q load and
+// merge, rounded to whole rounds of the 4 waves.
+int decode_pages_per_unit(long total_unit_pages) {
+  constexpr long kTargetUnits = 1024;
+  long pps = (total_unit_pages + kTargetUnits - 1) / kTargetUnits;
+  pps = std::max<long>(pps, 8);
+  pps = (pps + tge::kWaves - 1) / tge::kWaves * tge::kWaves;
+  return (int)pps;
+}
+
+// Splits [0, pages) into n nearly equal ranges and appends one unit each.
+void add_units(std::vector<tge::WorkRec>& work, std::vector<tge::ReduceRec>& red,
+               int& parts, int& max_splits, tge::WorkRec base, int pages, int pps) {
+  const int n = std::max(1, (pages + pps - 1) / pps);
+  max_splits = std::max(max_splits, n);
+  if (n == 1) {
+    base.page_begin = 0;
+    base.page_end = pages;
+    base.part = -1;
+    work.push_back(base);
+    return;
+  }
+  const int chunk = (pages + n - 1) / n;
+  tge::ReduceRec r{};
+  r.session = base.session;
+  r.row_begin = base.row_begin;
+  r.rows = base.rows;
+  r.rows_per_query = base.rows_per_query;
+  r.head_base = base.head_base;
+  r.first_part = parts;
+  r.n_parts = 0;
+  for (int b = 0; b < pages; b += chunk) {
+    tge::WorkRec w = base;
+    w.page_begin = b;
+    w.page_end = std::min(pages, b + chunk);
+    w.part = parts++;
+    work.push_back(w);
+    ++r.n_parts;
+  }
+  red.push_back(r);
+}
+
+
+// Copies `bytes` from pinned staging to device memory on `st`, growing both
+// buffers as needed; waits for the previous copy out of the staging buffer
+// before overwriting it.
+int stage_upload(char*& host, size_t& host_bytes, char*& dev, size_t& dev_bytes,
+                 hipEvent_t& staged, size_t bytes, hipStream_t st,
+                 const std::function<void(char*)>& fill) {
+  bytes = std::max<size_t>(bytes, 256);
+  if (staged) TGE_HIP(hipEventSynchronize(staged));
+  if (bytes > host_bytes) {
+    if (host) TGE_HIP(hipHostFree(host));
+    host = nullptr;
+    TGE_HIP(hipHostMalloc(&host, bytes));
+    host_bytes = bytes;
+  }
+  if (bytes > dev_bytes) {
+    if (dev) {
+      TGE_HIP(hipStreamSynchronize(st));
+      TGE_HIP(hipFree(dev));
+    }
+    dev = nullptr;
+    TGE_HIP(hipMalloc(&dev, bytes));
+    dev_bytes = bytes;
+  }
+  fill(host);
+  TGE_HIP(hipMemcpyAsync(dev, host, bytes, hipMemcpyHostToDevice, st));
+  if (!staged) TGE_HIP(hipEventCreateWithFlags(&staged, hipEventDisableTiming));
+  TGE_HIP(hipEventRecord(staged, st));
+  return TGE_OK;
+}
+
+// Uploads an attention plan's lists and sizes its split-K partial buffers.
+int upload_plan(AttnPlan& pl, int head_dim, hipStream_t st) {
+  const size_t wbytes = pl.work.size() * sizeof(tge::WorkRec);
+  pl.off_reduce = align256(wbytes);
+  const size_t total = pl.off_reduce + pl.reduce.size() * sizeof(tge::ReduceRec);
+  int s = stage_upload(pl.host, pl.host_bytes, pl.dev, pl.dev_bytes, pl.staged, total, st,
+                       [&](char* h) {
+                         if (wbytes) std::memcpy(h, pl.work.data(), wbytes);
+                         if (!pl.reduce.empty())
+                           std::memcpy(h + pl.off_reduce, pl.reduce.data(),
+                                       pl.reduce.size() * sizeof(tge::ReduceRec));
+                       });
+  if (s != TGE_OK) return s;
+  const size_t rows_cap = 16 * (size_t)pl.row_groups;
+  const size_t need = (size_t)std::max(pl.parts, 1) * rows_cap * head_dim;
+  if (need > pl.part_floats) {
+    if (pl.part_o) {
+      TGE_HIP(hipStreamSynchronize(st));
+      TGE_HIP(hipFree(pl.part_o));
+      TGE_HIP(hipFree(pl.part_ml));
+    }
+    pl.part_o = pl.part_ml = nullptr;
+    TGE_HIP(hipMalloc(&pl.part_o, need * sizeof(float)));
+    TGE_HIP(hipMalloc(&pl.part_ml, need / head_dim * 2 * sizeof(float)));
+    pl.part_floats = need;
+  }
+  pl.built = true;
+  return TGE_OK;
+}
+
+void build_decode(tge_batch* b) {
+  AttnPlan& pl = b->decode;
+  pl.work.clear();
+  pl.reduce.clear();
+  pl.parts = pl.max_splits = 0;
+  pl.row_groups = std::max(1, std::min(4, (b->max_rows + 15) / 16));
+  long unit_pages = 0;
+  for (const auto& sr : b->sessions) unit_pages += (long)((sr.ctx + sr.n_new + 15) / 16) * b->kv_heads;
+  const int pps = decode_pages_per_unit(unit_pages);
+  for (int s = 0; s < (int)b->sessions.size(); ++s) {
+    const tge::SessionRec& sr = b->sessions[s];
+    const int pages = (sr.ctx + sr.n_new + 15) / 16;
+    for (int h = 0; h < b->kv_heads; ++h) {
+      tge::WorkRec w{};
+      w.session = s;
+      w.kv_head = h;
+      w.row_begin = 0;
+      w.rows = sr.n_new * b->group;
+      w.rows_per_query = b->group;
+      w.head_base = h * b->group;
+      add_units(pl.work, pl.reduce, pl.parts, pl.max_splits, w, pages, pps);
+    }
+  }
+}
+
+// Prefill units: (session, query head, 32-query tile) x splits of 64 pages.
+void build_prefill(tge_batch* b) {
+  AttnPlan& pl = b->prefill;
+  pl.work.clear();
+  pl.reduce.clear();
+  pl.parts = pl.max_splits = 0;
+  pl.row_groups = 2;
+  const int tile = 16 * pl.row_groups;
+  const int pps = 64;
+  for (int s = 0; s < (int)b->sessions.size(); ++s) {
+    const tge::SessionRec& sr = b->sessions[s];
+    for (int hq = 0; hq < b->q_heads; ++hq) {
+      for (int a = 0; a < sr.n_new; a += tile) {
+        tge::WorkRec w{};
+        w.session = s;
+        w.kv_head = hq / b->group;
+        w.row_begin = a;
+        w.rows = std::min(tile, sr.n_new - a);
+        w.rows_per_query = 1;
+        w.head_base = hq;
+        const int pages = (sr.ctx + a + w.rows + 15) / 16;
+        add_units(pl.work, pl.reduce, pl.parts, pl.max_splits, w, pages, pps);
+      }
+    }
+  }
+}
+
+}  // namespace
+
+int tge_batch_plan(tge_batch* b, const tge_kv_pool* pool, const tge_batch_desc* d,
+                   void* stream) {
+  if (!b || !pool || !d) return fail(TGE_ERR_INVALID, "batch_plan: null argument");
+  const int ns = d->n_sessions;
+  if (ns <= 0 || !d->ctx || !d->n_new || !d->table_offsets || !d->page_ids)
+    return fail(TGE_ERR_INVALID, "batch_plan: empty or incomplete description");
+  const int hkv = pool->desc.kv_heads, hd = pool->desc.head_dim;
+  if (d->q_heads <= 0 || d->q_heads % hkv != 0)
+    return fail(TGE_ERR_INVALID, "batch_plan: q_heads must be a multiple of kv_heads");
+  const int group = d->q_heads / hkv;
+  if (d->table_offsets[0] != 0)
+    return fail(TGE_ERR_INVALID, "batch_plan: table_offsets[0] must be 0");
+  const int n_entries = d->table_offsets[ns];
+  if (n_entries < 0) return fail(TGE_ERR_INVALID, "batch_plan: negative table size");
+
+  // Validate first: a failed plan leaves the batch unplanned, never half-built.
+  int max_rows = 0;
+  for (int s = 0; s < ns; ++s) {
+    const int ctx = d->ctx[s], nn = d->n_new[s];
+    const int lo = d->table_offsets[s], hi = d->table_offsets[s + 1];
+    if (ctx < 0 || nn < 1)
+      return fail(TGE_ERR_INVALID, "batch_plan: ctx must be >= 0 and n_new >= 1");
+    if (hi < lo || hi > n_entries)
+      return fail(TGE_ERR_INVALID, "batch_plan: table_offsets must not decrease");
+    const long need = ((long)ctx + nn + 15) / 16;
+    if (hi - lo < need)
+      return fail(TGE_ERR_INVALID, "batch_plan: block table shorter than the context");
+    for (long i = 0; i < need; ++i) {
+      const int id = d->page_ids[lo + i];
+      if (id < 0 || id >= pool->desc.pages)
+        return fail(TGE_ERR_INVALID, "batch_plan: page id outside the pool");
+    }
+    max_rows = std::max(max_rows, nn * group);
+  }
+
+  b->planned = false;
+  b->sessions.assign(ns, {});
+  b->rows.clear();
+  b->tables.assign(d->page_ids, d->page_ids + n_entries);
+  int q_row = 0;
+  for (int s = 0; s < ns; ++s) {
+    const int ctx = d->ctx[s], nn = d->n_new[s], lo = d->table_offsets[s];
+    b->sessions[s] = tge::SessionRec{ctx, nn, q_row, lo};
+    for (int j = 0; j < nn; ++j) {
+      const int pos = ctx + j;
+      b->rows.push_back(tge::RowRec{d->page_ids[lo + pos / 16], pos % 16});
+    }
+    q_row += nn;
+  }
+  b->kv_heads = hkv;
+  b->head_dim = hd;
+  b->q_heads = d->q_heads;
+  b->group = group;
+  b->pages = pool->desc.pages;
+  b->max_rows = max_rows;
+  b->prefill.built = false;
+  b->decode.built = false;
+
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  const size_t o_sess = 0;
+  const size_t o_tab = align256(o_sess + b->sessions.size() * sizeof(tge::SessionRec));
+  const size_t o_rows = align256(o_tab + b->tables.size() * sizeof(int));
+  const size_t total = o_rows + b->rows.size() * sizeof(tge::RowRec);
+  int s = stage_upload(b->host, b->host_bytes, b->dev, b->dev_bytes, b->staged, total, st,
+                       [&](char* h) {
+                         std::memcpy(h + o_sess, b->sessions.data(),
+                                     b->sessions.size() * sizeof(tge::SessionRec));
+                         if (!b->tables.empty())
+                           std::memcpy(h + o_tab, b->tables.data(), b->tables.size() * sizeof(int));
+                         std::memcpy(h + o_rows, b->rows.data(),
+                                     b->rows.size() * sizeof(tge::RowRec));
+                       });
+  if (s != TGE_OK) return s;
+  b->off_sessions = o_sess;
+  b->off_tables = o_tab;
+  b->off_rows = o_rows;
+  // Decode lists are built eagerly when the rows fit a decode unit (the
+  // common case: one upload per step serves every layer).
+  if (max_rows <= tge::kMaxRows) {
+    build_decode(b);
+    s = upload_plan(b->decode, hd, st);
+    if (s != TGE_OK) return s;
+  }
+  b->planned = true;
+  return TGE_OK;
+}
+
+int tge_batch_info(const tge_batch* b, int* rows, int* work_items, int* max_splits) {
+  if (!b || !b->planned) return fail(TGE_ERR_INVALID, "batch_info: batch not planned");
+  if (rows) *rows = (int)b->rows.size();
+  if (work_items) *work_items = (int)b->decode.work.size();
+  if (max_splits) *max_splits = b->decode.max_splits;
+  return TGE_OK;
+}
+
+namespace {
+
+int check_use(const tge_batch* b, const tge_kv_pool* p, int layer, const char* who) {
+  if (!b || !p) return fail(TGE_ERR_INVALID, std::string(who) + ": null argument");
+  if (!b->planned) return fail(TGE_ERR_INVALID, std::string(who) + ": batch not planned");
+  if (b->kv_heads != p->desc.kv_heads || b->head_dim != p->desc.head_dim ||
+      b->pages != p->desc.pages)
+    return fail(TGE_ERR_INVALID, std::string(who) + ": batch planned for another pool");
+  if (layer < 0 || layer >= p->desc.layers)
+    return fail(TGE_ERR_INVALID, std::string(who) + ": layer out of range");
+  return TGE_OK;
+}
+
+tge::AttnParams attn_params(const tge_batch* b, const tge_kv_pool* p, int layer,
+                            const float* q, float* out, const AttnPlan& pl) {
+  tge_kv_layer_view v{};
+  tge_kv_pool_layer(p, layer, &v);
+  tge::AttnParams a{};
+  a.kpool = v.k;
+  a.vpool = v.v;
+  a.kscale = v.k_scales;
+  a.vscale = v.v_scales;
+  a.sessions = reinterpret_cast<const tge::SessionRec*>(b->dev + b->off_sessions);
+  a.work = reinterpret_cast<const tge::WorkRec*>(pl.dev);
+  a.tables = reinterpret_cast<const int*>(b->dev + b->off_tables);
+  a.q = q;
+  a.out = out;
+  a.part_o = pl.part_o;
+  a.part_ml = pl.part_ml;
+  a.rows_cap = 16 * pl.row_groups;
+  a.kv_heads = b->kv_heads;
+  a.q_heads = b->q_heads;
+  a.scale_log2 = (float)(1.4426950408889634 / std::sqrt((double)b->head_dim));
+  return a;
+}
+
+int run_attention(const tge_batch* b, const tge_kv_pool* p, int layer, const float* q,
+                  float* out, void* stream, const AttnPlan& pl, bool qsplit) {
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  const tge::AttnParams a = attn_params(b, p, layer, q, out, pl);
+  TGE_HIP(tge::launch_attention(p->desc.format, p->desc.scale_format == TGE_SCALE_F32,
+                                b->head_dim, pl.row_groups, qsplit, (int)pl.work.size(), a, st));
+  if (!pl.reduce.empty()) {
+    tge::ReduceParams r{};
+    r.sessions = a.sessions;
+    r.items = reinterpret_cast<const tge::ReduceRec*>(pl.dev + pl.off_reduce);
+    r.part_o = pl.part_o;
+    r.part_ml = pl.part_ml;
+    r.out = out;
+    r.rows_cap = a.rows_cap;
+    r.q_heads = b->q_heads;
+    TGE_HIP(tge::launch_reduce(b->head_dim, (int)pl.reduce.size(), r, st));
+  }
+  return TGE_OK;
+}
+
+}  // namespace
+
+int tge_kv_append(const tge_batch* b, tge_kv_pool* p, int layer, const float* k,
+                  const float* v, void* stream) {
+  int s = check_use(b, p, layer, "kv_append");
+  if (s != TGE_OK) return s;
+  if (!k || !v) return fail(TGE_ERR_INVALID, "kv_append: null k/v");
+  tge_kv_layer_view view{};
+  tge_kv_pool_layer(p, layer, &view);
+  tge::AppendParams a{};
+  a.k = k;
+  a.v = v;
+  a.kpool = view.k;
+  a.vpool = view.v;
+  a.kscale = view.k_scales;
+  a.vscale = view.v_scales;
+  a.rows = reinterpret_cast<const tge::RowRec*>(b->dev + b->off_rows);
+  a.n_rows = (int)b->rows.size();
+  a.kv_heads = b->kv_heads;
+  a.head_dim = b->head_dim;
+  a.scale_f32 = p->desc.scale_format == TGE_SCALE_F32;
+  TGE_HIP(tge::launch_kv_append(p->desc.format, a, static_cast<hipStream_t>(stream)));
+  return TGE_OK;
+}
+
+int tge_decode_attention(const tge_batch* b, const tge_kv_pool* p, int layer,
+                         const float* q, float* out, void* stream) {
+  int s = check_use(b, p, layer, "decode_attention");
+  if (s != TGE_OK) return s;
+  if (!q || !out) return fail(TGE_ERR_INVALID, "decode_attention: null q/out");
+  if (!b->decode.built)
+    return fail(TGE_ERR_INVALID, "decode_attention: n_new * group exceeds 64 rows");
+  return run_attention(b, p, layer, q, out, stream, b->decode, true);
+}
+
+int tge_prefill_attention(const tge_batch* b, const tge_kv_pool* p, int layer,
+                          const float* q, float* out, void* stream) {
+  int s = check_use(b, p, layer, "prefill_attention");
+  if (s != TGE_OK) return s;
+  if (!q || !out) return fail(TGE_ERR_INVALID, "prefill_attention: null q/out");
+  // The prefill lists are built on first use after each plan (decode-only
+  // steps never pay for them) and reused by every layer.
+  tge_batch* mb = const_cast<tge_batch*>(b);
+  if (!mb->prefill.built) {
+    build_prefill(mb);
+    s = upload_plan(mb->prefill, b->head_dim, static_cast<hipStream_t>(stream));
+    if (s != TGE_OK) return s;
+  }
+  return run_attention(b, p, layer, q, out, stream, b->prefill, p->desc.format == TGE_KV_I8);
+}
+
+int tge_kv_gather(const tge_batch* b, const tge_kv_pool* p, int layer, int session,
+                  int count, void* k_rows, void* v_rows, void* k_scales, void* v_scales,
+                  void* stream) {
+  int s = check_use(b, p, layer, "kv_gather");
+  if (s != TGE_OK) return s;
+  if (session < 0 || session >= (int)b->sessions.size())
+    return fail(TGE_ERR_INVALID, "kv_gather: session out of range");
+  const tge::SessionRec& sr = b->sessions[session];
+  if (count < 0 || count > sr.ctx + sr.n_new)
+    return fail(TGE_ERR_INVALID, "kv_gather: count beyond the session's positions");
+  if (!k_rows || !v_rows) return fail(TGE_ERR_INVALID, "kv_gather: null rows");
+  const bool i8 = p->desc.format == TGE_KV_I8;
+  if (i8 && (!k_scales || !v_scales)) return fail(TGE_ERR_INVALID, "kv_gather: null scales");
+  tge_kv_layer_view view{};
+  tge_kv_pool_layer(p, layer, &view);
+  tge::GatherParams g{};
+  g.kpool = view.k;
+  g.vpool = view.v;
+  g.kscale = view.k_scales;
+  g.vscale = view.v_scales;
+  g.table = reinterpret_cast<const int*>(b->dev + b->off_tables) + sr.table_off;
+  g.count = count;
+  g.kv_heads = b->kv_heads;
+  g.head_dim = b->head_dim;
+  g.scale_bytes = p->desc.scale_format == TGE_SCALE_F32 ? 4 : 2;
+  g.k_rows = k_rows;
+  g.v_rows = v_rows;
+  g.k_scales = i8 ? k_scales : nullptr;
+  g.v_scales = i8 ? v_scales : nullptr;
+  TGE_HIP(tge::launch_kv_gather(p->desc.format, g, static_cast<hipStream_t>(stream)));
+  return TGE_OK;
+}
+
+}  // extern "C"

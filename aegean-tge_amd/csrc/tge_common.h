@@ -1,0 +1,163 @@
+// Shared host/device definitions of the gfx950 paged-KV path: page layout,
+// plan records, the reference's f32->f16 bit recipe and int8 block quantizer.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace tge {
+
+constexpr int kPageTokens = 16;  // block_table.hpp:19 kBlockTokens
+constexpr int kWaves = 4;        // waves per decode workgroup
+constexpr int kMaxRows = 64;     // query rows (n_new * group) per decode unit
+
+enum Format { kF16 = 1, kI8 = 2 };
+
+// ---------------------------------------------------------------------------
+// Page layout. One page block = 16 tokens x head_dim of one KV head. The
+// in-block order is the register order of the CDNA4 matrix-core operands, so
+// that every lane of a wave fetches its operand with one contiguous 16-byte
+// (f16) or 8-byte (int8) load and a wave's load covers a contiguous 1 KiB:
+//
+//  K (A operand of S^T = K Q^T, v_mfma_f32_16x16x16_f16, row = token):
+//    dim d -> pair p = d/32, half h = (d/16)&1, group g = (d/4)&3, e = d&3
+//    index = ((p*4 + g)*16 + t)*8 + h*4 + e
+//    lane (g, t) of a wave reads the 8 elements at ((p*4+g)*16+t)*8: the
+//    operand for dims 32p+4g.. (h=0) and 32p+16+4g.. (h=1).
+//  V (A operand of O^T = V^T P^T, row = dim):
+//    tile j = d/16, pair p = j/2, h = j&1, dl = d&15, g = t/4, e = t&3
+//    index = ((p*4 + g)*16 + dl)*8 + h*4 + e
+//    lane (g, dl) reads tokens 4g..4g+3 of dims 32p+dl (h=0), 32p+16+dl (h=1).
+//  Scales (I8): one per (token, 32-dim block b): index b*16 + t, so the four
+//    tokens a lane's accumulator rows cover are 4 consecutive scales.
+// ---------------------------------------------------------------------------
+__host__ __device__ inline int k_index(int t, int d) {
+  return ((((d >> 5) << 2) + ((d >> 2) & 3)) * 16 + t) * 8 + (((d >> 4) & 1) << 2) +
+         (d & 3);
+}
+__host__ __device__ inline int v_index(int t, int d) {
+  return ((((d >> 5) << 2) + (t >> 2)) * 16 + (d & 15)) * 8 + (((d >> 4) & 1) << 2) +
+         (t & 3);
+}
+__host__ __device__ inline int scale_index(int t, int b) { return b * 16 + t; }
+
+// ---------------------------------------------------------------------------
+// Plan records (built on the host once per step, read by every layer).
+// ---------------------------------------------------------------------------
+struct SessionRec {
+  int ctx;        // positions cached before this step
+  int n_new;      // new tokens (query rows per head) this step
+  int q_row;      // first row of the session in q/k/v/out
+  int table_off;  // first entry of the session's block table
+};
+
+// One attention workgroup: a session, a KV head, up to 16*NRG query rows and a
+// range of logical pages. Row r is query row_begin + r / rows_per_query of
+// head head_base + r % rows_per_query (decode: the GQA group of each new
+// token; prefill: consecutive queries of one head).
+struct WorkRec {
+  int session;
+  int kv_head;
+  int page_begin;  // logical page range [page_begin, page_end)
+  int page_end;
+  int part;        // partial slot, or -1 when the unit writes the output
+  int row_begin;
+  int rows;
+  int rows_per_query;
+  int head_base;
+  int pad0, pad1, pad2;
+};
+
+// One row set whose context was split over several units.
+struct ReduceRec {
+  int session;
+  int row_begin;
+  int rows;
+  int rows_per_query;
+  int head_base;
+  int first_part;
+  int n_parts;
+  int pad;
+};
+
+struct RowRec {  // one new token: destination page and slot
+  int page;
+  int slot;
+};
+
+// ---------------------------------------------------------------------------
+// Reference conversions, restated (bit-for-bit) for host and device.
+// ---------------------------------------------------------------------------
+__host__ __device__ inline uint32_t f32_as_u32(float x) {
+#ifdef __HIP_DEVICE_COMPILE__
+  return __float_as_uint(x);
+#else
+  uint32_t u;
+  __builtin_memcpy(&u, &x, 4);
+  return u;
+#endif
+}
+
+// kernels.hpp:358-386: truncate the mantissa and add the guard bit (first
+// dropped bit), so exact ties go away from zero and sticky bits are ignored;
+// |x| < 2^-24 flushes to signed zero, overflow gives infinity, NaN gives the
+// quiet pattern sign|0x7E00. Pure integer work, identical on every target.
+__host__ __device__ inline uint16_t float_to_half_ref(float value) {
+  const uint32_t u = f32_as_u32(value);
+  const uint32_t sign = (u >> 16) & 0x8000u;
+  const uint32_t biased = (u >> 23) & 0xFFu;
+  const uint32_t frac = u & 0x7FFFFFu;
+  if (biased == 0xFFu) return (uint16_t)(sign | 0x7C00u | (frac ? 0x200u : 0u));
+  const int e = (int)biased - 127;
+  if (e < -24) return (uint16_t)sign;
+  if (e > 15) return (uint16_t)(sign | 0x7C00u);
+  if (e < -14) {
+    const uint32_t sig = 0x800000u | frac;
+    const uint32_t drop = (uint32_t)(-14 - e) + 13u;
+    return (uint16_t)(sign | ((sig >> drop) + ((sig >> (drop - 1u)) & 1u)));
+  }
+  const uint32_t kept = ((uint32_t)(e + 15) << 10) | (frac >> 13);
+  return (uint16_t)(sign | (kept + ((frac >> 12) & 1u)));
+}
+
+// static_cast<int>(float) as the reference's x86-64 build executes it
+// (cvttss2si): truncation toward zero, INT_MIN for NaN and out-of-range.
+__host__ __device__ inline int trunc_to_int_x86(float r) {
+  if (!(r > -2147483904.0f && r < 2147483648.0f)) return (int)0x80000000u;
+  return (int)r;
+}
+
+// qwen2.cpp:88-104 (quantize_kv_block) for 32 values: sequential absmax fold
+// in which a later equal value wins (an all-zero block keeps the sign of
+// element 31), correctly rounded fp32 division, then a separate multiply and
+// add per code (never contracted into an FMA), truncation and clamp.
+__host__ __device__ inline float quantize_block_ref(const float* x, int8_t* codes) {
+  float maximum = 0.0f;
+  for (int i = 0; i < 32; ++i) {
+    const float a = x[i] >= 0.0f ? x[i] : -x[i];
+    if (!(maximum > a)) maximum = a;
+  }
+#ifdef __HIP_DEVICE_COMPILE__
+  const float scale = __fdiv_rn(maximum, 127.0f);
+  const float inverse = scale != 0.0f ? __fdiv_rn(1.0f, scale) : 0.0f;
+#else
+  const float scale = maximum / 127.0f;
+  const float inverse = scale != 0.0f ? 1.0f / scale : 0.0f;
+#endif
+  for (int i = 0; i < 32; ++i) {
+#ifdef __HIP_DEVICE_COMPILE__
+    const float scaled = __fmul_rn(x[i], inverse);
+    const float rounded =
+        scaled >= 0.0f ? __fadd_rn(scaled, 0.5f) : __fadd_rn(scaled, -0.5f);
+#else
+    const float scaled = x[i] * inverse;
+    const float rounded = scaled >= 0.0f ? scaled + 0.5f : scaled - 0.5f;
+#endif
+    int c = trunc_to_int_x86(rounded);
+    c = c > 127 ? 127 : (c < -127 ? -127 : c);
+    codes[i] = (int8_t)c;
+  }
+  return scale;
+}
+
+}  // namespace tge

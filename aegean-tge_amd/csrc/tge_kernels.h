@@ -1,0 +1,78 @@
+// Kernel parameter blocks and launchers shared by the API layer and the
+// kernel translation units. Internal to libtge_kv.so.
+#pragma once
+
+#include <hip/hip_runtime.h>
+
+#include "tge_common.h"
+
+namespace tge {
+
+struct AppendParams {
+  const float* k;  // [n_rows][kv_heads*head_dim]
+  const float* v;
+  void* kpool;  // layer base of the K page blocks
+  void* vpool;
+  void* kscale;  // I8 only
+  void* vscale;
+  const RowRec* rows;  // device, n_rows
+  int n_rows;
+  int kv_heads;
+  int head_dim;
+  int scale_f32;
+};
+
+struct GatherParams {
+  const void* kpool;
+  const void* vpool;
+  const void* kscale;
+  const void* vscale;
+  const int* table;  // device, the session's page ids
+  int count;         // positions to gather
+  int kv_heads;
+  int head_dim;
+  int scale_bytes;  // 2 or 4
+  void* k_rows;
+  void* v_rows;
+  void* k_scales;  // NULL unless I8
+  void* v_scales;
+};
+
+struct AttnParams {
+  const void* kpool;  // layer base pointers
+  const void* vpool;
+  const void* kscale;
+  const void* vscale;
+  const SessionRec* sessions;
+  const WorkRec* work;
+  const int* tables;
+  const float* q;
+  float* out;
+  float* part_o;   // [parts][rows_cap][head_dim]
+  float* part_ml;  // [parts][rows_cap][2]: max (log2 domain), sum
+  int rows_cap;    // 16 * row groups of the plan
+  int kv_heads;
+  int q_heads;
+  float scale_log2;  // log2(e) / sqrt(head_dim)
+};
+
+struct ReduceParams {
+  const SessionRec* sessions;
+  const ReduceRec* items;
+  const float* part_o;
+  const float* part_ml;
+  float* out;
+  int rows_cap;
+  int q_heads;
+};
+
+hipError_t launch_kv_append(int format, const AppendParams& p, hipStream_t stream);
+hipError_t launch_kv_gather(int format, const GatherParams& p, hipStream_t stream);
+// row_groups: 16-row groups per unit (1..4). qsplit: Q as f16 hi + lo.
+hipError_t launch_attention(int format, int scale_f32, int head_dim, int row_groups,
+                            bool qsplit, int n_work, const AttnParams& p,
+                            hipStream_t stream);
+hipError_t launch_reduce(int head_dim, int n_items, const ReduceParams& p,
+                         hipStream_t stream);
+
+}  // namespace tge

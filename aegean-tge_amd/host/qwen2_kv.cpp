@@ -1,0 +1,370 @@
+// Qwen2-shaped paged KV driver and the C wrappers of the BlockTable and the
+// driver. See include/tge_amd/qwen2_kv.hpp and include/tge_kv.h.
+#include "tge_amd/qwen2_kv.hpp"
+
+#include "../csrc/tge_error.h"
+
+#include <algorithm>
+#include <stdexcept>
+#include <string>
+
+namespace tge::models {
+namespace {
+
+// A HIP/ABI failure below the driver: carries the C status.
+struct StatusError : std::runtime_error {
+  int status;
+  StatusError(int s, const std::string& what) : std::runtime_error(what), status(s) {}
+};
+
+void check(int status, const char* who) {
+  if (status != TGE_OK) {
+    throw StatusError(status, std::string(who) + ": " + tge_last_error());
+  }
+}
+
+}  // namespace
+
+Qwen2KvPath::Qwen2KvPath(const Qwen2KvConfig& config) : config_(config) {
+  if (config_.layers <= 0 || config_.q_heads <= 0 || config_.kv_heads <= 0 ||
+      config_.head_dim <= 0 || config_.sequences <= 0 || config_.context <= 0) {
+    throw std::invalid_argument("Qwen2KvPath: non-positive shape");
+  }
+  if (config_.q_heads % config_.kv_heads != 0) {
+    throw std::invalid_argument("Qwen2KvPath: q_heads must be a multiple of kv_heads");
+  }
+  if (config_.format == TGE_KV_I8 && (config_.kv_heads * config_.head_dim) % 32 != 0) {
+    // qwen2.cpp:406-409: the i8 cache needs kv_dim to be a multiple of 32.
+    throw std::invalid_argument("Qwen2KvPath: i8 KV needs kv_dim to be a multiple of 32");
+  }
+  config_.context = std::min(config_.context, kHardMaxContext);
+  if (config_.pages <= 0) {
+    config_.pages = config_.sequences * ((config_.context + kBlockTokens - 1) / kBlockTokens);
+  }
+  table_ = std::make_unique<BlockTable>(config_.pages, kBlockTokens);
+  pages_.assign(static_cast<std::size_t>(config_.sequences), {});
+  length_.assign(static_cast<std::size_t>(config_.sequences), 0);
+  tge_kv_pool_desc d{};
+  d.layers = config_.layers;
+  d.pages = config_.pages;
+  d.kv_heads = config_.kv_heads;
+  d.head_dim = config_.head_dim;
+  d.format = config_.format;
+  d.scale_format = config_.scale_format;
+  check(tge_kv_pool_create(&d, &pool_), "Qwen2KvPath");
+  check(tge_batch_create(&batch_), "Qwen2KvPath");
+}
+
+Qwen2KvPath::~Qwen2KvPath() {
+  tge_batch_destroy(batch_);
+  tge_kv_pool_destroy(pool_);
+}
+
+void Qwen2KvPath::check_sequence(int sequence, const char* who) const {
+  if (sequence < 0 || sequence >= config_.sequences) {
+    throw std::runtime_error(std::string(who) + ": sequence outside the model");
+  }
+}
+
+int Qwen2KvPath::length(int sequence) const {
+  check_sequence(sequence, "length");
+  return length_[static_cast<std::size_t>(sequence)];
+}
+
+const std::vector<int>& Qwen2KvPath::pages(int sequence) const {
+  check_sequence(sequence, "pages");
+  return pages_[static_cast<std::size_t>(sequence)];
+}
+
+void Qwen2KvPath::begin(const std::vector<Group>& groups, void* stream) {
+  begun_ = false;
+  // Validate everything before touching the table, so a failed call leaves
+  // the model unchanged.
+  std::vector<int> need_pages(static_cast<std::size_t>(config_.sequences), 0);
+  int extra = 0;
+  for (const Group& g : groups) {
+    const std::size_t s = static_cast<std::size_t>(g.sequence);
+    if (g.start > length_[s]) {
+      throw std::runtime_error("forward: position leaves a gap in the cache");
+    }
+    const int need = (g.start + g.count + kBlockTokens - 1) / kBlockTokens;
+    const int have = std::max(static_cast<int>(pages_[s].size()), need_pages[s]);
+    if (need > have) {
+      extra += need - have;
+      need_pages[s] = need;
+    }
+  }
+  if (extra > table_->free_count()) throw std::runtime_error("BlockTable: table full");
+
+  std::vector<int> ctx, n_new, offsets{0}, ids;
+  int max_count = 0;
+  for (const Group& g : groups) {
+    auto& list = pages_[static_cast<std::size_t>(g.sequence)];
+    const int need = (g.start + g.count + kBlockTokens - 1) / kBlockTokens;
+    while (static_cast<int>(list.size()) < need) list.push_back(table_->allocate());
+    length_[static_cast<std::size_t>(g.sequence)] = g.start + g.count;
+    ctx.push_back(g.start);
+    n_new.push_back(g.count);
+    ids.insert(ids.end(), list.begin(), list.end());
+    offsets.push_back(static_cast<int>(ids.size()));
+    max_count = std::max(max_count, g.count);
+  }
+  tge_batch_desc d{};
+  d.n_sessions = static_cast<int>(groups.size());
+  d.ctx = ctx.data();
+  d.n_new = n_new.data();
+  d.table_offsets = offsets.data();
+  d.page_ids = ids.data();
+  d.q_heads = config_.q_heads;
+  check(tge_batch_plan(batch_, pool_, &d, stream), "begin");
+  const int group = config_.q_heads / config_.kv_heads;
+  prefill_ = max_count > kSpeculativeBatch || max_count * group > 64;
+  step_rows_ = 0;
+  for (int c : n_new) step_rows_ += c;
+  begun_ = true;
+}
+
+void Qwen2KvPath::begin_forward(int sequence, int position, void* stream) {
+  // qwen2.cpp:2036-2044
+  if (position < 0 || position >= config_.context) {
+    throw std::runtime_error("forward: position outside the allocated context");
+  }
+  check_sequence(sequence, "forward");
+  begin({Group{sequence, position, 1}}, stream);
+}
+
+void Qwen2KvPath::begin_forward_batch(const int* positions, int count, const int* sequences,
+                                      void* stream) {
+  // qwen2.cpp:1615-1639
+  if (positions == nullptr || sequences == nullptr || count <= 0) {
+    throw std::runtime_error("forward_batch: invalid batch");
+  }
+  std::vector<Group> groups;
+  std::vector<int> seen(static_cast<std::size_t>(config_.sequences), 0);
+  for (int i = 0; i < count; ++i) {
+    if (positions[i] < 0 || positions[i] >= config_.context) {
+      throw std::runtime_error("forward_batch: position outside the context");
+    }
+    if (sequences[i] < 0 || sequences[i] >= config_.sequences) {
+      throw std::runtime_error("forward_batch: sequence outside the slots");
+    }
+    if (!groups.empty() && groups.back().sequence == sequences[i] &&
+        groups.back().start + groups.back().count == positions[i]) {
+      ++groups.back().count;
+      continue;
+    }
+    if (seen[static_cast<std::size_t>(sequences[i])]++) {
+      throw std::runtime_error(
+          "forward_batch: a sequence's rows must be consecutive positions");
+    }
+    groups.push_back(Group{sequences[i], positions[i], 1});
+  }
+  begin(groups, stream);
+}
+
+void Qwen2KvPath::begin_prefill(int sequence, int start_position, int count, void* stream) {
+  // qwen2.cpp:2132-2142
+  check_sequence(sequence, "prefill");
+  if (count <= 0 || start_position < 0 || start_position + count > config_.context) {
+    throw std::runtime_error("prefill: tokens outside the allocated context");
+  }
+  begin({Group{sequence, start_position, count}}, stream);
+}
+
+void Qwen2KvPath::begin_verify_draft(int sequence, int start_position, int count,
+                                     void* stream) {
+  // qwen2.cpp:2518-2531 (the reference pins sequence 0; any slot here)
+  if (count <= 0 || count > kSpeculativeBatch) {
+    throw std::runtime_error("verify_draft_logits: invalid draft");
+  }
+  check_sequence(sequence, "verify_draft");
+  if (start_position < 0 || start_position + count > config_.context) {
+    throw std::runtime_error("verify_draft: tokens outside the allocated context");
+  }
+  begin({Group{sequence, start_position, count}}, stream);
+}
+
+void Qwen2KvPath::layer(int layer, const float* q, const float* k, const float* v,
+                        float* out, void* stream) {
+  if (!begun_) throw std::runtime_error("layer: no step begun");
+  if (layer < 0 || layer >= config_.layers) {
+    throw std::invalid_argument("layer: layer out of range");
+  }
+  check(tge_kv_append(batch_, pool_, layer, k, v, stream), "layer");
+  if (prefill_) {
+    check(tge_prefill_attention(batch_, pool_, layer, q, out, stream), "layer");
+  } else {
+    check(tge_decode_attention(batch_, pool_, layer, q, out, stream), "layer");
+  }
+}
+
+void Qwen2KvPath::reset_cache(int sequence) {
+  // qwen2.cpp:2540-2543; zero-fill becomes page release.
+  if (sequence < 0 || sequence >= config_.sequences) {
+    throw std::runtime_error("reset_cache: sequence outside the model");
+  }
+  auto& list = pages_[static_cast<std::size_t>(sequence)];
+  for (int id : list) table_->release(id);
+  list.clear();
+  length_[static_cast<std::size_t>(sequence)] = 0;
+  begun_ = false;
+}
+
+void Qwen2KvPath::reset_cache() {
+  for (int s = 0; s < config_.sequences; ++s) reset_cache(s);
+}
+
+}  // namespace tge::models
+
+// ---------------------------------------------------------------------------
+// C wrappers
+// ---------------------------------------------------------------------------
+namespace {
+
+template <typename F>
+int guarded(F&& f) {
+  try {
+    f();
+    return TGE_OK;
+  } catch (const tge::models::StatusError& e) {
+    tge::set_last_error(e.what());
+    return e.status;
+  } catch (const std::invalid_argument& e) {
+    tge::set_last_error(e.what());
+    return TGE_ERR_INVALID;
+  } catch (const std::runtime_error& e) {
+    tge::set_last_error(e.what());
+    return TGE_ERR_RUNTIME;
+  } catch (const std::bad_alloc&) {
+    tge::set_last_error("out of host memory");
+    return TGE_ERR_CAPACITY;
+  }
+}
+
+}  // namespace
+
+struct tge_block_table {
+  tge::models::BlockTable impl;
+  tge_block_table(int blocks, int tokens) : impl(blocks, tokens) {}
+};
+
+struct tge_qwen2_kv {
+  tge::models::Qwen2KvPath impl;
+  explicit tge_qwen2_kv(const tge::models::Qwen2KvConfig& c) : impl(c) {}
+};
+
+extern "C" {
+
+int tge_block_table_create(int blocks, int block_tokens, tge_block_table** out) {
+  if (!out) return TGE_ERR_INVALID;
+  return guarded([&] { *out = new tge_block_table(blocks, block_tokens); });
+}
+void tge_block_table_destroy(tge_block_table* t) { delete t; }
+int tge_block_table_allocate(tge_block_table* t, int* block) {
+  if (!t || !block) return TGE_ERR_INVALID;
+  return guarded([&] { *block = t->impl.allocate(); });
+}
+int tge_block_table_share(tge_block_table* t, int block) {
+  if (!t) return TGE_ERR_INVALID;
+  return guarded([&] { t->impl.share(block); });
+}
+int tge_block_table_release(tge_block_table* t, int block) {
+  if (!t) return TGE_ERR_INVALID;
+  return guarded([&] { t->impl.release(block); });
+}
+int tge_block_table_refcount(const tge_block_table* t, int block, int* out) {
+  if (!t || !out) return TGE_ERR_INVALID;
+  return guarded([&] { *out = t->impl.refcount(block); });
+}
+int tge_block_table_free_count(const tge_block_table* t) {
+  return t ? t->impl.free_count() : TGE_ERR_INVALID;
+}
+int tge_block_table_capacity(const tge_block_table* t) {
+  return t ? t->impl.capacity() : TGE_ERR_INVALID;
+}
+int tge_block_table_remember_prefix(tge_block_table* t, uint64_t hash, int block) {
+  if (!t) return TGE_ERR_INVALID;
+  return guarded([&] { t->impl.remember_prefix(hash, block); });
+}
+int tge_block_table_find_prefix(const tge_block_table* t, uint64_t hash) {
+  return t ? t->impl.find_prefix(hash) : TGE_ERR_INVALID;
+}
+int tge_slot_for(int logical_pos, int block_tokens, int* block, int* offset) {
+  if (!block || !offset) return TGE_ERR_INVALID;
+  return guarded([&] {
+    const auto s = tge::models::BlockTable::slot_for(logical_pos, block_tokens);
+    *block = s.first;
+    *offset = s.second;
+  });
+}
+int tge_hash_tokens(const int* tokens, int count, uint64_t* out) {
+  if (!out) return TGE_ERR_INVALID;
+  return guarded([&] { *out = tge::models::BlockTable::hash_tokens(tokens, count); });
+}
+
+int tge_qwen2_kv_create(const tge_qwen2_kv_config* c, tge_qwen2_kv** out) {
+  if (!c || !out) return TGE_ERR_INVALID;
+  tge::models::Qwen2KvConfig cfg;
+  cfg.layers = c->layers;
+  cfg.q_heads = c->q_heads;
+  cfg.kv_heads = c->kv_heads;
+  cfg.head_dim = c->head_dim;
+  cfg.context = c->context;
+  cfg.sequences = c->sequences;
+  cfg.pages = c->pages;
+  cfg.format = c->format;
+  cfg.scale_format = c->scale_format;
+  return guarded([&] { *out = new tge_qwen2_kv(cfg); });
+}
+void tge_qwen2_kv_destroy(tge_qwen2_kv* m) { delete m; }
+int tge_qwen2_kv_begin_forward(tge_qwen2_kv* m, int sequence, int position, void* stream) {
+  if (!m) return TGE_ERR_INVALID;
+  return guarded([&] { m->impl.begin_forward(sequence, position, stream); });
+}
+int tge_qwen2_kv_begin_forward_batch(tge_qwen2_kv* m, const int* positions, int count,
+                                     const int* sequences, void* stream) {
+  if (!m) return TGE_ERR_INVALID;
+  return guarded([&] { m->impl.begin_forward_batch(positions, count, sequences, stream); });
+}
+int tge_qwen2_kv_begin_prefill(tge_qwen2_kv* m, int sequence, int start, int count,
+                               void* stream) {
+  if (!m) return TGE_ERR_INVALID;
+  return guarded([&] { m->impl.begin_prefill(sequence, start, count, stream); });
+}
+int tge_qwen2_kv_begin_verify(tge_qwen2_kv* m, int sequence, int start, int count,
+                              void* stream) {
+  if (!m) return TGE_ERR_INVALID;
+  return guarded([&] { m->impl.begin_verify_draft(sequence, start, count, stream); });
+}
+int tge_qwen2_kv_layer(tge_qwen2_kv* m, int layer, const float* q, const float* k,
+                       const float* v, float* out, void* stream) {
+  if (!m) return TGE_ERR_INVALID;
+  return guarded([&] { m->impl.layer(layer, q, k, v, out, stream); });
+}
+int tge_qwen2_kv_reset(tge_qwen2_kv* m, int sequence) {
+  if (!m) return TGE_ERR_INVALID;
+  return guarded([&] { m->impl.reset_cache(sequence); });
+}
+int tge_qwen2_kv_length(const tge_qwen2_kv* m, int sequence) {
+  if (!m) return TGE_ERR_INVALID;
+  int n = 0;
+  const int s = guarded([&] { n = m->impl.length(sequence); });
+  return s == TGE_OK ? n : s;
+}
+int tge_qwen2_kv_pages(const tge_qwen2_kv* m, int sequence, int* ids, int cap) {
+  if (!m) return TGE_ERR_INVALID;
+  int n = 0;
+  const int s = guarded([&] {
+    const auto& list = m->impl.pages(sequence);
+    n = static_cast<int>(list.size());
+    for (int i = 0; i < std::min(n, cap); ++i) ids[i] = list[static_cast<std::size_t>(i)];
+  });
+  return s == TGE_OK ? n : s;
+}
+const tge_kv_pool* tge_qwen2_kv_pool(const tge_qwen2_kv* m) { return m ? m->impl.pool() : nullptr; }
+const tge_batch* tge_qwen2_kv_batch(const tge_qwen2_kv* m) { return m ? m->impl.batch() : nullptr; }
+int tge_qwen2_kv_free_pages(const tge_qwen2_kv* m) {
+  return m ? m->impl.table().free_count() : TGE_ERR_INVALID;
+}
+
+}  // extern "C"

@@ -1,0 +1,495 @@
+"""Python binding of libtge_kv.so (include/tge_kv.h) over ctypes.
+
+The library is the product: gfx950 kernels for the paged-KV append, decode
+attention and chunked-prefill attention of the reference engine's Qwen2
+KV path, its C ABI and the C++20 Qwen2-shaped driver. This module only binds
+it. Device memory, copies and timing go through the system HIP runtime
+(libamdhip64, loaded by the library itself); there is no CPU fallback: if the
+library is missing or the GPU is unavailable, calls raise.
+"""
+from __future__ import annotations
+
+import ctypes as C
+import os
+from dataclasses import dataclass
+
+import numpy as np
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+LIB_PATH = os.path.join(HERE, "libtge_kv.so")
+
+PAGE_TOKENS = 16
+OK, ERR_INVALID, ERR_RUNTIME, ERR_UNAVAILABLE, ERR_DEVICE, ERR_CAPACITY = 0, -1, -2, -3, -4, -5
+KV_F16, KV_I8 = 1, 2
+SCALE_F16, SCALE_F32 = 0, 1
+
+_lib = None
+_hip = None
+
+
+class TgeError(RuntimeError):
+    def __init__(self, status, message):
+        super().__init__(f"{message} (status {status})")
+        self.status = status
+
+
+class PoolDesc(C.Structure):
+    _fields_ = [("layers", C.c_int), ("pages", C.c_int), ("kv_heads", C.c_int),
+                ("head_dim", C.c_int), ("format", C.c_int), ("scale_format", C.c_int)]
+
+
+class LayerView(C.Structure):
+    _fields_ = [("k", C.c_void_p), ("v", C.c_void_p), ("k_scales", C.c_void_p),
+                ("v_scales", C.c_void_p), ("kv_block_bytes", C.c_size_t),
+                ("scale_block_bytes", C.c_size_t)]
+
+
+class BatchDesc(C.Structure):
+    _fields_ = [("n_sessions", C.c_int), ("ctx", C.POINTER(C.c_int)),
+                ("n_new", C.POINTER(C.c_int)), ("table_offsets", C.POINTER(C.c_int)),
+                ("page_ids", C.POINTER(C.c_int)), ("q_heads", C.c_int)]
+
+
+class Qwen2Config(C.Structure):
+    _fields_ = [("layers", C.c_int), ("q_heads", C.c_int), ("kv_heads", C.c_int),
+                ("head_dim", C.c_int), ("context", C.c_int), ("sequences", C.c_int),
+                ("pages", C.c_int), ("format", C.c_int), ("scale_format", C.c_int)]
+
+
+# (name, restype, argtypes) of every symbol include/tge_kv.h declares.
+_VP, _I, _PI = C.c_void_p, C.c_int, C.POINTER(C.c_int)
+SIGNATURES = [
+    ("tge_status_string", C.c_char_p, [_I]),
+    ("tge_last_error", C.c_char_p, []),
+    ("tge_backend_init", _I, []),
+    ("tge_backend_arch", C.c_char_p, []),
+    ("tge_kv_pool_create", _I, [C.POINTER(PoolDesc), C.POINTER(_VP)]),
+    ("tge_kv_pool_destroy", None, [_VP]),
+    ("tge_kv_pool_layer", _I, [_VP, _I, C.POINTER(LayerView)]),
+    ("tge_kv_pool_bytes", C.c_size_t, [_VP]),
+    ("tge_kv_k_index", _I, [_I, _I]),
+    ("tge_kv_v_index", _I, [_I, _I]),
+    ("tge_batch_create", _I, [C.POINTER(_VP)]),
+    ("tge_batch_destroy", None, [_VP]),
+    ("tge_batch_plan", _I, [_VP, _VP, C.POINTER(BatchDesc), _VP]),
+    ("tge_batch_info", _I, [_VP, _PI, _PI, _PI]),
+    ("tge_kv_append", _I, [_VP, _VP, _I, _VP, _VP, _VP]),
+    ("tge_decode_attention", _I, [_VP, _VP, _I, _VP, _VP, _VP]),
+    ("tge_prefill_attention", _I, [_VP, _VP, _I, _VP, _VP, _VP]),
+    ("tge_kv_gather", _I, [_VP, _VP, _I, _I, _I, _VP, _VP, _VP, _VP, _VP]),
+    ("tge_block_table_create", _I, [_I, _I, C.POINTER(_VP)]),
+    ("tge_block_table_destroy", None, [_VP]),
+    ("tge_block_table_allocate", _I, [_VP, _PI]),
+    ("tge_block_table_share", _I, [_VP, _I]),
+    ("tge_block_table_release", _I, [_VP, _I]),
+    ("tge_block_table_refcount", _I, [_VP, _I, _PI]),
+    ("tge_block_table_free_count", _I, [_VP]),
+    ("tge_block_table_capacity", _I, [_VP]),
+    ("tge_block_table_remember_prefix", _I, [_VP, C.c_uint64, _I]),
+    ("tge_block_table_find_prefix", _I, [_VP, C.c_uint64]),
+    ("tge_slot_for", _I, [_I, _I, _PI, _PI]),
+    ("tge_hash_tokens", _I, [_PI, _I, C.POINTER(C.c_uint64)]),
+    ("tge_qwen2_kv_create", _I, [C.POINTER(Qwen2Config), C.POINTER(_VP)]),
+    ("tge_qwen2_kv_destroy", None, [_VP]),
+    ("tge_qwen2_kv_begin_forward", _I, [_VP, _I, _I, _VP]),
+    ("tge_qwen2_kv_begin_forward_batch", _I, [_VP, _PI, _I, _PI, _VP]),
+    ("tge_qwen2_kv_begin_prefill", _I, [_VP, _I, _I, _I, _VP]),
+    ("tge_qwen2_kv_begin_verify", _I, [_VP, _I, _I, _I, _VP]),
+    ("tge_qwen2_kv_layer", _I, [_VP, _I, _VP, _VP, _VP, _VP, _VP]),
+    ("tge_qwen2_kv_reset", _I, [_VP, _I]),
+    ("tge_qwen2_kv_length", _I, [_VP, _I]),
+    ("tge_qwen2_kv_pages", _I, [_VP, _I, _PI, _I]),
+    ("tge_qwen2_kv_pool", _VP, [_VP]),
+    ("tge_qwen2_kv_batch", _VP, [_VP]),
+    ("tge_qwen2_kv_free_pages", _I, [_VP]),
+]
+
+
+def lib():
+    """Loads libtge_kv.so (built in-tree by __graft_entry__.build())."""
+    global _lib
+    if _lib is None:
+        if not os.path.exists(LIB_PATH):
+            raise RuntimeError(f"{LIB_PATH} is missing: build it (make -C aegean-tge_amd)")
+        L = C.CDLL(LIB_PATH)
+        for name, res, args in SIGNATURES:
+            fn = getattr(L, name)
+            fn.restype = res
+            fn.argtypes = args
+        _lib = L
+    return _lib
+
+
+def check(status, what=""):
+    if status != OK:
+        msg = lib().tge_last_error().decode(errors="replace")
+        raise TgeError(status, f"{what}: {msg}" if what else msg)
+    return status
+
+
+def backend_ready():
+    return lib().tge_backend_init() == OK
+
+
+def require_gpu():
+    check(lib().tge_backend_init(), "tge_backend_init")
+
+
+# ---------------------------------------------------------------------------
+# Minimal HIP runtime access (device memory, copies, events, streams).
+# ---------------------------------------------------------------------------
+class Hip:
+    H2D, D2H, D2D = 1, 2, 3
+
+    def __init__(self):
+        lib()  # libtge_kv.so pulls in the system libamdhip64 first
+        h = C.CDLL("libamdhip64.so.7")
+        h.hipMalloc.argtypes = [C.POINTER(C.c_void_p), C.c_size_t]
+        h.hipFree.argtypes = [C.c_void_p]
+        h.hipMemcpy.argtypes = [C.c_void_p, C.c_void_p, C.c_size_t, C.c_int]
+        h.hipMemcpyAsync.argtypes = [C.c_void_p, C.c_void_p, C.c_size_t, C.c_int, C.c_void_p]
+        h.hipMemset.argtypes = [C.c_void_p, C.c_int, C.c_size_t]
+        h.hipDeviceSynchronize.argtypes = []
+        h.hipStreamSynchronize.argtypes = [C.c_void_p]
+        h.hipEventCreate.argtypes = [C.POINTER(C.c_void_p)]
+        h.hipEventRecord.argtypes = [C.c_void_p, C.c_void_p]
+        h.hipEventSynchronize.argtypes = [C.c_void_p]
+        h.hipEventElapsedTime.argtypes = [C.POINTER(C.c_float), C.c_void_p, C.c_void_p]
+        h.hipEventDestroy.argtypes = [C.c_void_p]
+        h.hipStreamCreate.argtypes = [C.POINTER(C.c_void_p)]
+        h.hipStreamDestroy.argtypes = [C.c_void_p]
+        h.hipGetErrorString.restype = C.c_char_p
+        h.hipGetErrorString.argtypes = [C.c_int]
+        h.hipMemGetInfo.argtypes = [C.POINTER(C.c_size_t), C.POINTER(C.c_size_t)]
+        self.h = h
+
+    def ok(self, e, what):
+        if e != 0:
+            raise TgeError(ERR_DEVICE, f"{what}: {self.h.hipGetErrorString(e).decode()}")
+
+    def malloc(self, nbytes):
+        p = C.c_void_p()
+        self.ok(self.h.hipMalloc(C.byref(p), max(int(nbytes), 1)), "hipMalloc")
+        return p.value
+
+    def free(self, p):
+        if p:
+            self.ok(self.h.hipFree(C.c_void_p(p)), "hipFree")
+
+    def upload(self, dst, arr):
+        arr = np.ascontiguousarray(arr)
+        self.ok(self.h.hipMemcpy(C.c_void_p(dst), arr.ctypes.data_as(C.c_void_p), arr.nbytes,
+                                 self.H2D), "hipMemcpy H2D")
+
+    def download(self, src, arr):
+        assert arr.flags["C_CONTIGUOUS"]
+        self.ok(self.h.hipMemcpy(arr.ctypes.data_as(C.c_void_p), C.c_void_p(src), arr.nbytes,
+                                 self.D2H), "hipMemcpy D2H")
+        return arr
+
+    def memset(self, p, value, nbytes):
+        self.ok(self.h.hipMemset(C.c_void_p(p), value, nbytes), "hipMemset")
+
+    def sync(self):
+        self.ok(self.h.hipDeviceSynchronize(), "hipDeviceSynchronize")
+
+    def event(self):
+        e = C.c_void_p()
+        self.ok(self.h.hipEventCreate(C.byref(e)), "hipEventCreate")
+        return e.value
+
+    def record(self, ev, stream=None):
+        self.ok(self.h.hipEventRecord(C.c_void_p(ev), C.c_void_p(stream)), "hipEventRecord")
+
+    def elapsed_ms(self, a, b):
+        self.ok(self.h.hipEventSynchronize(C.c_void_p(b)), "hipEventSynchronize")
+        ms = C.c_float()
+        self.ok(self.h.hipEventElapsedTime(C.byref(ms), C.c_void_p(a), C.c_void_p(b)),
+                "hipEventElapsedTime")
+        return ms.value
+
+    def mem_info(self):
+        free, total = C.c_size_t(), C.c_size_t()
+        self.ok(self.h.hipMemGetInfo(C.byref(free), C.byref(total)), "hipMemGetInfo")
+        return free.value, total.value
+
+
+_hip_inst = None
+
+
+def hip():
+    global _hip_inst
+    if _hip_inst is None:
+        _hip_inst = Hip()
+    return _hip_inst
+
+
+class DeviceArray:
+    """A device allocation with a numpy shape/dtype, freed on close()."""
+
+    def __init__(self, shape, dtype):
+        self.shape = tuple(int(s) for s in (shape if isinstance(shape, (tuple, list)) else (shape,)))
+        self.dtype = np.dtype(dtype)
+        self.nbytes = int(np.prod(self.shape, dtype=np.int64)) * self.dtype.itemsize
+        self.ptr = hip().malloc(self.nbytes)
+
+    @classmethod
+    def from_numpy(cls, arr):
+        arr = np.ascontiguousarray(arr)
+        d = cls(arr.shape, arr.dtype)
+        hip().upload(d.ptr, arr)
+        return d
+
+    def numpy(self):
+        return hip().download(self.ptr, np.empty(self.shape, self.dtype))
+
+    def zero(self):
+        hip().memset(self.ptr, 0, self.nbytes)
+        return self
+
+    def close(self):
+        if self.ptr:
+            hip().free(self.ptr)
+            self.ptr = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+
+def _ints(values):
+    arr = (C.c_int * max(len(values), 1))(*[int(v) for v in values])
+    return arr
+
+
+# ---------------------------------------------------------------------------
+# Object wrappers
+# ---------------------------------------------------------------------------
+class BlockTable:
+    """tge_block_table_*: the reference BlockTable's behaviour (host side)."""
+
+    def __init__(self, blocks, block_tokens=PAGE_TOKENS):
+        h = C.c_void_p()
+        check(lib().tge_block_table_create(blocks, block_tokens, C.byref(h)), "BlockTable")
+        self.h = h
+
+    def allocate(self):
+        out = C.c_int()
+        check(lib().tge_block_table_allocate(self.h, C.byref(out)), "allocate")
+        return out.value
+
+    def share(self, block):
+        check(lib().tge_block_table_share(self.h, block), "share")
+
+    def release(self, block):
+        check(lib().tge_block_table_release(self.h, block), "release")
+
+    def refcount(self, block):
+        out = C.c_int()
+        check(lib().tge_block_table_refcount(self.h, block, C.byref(out)), "refcount")
+        return out.value
+
+    def free_count(self):
+        return lib().tge_block_table_free_count(self.h)
+
+    def capacity(self):
+        return lib().tge_block_table_capacity(self.h)
+
+    def remember_prefix(self, hash_value, block):
+        check(lib().tge_block_table_remember_prefix(self.h, C.c_uint64(hash_value), block),
+              "remember_prefix")
+
+    def find_prefix(self, hash_value):
+        return lib().tge_block_table_find_prefix(self.h, C.c_uint64(hash_value))
+
+    @staticmethod
+    def slot_for(pos, block_tokens=PAGE_TOKENS):
+        b, o = C.c_int(), C.c_int()
+        check(lib().tge_slot_for(pos, block_tokens, C.byref(b), C.byref(o)), "slot_for")
+        return b.value, o.value
+
+    @staticmethod
+    def hash_tokens(tokens):
+        out = C.c_uint64()
+        arr = _ints(tokens) if len(tokens) else None
+        check(lib().tge_hash_tokens(arr, len(tokens), C.byref(out)), "hash_tokens")
+        return out.value
+
+    def close(self):
+        if self.h:
+            lib().tge_block_table_destroy(self.h)
+            self.h = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+
+class KvPool:
+    def __init__(self, layers, pages, kv_heads, head_dim, fmt=KV_F16, scale_format=SCALE_F16):
+        self.desc = PoolDesc(layers, pages, kv_heads, head_dim, fmt, scale_format)
+        h = C.c_void_p()
+        check(lib().tge_kv_pool_create(C.byref(self.desc), C.byref(h)), "kv_pool_create")
+        self.h = h
+        self.layers, self.pages, self.kv_heads, self.head_dim = layers, pages, kv_heads, head_dim
+        self.format, self.scale_format = fmt, scale_format
+
+    def layer(self, layer):
+        v = LayerView()
+        check(lib().tge_kv_pool_layer(self.h, layer, C.byref(v)), "kv_pool_layer")
+        return v
+
+    def bytes(self):
+        return lib().tge_kv_pool_bytes(self.h)
+
+    def close(self):
+        if self.h:
+            lib().tge_kv_pool_destroy(self.h)
+            self.h = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+
+@dataclass
+class Session:
+    ctx: int
+    n_new: int
+    pages: list
+
+
+class Batch:
+    def __init__(self):
+        h = C.c_void_p()
+        check(lib().tge_batch_create(C.byref(h)), "batch_create")
+        self.h = h
+        self.sessions = []
+
+    def plan(self, pool, sessions, q_heads, stream=None):
+        ctx = [s.ctx for s in sessions]
+        n_new = [s.n_new for s in sessions]
+        offs = [0]
+        ids = []
+        for s in sessions:
+            ids.extend(int(p) for p in s.pages)
+            offs.append(len(ids))
+        self._keep = (_ints(ctx), _ints(n_new), _ints(offs), _ints(ids))
+        d = BatchDesc(len(sessions), self._keep[0], self._keep[1], self._keep[2], self._keep[3],
+                      q_heads)
+        check(lib().tge_batch_plan(self.h, pool.h, C.byref(d), stream), "batch_plan")
+        self.sessions = list(sessions)
+        self.rows = sum(n_new)
+        return self
+
+    def info(self):
+        r, w, s = C.c_int(), C.c_int(), C.c_int()
+        check(lib().tge_batch_info(self.h, C.byref(r), C.byref(w), C.byref(s)), "batch_info")
+        return r.value, w.value, s.value
+
+    def append(self, pool, layer, k, v, stream=None):
+        check(lib().tge_kv_append(self.h, pool.h, layer, k.ptr, v.ptr, stream), "kv_append")
+
+    def decode(self, pool, layer, q, out, stream=None):
+        check(lib().tge_decode_attention(self.h, pool.h, layer, q.ptr, out.ptr, stream),
+              "decode_attention")
+
+    def prefill(self, pool, layer, q, out, stream=None):
+        check(lib().tge_prefill_attention(self.h, pool.h, layer, q.ptr, out.ptr, stream),
+              "prefill_attention")
+
+    def gather(self, pool, layer, session, count):
+        """Positions [0, count) of a session as flat rows (codes/bits, scales)."""
+        kv_dim = pool.kv_heads * pool.head_dim
+        et = np.uint16 if pool.format == KV_F16 else np.int8
+        k = DeviceArray((count, kv_dim), et)
+        v = DeviceArray((count, kv_dim), et)
+        ks = vs = None
+        if pool.format == KV_I8:
+            st = np.float32 if pool.scale_format == SCALE_F32 else np.uint16
+            ks = DeviceArray((count, kv_dim // 32), st)
+            vs = DeviceArray((count, kv_dim // 32), st)
+        check(lib().tge_kv_gather(self.h, pool.h, layer, session, count, k.ptr, v.ptr,
+                                  ks.ptr if ks else None, vs.ptr if vs else None, None),
+              "kv_gather")
+        hip().sync()
+        res = (k.numpy(), v.numpy(), ks.numpy() if ks else None, vs.numpy() if vs else None)
+        for a in (k, v, ks, vs):
+            if a is not None:
+                a.close()
+        return res
+
+    def close(self):
+        if self.h:
+            lib().tge_batch_destroy(self.h)
+            self.h = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+
+class Qwen2KvPath:
+    """tge_qwen2_kv_*: the Qwen2-shaped store-then-attend driver."""
+
+    def __init__(self, layers, q_heads, kv_heads, head_dim, context=4096, sequences=1, pages=0,
+                 fmt=KV_F16, scale_format=SCALE_F16):
+        self.cfg = Qwen2Config(layers, q_heads, kv_heads, head_dim, context, sequences, pages,
+                               fmt, scale_format)
+        h = C.c_void_p()
+        check(lib().tge_qwen2_kv_create(C.byref(self.cfg), C.byref(h)), "qwen2_kv_create")
+        self.h = h
+
+    def begin_forward(self, sequence, position):
+        check(lib().tge_qwen2_kv_begin_forward(self.h, sequence, position, None), "forward")
+
+    def begin_forward_batch(self, positions, sequences):
+        check(lib().tge_qwen2_kv_begin_forward_batch(self.h, _ints(positions), len(positions),
+                                                     _ints(sequences), None), "forward_batch")
+
+    def begin_prefill(self, sequence, start, count):
+        check(lib().tge_qwen2_kv_begin_prefill(self.h, sequence, start, count, None), "prefill")
+
+    def begin_verify(self, sequence, start, count):
+        check(lib().tge_qwen2_kv_begin_verify(self.h, sequence, start, count, None), "verify")
+
+    def layer(self, layer, q, k, v, out):
+        check(lib().tge_qwen2_kv_layer(self.h, layer, q.ptr, k.ptr, v.ptr, out.ptr, None), "layer")
+
+    def reset(self, sequence):
+        check(lib().tge_qwen2_kv_reset(self.h, sequence), "reset_cache")
+
+    def length(self, sequence):
+        n = lib().tge_qwen2_kv_length(self.h, sequence)
+        if n < 0:
+            check(n, "length")
+        return n
+
+    def pages(self, sequence):
+        buf = (C.c_int * 65536)()
+        n = lib().tge_qwen2_kv_pages(self.h, sequence, buf, 65536)
+        if n < 0:
+            check(n, "pages")
+        return list(buf[:n])
+
+    def free_pages(self):
+        return lib().tge_qwen2_kv_free_pages(self.h)
+
+    def close(self):
+        if self.h:
+            lib().tge_qwen2_kv_destroy(self.h)
+            self.h = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass

@@ -1,0 +1,100 @@
+// tge::models::Qwen2KvPath — the Qwen2 decoder's KV-cache path over paged
+// gfx950 memory.
+//
+// Mirrors the cache-facing half of the reference's Qwen2 class
+// (include/tge/models/qwen2.hpp:107-305 in AegeanWorks/Aegean-TGE):
+// forward / forward_batch / prefill / verify_draft / reset_cache keep their
+// validation rules and their store-then-attend order per layer
+// (qwen2.cpp:2032-2095, 1613-1747, 2130-2335, 2502-2577), with the flat
+// [sequence][layer][position][kv_dim] cache replaced by BlockTable pages.
+// Weights are not on this path: the caller supplies each layer's post-RoPE
+// q, k, v rows (device memory) and receives the attention rows.
+//
+// A step is begun once (pages allocated from the BlockTable, plan uploaded)
+// and then run layer by layer, so every layer reuses one host->device copy.
+// Misuse throws std::runtime_error (model contract) or std::invalid_argument
+// (shape contract); device failures throw std::runtime_error with the HIP
+// message.
+#pragma once
+
+#include <memory>
+#include <vector>
+
+#include "tge_amd/block_table.hpp"
+#include "tge_kv.h"
+
+namespace tge::models {
+
+struct Qwen2KvConfig {
+  int layers = 0;
+  int q_heads = 0;
+  int kv_heads = 0;
+  int head_dim = 0;
+  int context = 4096;  // kDefaultContext, qwen2.cpp:25
+  int sequences = 1;
+  int pages = 0;       // 0: sequences * ceil(context / 16)
+  int format = TGE_KV_F16;
+  int scale_format = TGE_SCALE_F16;
+};
+
+class Qwen2KvPath {
+ public:
+  static constexpr int kSpeculativeBatch = 6;  // qwen2.hpp:140
+  static constexpr int kHardMaxContext = 32768;  // qwen2.cpp:26
+
+  explicit Qwen2KvPath(const Qwen2KvConfig& config);
+  ~Qwen2KvPath();
+  Qwen2KvPath(const Qwen2KvPath&) = delete;
+  Qwen2KvPath& operator=(const Qwen2KvPath&) = delete;
+
+  const Qwen2KvConfig& config() const { return config_; }
+  int sequence_count() const { return config_.sequences; }
+  int max_context() const { return config_.context; }
+
+  // Step set-up. `stream` is a hipStream_t (nullptr = default stream).
+  void begin_forward(int sequence, int position, void* stream = nullptr);
+  void begin_forward_batch(const int* positions, int count, const int* sequences,
+                           void* stream = nullptr);
+  void begin_prefill(int sequence, int start_position, int count, void* stream = nullptr);
+  void begin_verify_draft(int sequence, int start_position, int count,
+                          void* stream = nullptr);
+
+  // Store this step's K/V rows for `layer`, then attend (decode kernel for
+  // short steps, MFMA block-prefill kernel for long f16 chunks).
+  void layer(int layer, const float* q, const float* k, const float* v, float* out,
+             void* stream = nullptr);
+
+  // reset_cache(sequence): the sequence's pages go back to the table in
+  // logical order; reset_cache() does every sequence.
+  void reset_cache(int sequence);
+  void reset_cache();
+
+  int length(int sequence) const;
+  const std::vector<int>& pages(int sequence) const;
+  const BlockTable& table() const { return *table_; }
+  const tge_kv_pool* pool() const { return pool_; }
+  const tge_batch* batch() const { return batch_; }
+  int step_rows() const { return step_rows_; }
+  bool step_is_prefill() const { return prefill_; }
+
+ private:
+  struct Group {
+    int sequence;
+    int start;
+    int count;
+  };
+  void check_sequence(int sequence, const char* who) const;
+  void begin(const std::vector<Group>& groups, void* stream);
+
+  Qwen2KvConfig config_;
+  std::unique_ptr<BlockTable> table_;
+  std::vector<std::vector<int>> pages_;
+  std::vector<int> length_;
+  tge_kv_pool* pool_ = nullptr;
+  tge_batch* batch_ = nullptr;
+  int step_rows_ = 0;
+  bool prefill_ = false;
+  bool begun_ = false;
+};
+
+}  // namespace tge::models

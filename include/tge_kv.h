@@ -1,0 +1,277 @@
+/*
+ * tge_kv.h — C ABI of the MI355X (gfx950) paged-KV hot path.
+ *
+ * Replaces, behind a thin C boundary, what the reference engine does on the
+ * CPU for its KV cache (AegeanWorks/Aegean-TGE, paths relative to its root):
+ *   - the per-token K/V store          src/models/qwen2.cpp:2073-2093,
+ *                                       1681-1702, 2308-2329, 88-120
+ *   - GQA decode attention + split-K    include/tge/cpu/kernels.hpp:207-288
+ *     (KernelSet::attention_head /      include/tge/core/dispatch.hpp:31-33
+ *      attention_group + merge)         src/models/qwen2.cpp:1243-1522
+ *   - the query-block prefill kernel    include/tge/cpu/kernels.hpp:290-317
+ *                                       src/models/qwen2.cpp:1524-1571
+ *   - the block table                   include/tge/models/block_table.hpp
+ * Conventions (the reference's, restated for a C boundary):
+ *   - every entry point returns an int status (TGE_OK = 0); no exception or
+ *     C++ type crosses it. TGE_ERR_INVALID is the reference's
+ *     std::invalid_argument (kernel argument checks, attention_scalar.cpp:
+ *     11-44); TGE_ERR_RUNTIME its std::runtime_error (model/BlockTable misuse,
+ *     qwen2.cpp:2036-2044, block_table.hpp:25-123).
+ *   - outputs are left untouched when a call fails (backend.hpp:87-89).
+ *   - all pointers are borrowed. Pointers documented "device" address HIP
+ *     device memory; "host" pointers are read during the call only.
+ *   - `stream` is a hipStream_t (NULL = the default stream). Work is
+ *     enqueued asynchronously; the caller synchronises.
+ *
+ * Storage: K/V live in device pages of TGE_PAGE_TOKENS tokens, one pool per
+ * layer, addressed by physical page id. The in-page order is chosen for the
+ * CDNA4 matrix cores and documented below (tge_kv_k_index / tge_kv_v_index);
+ * tge_kv_gather turns pages back into the reference's flat row-major rows.
+ */
+#ifndef TGE_KV_H
+#define TGE_KV_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define TGE_PAGE_TOKENS 16 /* block_table.hpp:19 kBlockTokens */
+
+enum tge_status {
+  TGE_OK = 0,
+  TGE_ERR_INVALID = -1,     /* bad argument (std::invalid_argument) */
+  TGE_ERR_RUNTIME = -2,     /* misuse of model/table state (std::runtime_error) */
+  TGE_ERR_UNAVAILABLE = -3, /* no usable gfx950 device, or forced off */
+  TGE_ERR_DEVICE = -4,      /* a HIP runtime call failed */
+  TGE_ERR_CAPACITY = -5     /* page pool or table full */
+};
+
+enum tge_kv_format {
+  TGE_KV_F16 = 1, /* IEEE half bits, the reference's float_to_half recipe */
+  TGE_KV_I8 = 2   /* int8 codes, one scale per 32 values (store_kv_q8) */
+};
+
+enum tge_scale_format {
+  TGE_SCALE_F16 = 0, /* scale stored as float_to_half(fp32 scale) */
+  TGE_SCALE_F32 = 1  /* scale stored as the fp32 value (reference layout) */
+};
+
+/* Text for a status code; the last error message of the calling thread. */
+const char* tge_status_string(int status);
+const char* tge_last_error(void);
+
+/*
+ * Backend bring-up, never throws, idempotent (reference gpu::init(),
+ * backend.hpp:52-54). Returns TGE_OK when a gfx950 device is usable.
+ * Setting the environment variable TGE_FORCE_UNAVAILABLE=1 makes it report
+ * TGE_ERR_UNAVAILABLE (for fallback tests).
+ */
+int tge_backend_init(void);
+/* Name of the device's architecture (e.g. "gfx950"), or "" when none. */
+const char* tge_backend_arch(void);
+
+/* ---------------------------------------------------------------------------
+ * Page pool. Device memory for `layers` x `pages` x `kv_heads` page blocks.
+ * Each page block holds TGE_PAGE_TOKENS tokens of one KV head:
+ *   K and V: 16 * head_dim elements (f16 bits or int8 codes)
+ *   I8 only, K and V scales: 16 * head_dim/32 scales (f16 bits or fp32)
+ * Element (token t, dim d) of a block sits at:
+ *   K: tge_kv_k_index(t, d)      V: tge_kv_v_index(t, d)
+ *   scale of (t, block b = d/32): b*16 + t
+ * head_dim must be 64 or 128 (the configurations' head sizes).
+ * ------------------------------------------------------------------------ */
+typedef struct tge_kv_pool tge_kv_pool;
+
+typedef struct {
+  int layers;
+  int pages;        /* physical pages per layer (BlockTable capacity) */
+  int kv_heads;
+  int head_dim;
+  int format;       /* enum tge_kv_format */
+  int scale_format; /* enum tge_scale_format, I8 only */
+} tge_kv_pool_desc;
+
+typedef struct {
+  void* k;        /* device, pages*kv_heads blocks for this layer */
+  void* v;
+  void* k_scales; /* NULL for F16 */
+  void* v_scales;
+  size_t kv_block_bytes;    /* bytes of one K (or V) page block */
+  size_t scale_block_bytes; /* bytes of one scale page block (0 for F16) */
+} tge_kv_layer_view;
+
+int tge_kv_pool_create(const tge_kv_pool_desc* desc, tge_kv_pool** out);
+void tge_kv_pool_destroy(tge_kv_pool* pool);
+int tge_kv_pool_layer(const tge_kv_pool* pool, int layer,
+                      tge_kv_layer_view* out);
+/* Device bytes the pool holds. */
+size_t tge_kv_pool_bytes(const tge_kv_pool* pool);
+
+/* In-page element index of (token, dim) for K and V blocks. */
+int tge_kv_k_index(int token, int dim);
+int tge_kv_v_index(int token, int dim);
+
+/* ---------------------------------------------------------------------------
+ * Batch: the sessions one step works on. A plan is built once per step on the
+ * host and uploaded once; every layer's append and attention then reuse it.
+ *
+ * Session s owns n_new[s] new tokens at positions ctx[s] .. ctx[s]+n_new[s]-1
+ * (appended first, then attended causally: new token i sees positions
+ * 0 .. ctx[s]+i, the store-then-attend order of qwen2.cpp:2073-2095).
+ * Its block table lists physical page ids in logical order:
+ * page_ids[table_offsets[s] .. table_offsets[s+1]) and must cover
+ * ceil((ctx+n_new)/16) pages. Rows of q/k/v/out are the sessions' new tokens
+ * in session order (session s starts at row sum(n_new[0..s-1])), the
+ * per-token row order of forward_batch (qwen2.cpp:1613-1747).
+ *   q, out: [rows][q_heads*head_dim] fp32     k, v: [rows][kv_heads*head_dim] fp32
+ * ------------------------------------------------------------------------ */
+typedef struct tge_batch tge_batch;
+
+typedef struct {
+  int n_sessions;
+  const int* ctx;           /* host [n_sessions] */
+  const int* n_new;         /* host [n_sessions], >= 1 */
+  const int* table_offsets; /* host [n_sessions+1] */
+  const int* page_ids;      /* host [table_offsets[n_sessions]] */
+  int q_heads;              /* multiple of the pool's kv_heads */
+} tge_batch_desc;
+
+int tge_batch_create(tge_batch** out);
+void tge_batch_destroy(tge_batch* batch);
+
+/* Validates the description against `pool`, builds the work lists and
+ * uploads tables and plan (one host-to-device copy on `stream`). */
+int tge_batch_plan(tge_batch* batch, const tge_kv_pool* pool,
+                   const tge_batch_desc* desc, void* stream);
+
+/* Plan statistics: total new-token rows, decode work items, splits. */
+int tge_batch_info(const tge_batch* batch, int* rows, int* work_items,
+                   int* max_splits);
+
+/*
+ * Fused quantize-and-scatter of every new token's K and V rows into its page
+ * slot (the store sites above). F16: bits of the reference float_to_half
+ * (kernels.hpp:358-386). I8: per 32 values, codes and scale exactly as
+ * quantize_kv_block (qwen2.cpp:88-104); the scale is stored as fp32 or as
+ * float_to_half(scale) per the pool's scale_format.
+ */
+int tge_kv_append(const tge_batch* batch, tge_kv_pool* pool, int layer,
+                  const float* k, const float* v, void* stream);
+
+/*
+ * Decode attention for every session of the batch (n_new small: decode and
+ * speculative verify). One workgroup per (session, kv head, position split)
+ * shares each K/V page across the whole query-head group; splits of long
+ * contexts are merged by a reduction pass (merge_gqa_chunks,
+ * qwen2.cpp:1469-1522). softmax scale = 1/sqrt(head_dim) (qwen2.cpp:1278).
+ * Requires n_new*group <= 64 for every session.
+ */
+int tge_decode_attention(const tge_batch* batch, const tge_kv_pool* pool,
+                         int layer, const float* q, float* out, void* stream);
+
+/*
+ * Chunked-prefill block attention (attention_block_head_avx2,
+ * attention_avx2.cpp:660-864): each new token attends causally to every
+ * prior page and the chunk itself, on f16 MFMA (Q rounded to f16 for F16
+ * pools; I8 pools keep Q as f16 hi + lo, the reference's per-token i8 path
+ * qwen2.cpp:1535-1538 computes the same values). Tiles of 32 queries of one
+ * head; long prefixes are split and merged like decode.
+ */
+int tge_prefill_attention(const tge_batch* batch, const tge_kv_pool* pool,
+                          int layer, const float* q, float* out, void* stream);
+
+/*
+ * Device gather of one session's positions [0, count) back to the flat
+ * row-major layout of the reference cache (gather_blocks_row_major,
+ * kv_block_layout.hpp:64-84, applied per element): k_rows/v_rows receive
+ * [count][kv_heads*head_dim] elements (f16 bits or int8 codes), scales
+ * [count][kv_heads*head_dim/32] (I8 only; may be NULL otherwise).
+ */
+int tge_kv_gather(const tge_batch* batch, const tge_kv_pool* pool, int layer,
+                  int session, int count, void* k_rows, void* v_rows,
+                  void* k_scales, void* v_scales, void* stream);
+
+/* ---------------------------------------------------------------------------
+ * Block table (block_table.hpp:21-130), host-side page-id allocator.
+ * allocate: LIFO free list (a fresh table hands out 0,1,2,...); release at
+ * refcount 0 returns the page to the free list; misuse -> TGE_ERR_RUNTIME.
+ * ------------------------------------------------------------------------ */
+typedef struct tge_block_table tge_block_table;
+
+int tge_block_table_create(int blocks, int block_tokens, tge_block_table** out);
+void tge_block_table_destroy(tge_block_table* table);
+int tge_block_table_allocate(tge_block_table* table, int* block);
+int tge_block_table_share(tge_block_table* table, int block);
+int tge_block_table_release(tge_block_table* table, int block);
+int tge_block_table_refcount(const tge_block_table* table, int block, int* out);
+int tge_block_table_free_count(const tge_block_table* table);
+int tge_block_table_capacity(const tge_block_table* table);
+int tge_block_table_remember_prefix(tge_block_table* table, uint64_t hash,
+                                    int block);
+/* -1 on a miss (find_prefix). */
+int tge_block_table_find_prefix(const tge_block_table* table, uint64_t hash);
+/* slot_for (block_table.hpp:77-82); hash_tokens FNV-1a (:85-98). */
+int tge_slot_for(int logical_pos, int block_tokens, int* block, int* offset);
+int tge_hash_tokens(const int* tokens, int count, uint64_t* out);
+
+/* ---------------------------------------------------------------------------
+ * Qwen2-shaped KV driver: the store-then-attend sequence of Qwen2::forward /
+ * forward_batch / prefill_run / verify_draft / reset_cache (qwen2.hpp:249-
+ * 297) over paged device KV. Weights are outside this path: callers pass the
+ * post-RoPE q/k/v of each layer (device pointers, rows as in the batch).
+ * A step is begun once (pages allocated, plan uploaded) and then run layer
+ * by layer.
+ * ------------------------------------------------------------------------ */
+typedef struct tge_qwen2_kv tge_qwen2_kv;
+
+typedef struct {
+  int layers;
+  int q_heads;
+  int kv_heads;
+  int head_dim;
+  int context;      /* max positions per sequence (qwen2.cpp:25-26) */
+  int sequences;    /* KV slots */
+  int pages;        /* physical pages in the shared pool */
+  int format;       /* enum tge_kv_format */
+  int scale_format; /* enum tge_scale_format */
+} tge_qwen2_kv_config;
+
+int tge_qwen2_kv_create(const tge_qwen2_kv_config* config, tge_qwen2_kv** out);
+void tge_qwen2_kv_destroy(tge_qwen2_kv* model);
+
+/* forward(sequence, token, position): one token of one sequence. */
+int tge_qwen2_kv_begin_forward(tge_qwen2_kv* model, int sequence, int position,
+                               void* stream);
+/* forward_batch: row i is (sequences[i], positions[i]); each sequence's rows
+ * must be consecutive positions in ascending row order. */
+int tge_qwen2_kv_begin_forward_batch(tge_qwen2_kv* model, const int* positions,
+                                     int count, const int* sequences,
+                                     void* stream);
+/* prefill_run: `count` tokens of one sequence from start_position. */
+int tge_qwen2_kv_begin_prefill(tge_qwen2_kv* model, int sequence,
+                               int start_position, int count, void* stream);
+/* verify_draft: count <= 6 (kSpeculativeBatch, qwen2.hpp:140) draft tokens. */
+int tge_qwen2_kv_begin_verify(tge_qwen2_kv* model, int sequence,
+                              int start_position, int count, void* stream);
+/* Append the step's K/V rows for `layer`, then attend. */
+int tge_qwen2_kv_layer(tge_qwen2_kv* model, int layer, const float* q,
+                       const float* k, const float* v, float* out,
+                       void* stream);
+/* reset_cache(sequence): release the sequence's pages in logical order. */
+int tge_qwen2_kv_reset(tge_qwen2_kv* model, int sequence);
+/* Positions currently cached for a sequence; its page ids (logical order). */
+int tge_qwen2_kv_length(const tge_qwen2_kv* model, int sequence);
+int tge_qwen2_kv_pages(const tge_qwen2_kv* model, int sequence, int* ids,
+                       int cap);
+const tge_kv_pool* tge_qwen2_kv_pool(const tge_qwen2_kv* model);
+const tge_batch* tge_qwen2_kv_batch(const tge_qwen2_kv* model);
+int tge_qwen2_kv_free_pages(const tge_qwen2_kv* model);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* TGE_KV_H */

@@ -1,0 +1,210 @@
+"""CPU tests of the product library: it loads, exports every symbol the C
+header declares, and its host-side logic (BlockTable, slot_for, hash, page
+layout, argument checks, the unavailable-backend path) behaves like the
+reference. No GPU compute is called here."""
+import ctypes as C
+import os
+import re
+import shutil
+import subprocess
+import tempfile
+
+import numpy as np
+import pytest
+
+import oracle as O
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+HEADER = os.path.join(ROOT, "include", "tge_kv.h")
+
+
+def declared_functions():
+    text = open(HEADER).read()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    return sorted(set(re.findall(r"\b(tge_\w+)\s*\(", text)))
+
+
+def test_library_exports_every_declared_symbol(tk):
+    names = declared_functions()
+    assert len(names) > 30
+    bound = {n for n, _, _ in tk.SIGNATURES}
+    for n in names:
+        assert hasattr(tk.lib(), n), f"libtge_kv.so does not export {n}"
+        assert n in bound, f"tge_kv.py does not bind {n}"
+
+
+def test_status_strings(tk):
+    for s in (tk.OK, tk.ERR_INVALID, tk.ERR_RUNTIME, tk.ERR_UNAVAILABLE, tk.ERR_DEVICE,
+              tk.ERR_CAPACITY):
+        assert tk.lib().tge_status_string(s)
+
+
+def test_backend_forced_unavailable(tmp_path):
+    # A child process with TGE_FORCE_UNAVAILABLE=1 must see the backend as
+    # unavailable and pool creation refused, outputs untouched.
+    code = (
+        "import sys; sys.path.insert(0, %r); import tge_kv as t;"
+        "assert t.lib().tge_backend_init() == t.ERR_UNAVAILABLE;"
+        "import ctypes as C; h = C.c_void_p();"
+        "d = t.PoolDesc(1, 4, 1, 64, t.KV_F16, 0);"
+        "assert t.lib().tge_kv_pool_create(C.byref(d), C.byref(h)) == t.ERR_UNAVAILABLE;"
+        "assert h.value is None; print('ok')" % os.path.join(ROOT, "aegean-tge_amd"))
+    env = dict(os.environ, TGE_FORCE_UNAVAILABLE="1")
+    r = subprocess.run(["python3", "-c", code], env=env, capture_output=True, text=True,
+                       timeout=120)
+    assert r.returncode == 0 and "ok" in r.stdout, r.stderr
+
+
+def test_pool_argument_checks(tk):
+    h = C.c_void_p()
+    for desc in [(0, 4, 1, 64, 1, 0), (1, 4, 1, 96, 1, 0), (1, 4, 1, 64, 7, 0),
+                 (1, 4, 1, 64, 2, 9), (1, -1, 1, 64, 1, 0)]:
+        d = tk.PoolDesc(*desc)
+        assert tk.lib().tge_kv_pool_create(C.byref(d), C.byref(h)) == tk.ERR_INVALID
+        assert h.value is None
+
+
+def test_page_layout_is_a_bijection(tk):
+    for hd in (64, 128):
+        ks = {tk.lib().tge_kv_k_index(t, d) for t in range(16) for d in range(hd)}
+        vs = {tk.lib().tge_kv_v_index(t, d) for t in range(16) for d in range(hd)}
+        assert ks == set(range(16 * hd)) and vs == set(range(16 * hd))
+    # operand contiguity: lane (g, t) of pair p reads 8 consecutive elements
+    for p in range(4):
+        for g in range(4):
+            for t in range(16):
+                dims = [32 * p + 4 * g + e for e in range(4)] + [32 * p + 16 + 4 * g + e for e in range(4)]
+                idx = [tk.lib().tge_kv_k_index(t, d) for d in dims]
+                assert idx == list(range(idx[0], idx[0] + 8)) and idx[0] == ((p * 4 + g) * 16 + t) * 8
+
+
+# ---------------------------------------------------------------------------
+# BlockTable: reference KATs (test_block_table.cpp) and differential runs
+# ---------------------------------------------------------------------------
+def test_block_table_kats(tk):
+    t = tk.BlockTable(4, 16)
+    assert t.free_count() == 4
+    a, b = t.allocate(), t.allocate()
+    assert (a, b) == (0, 1) and t.free_count() == 2
+    t.release(a)
+    assert t.free_count() == 3
+    c = t.allocate()
+    assert c == a and t.refcount(c) == 1
+    full = tk.BlockTable(1, 16)
+    full.allocate()
+    with pytest.raises(tk.TgeError) as e:
+        full.allocate()
+    assert e.value.status == tk.ERR_RUNTIME
+    assert tk.BlockTable.slot_for(0) == (0, 0)
+    assert tk.BlockTable.slot_for(17) == (1, 1)
+    assert tk.BlockTable.slot_for(64) == (4, 0)
+    with pytest.raises(tk.TgeError):
+        tk.BlockTable.slot_for(-1)
+    s = tk.BlockTable(2, 16)
+    x = s.allocate()
+    s.share(x)
+    assert s.refcount(x) == 2
+    s.release(x)
+    assert s.refcount(x) == 1 and s.free_count() == 1
+    s.release(x)
+    assert s.free_count() == 2
+    bad = tk.BlockTable(2, 16)
+    with pytest.raises(tk.TgeError):
+        bad.share(7)
+    with pytest.raises(tk.TgeError):
+        bad.release(0)
+
+
+def test_hash_tokens(tk):
+    a, b = [1, 2, 3, 4], [1, 2, 3, 5]
+    assert tk.BlockTable.hash_tokens(a) == tk.BlockTable.hash_tokens(a)
+    assert tk.BlockTable.hash_tokens(a) != tk.BlockTable.hash_tokens(b)
+    # FNV-1a 64 closed forms: empty input is the offset basis; one zero byte
+    # is basis * prime.
+    assert tk.BlockTable.hash_tokens([]) == 1469598103934665603
+    assert tk.BlockTable.hash_tokens([0]) == O.OracleBlockTable.hash_tokens([0])
+    assert tk.BlockTable.hash_tokens([-7, 2 ** 31 - 1]) == O.OracleBlockTable.hash_tokens([-7, 2 ** 31 - 1])
+    t = tk.BlockTable(4, 16)
+    h = tk.BlockTable.hash_tokens(a)
+    assert t.find_prefix(h) == -1
+    blk = t.allocate()
+    t.remember_prefix(h, blk)
+    assert t.find_prefix(h) == blk
+    t.release(blk)
+    assert t.find_prefix(h) == -1
+
+
+def _ref_table_ops(ref, handle, op, arg):
+    if op == "allocate":
+        return ref.ref_bt_allocate(handle)
+    if op == "release":
+        return ref.ref_bt_release(handle, arg)
+    if op == "share":
+        return ref.ref_bt_share(handle, arg)
+    return ref.ref_bt_refcount(handle, arg)
+
+
+@pytest.mark.parametrize("seed", range(6))
+def test_block_table_random_ops_match_oracle_and_reference(tk, seed):
+    rng = np.random.default_rng(seed)
+    n = int(rng.integers(1, 40))
+    prod = tk.BlockTable(n)
+    orc = O.OracleBlockTable(n)
+    ref = O.ref() if O.ref_available() else None
+    rh = ref.ref_bt_create(n, 16) if ref else None
+    try:
+        for _ in range(600):
+            op = ["allocate", "release", "share", "refcount"][int(rng.integers(0, 4))]
+            arg = int(rng.integers(-2, n + 2))
+            try:
+                want = orc.allocate() if op == "allocate" else getattr(orc, op)(arg)
+                want = 0 if want is None else want
+                ok = True
+            except O.OracleBlockTable.Error:
+                ok = False
+            try:
+                got = prod.allocate() if op == "allocate" else getattr(prod, op)(arg)
+                got = 0 if got is None else got
+                assert ok, (op, arg, "product accepted what the oracle rejects")
+                assert got == want, (op, arg)
+            except tk.TgeError as e:
+                assert not ok and e.status == tk.ERR_RUNTIME, (op, arg)
+            if ref:
+                r = _ref_table_ops(ref, rh, op, arg)
+                assert (r >= 0) == ok and (not ok or r == want), (op, arg, r, want)
+            assert prod.free_count() == orc.free_count()
+    finally:
+        if ref:
+            ref.ref_bt_destroy(rh)
+
+
+# ---------------------------------------------------------------------------
+# The C++20 surface compiles and behaves from C++ (host-only parts)
+# ---------------------------------------------------------------------------
+def test_cpp_header_surface(tmp_path):
+    gxx = shutil.which("g++")
+    if gxx is None:
+        pytest.skip("g++ not available")
+    src = tmp_path / "t.cpp"
+    src.write_text(r'''
+#include "tge_amd/block_table.hpp"
+#include "tge_amd/qwen2_kv.hpp"
+#include <cstdio>
+int main() {
+  using tge::models::BlockTable;
+  BlockTable t(4, 16);
+  int a = t.allocate(), b = t.allocate();
+  t.release(a);
+  int c = t.allocate();
+  bool threw = false;
+  try { BlockTable::slot_for(-1, 16); } catch (const std::runtime_error&) { threw = true; }
+  auto s = BlockTable::slot_for(17, 16);
+  std::printf("%d %d %d %d %d %d\n", a, b, c, threw, s.first, s.second);
+  return 0;
+}
+''')
+    exe = tmp_path / "t"
+    subprocess.run([gxx, "-std=c++20", "-O1", "-I", os.path.join(ROOT, "include"), str(src), "-o",
+                    str(exe)], check=True)
+    out = subprocess.run([str(exe)], check=True, capture_output=True, text=True).stdout.split()
+    assert out == ["0", "1", "0", "1", "1", "1"]

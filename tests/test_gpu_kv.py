@@ -1,0 +1,270 @@
+"""GPU parity of the KV append (bit-exact) and attention (tolerance) against
+the CPU oracle, through the C ABI. Runs on a gfx950 device."""
+import math
+import sys
+
+import numpy as np
+import pytest
+
+import oracle as O
+import synth
+import tge_kv as tk
+from _paged import PagedCase
+from _util import assert_attention_close, bits
+
+pytestmark = pytest.mark.gpu
+
+
+def say(*a):
+    print(*a, flush=True)
+    sys.stdout.flush()
+
+
+def raw_pool_rows(case, layer, s, count):
+    """Decode positions [0, count) of session s straight from the pool bytes
+    with the documented layout formulas (independent of tge_kv_gather)."""
+    view = case.pool.layer(layer)
+    pages = case.pool.pages
+    elem = np.uint16 if case.fmt == tk.KV_F16 else np.int8
+    blk = 16 * case.hd
+    kraw = tk.hip().download(view.k, np.empty(pages * case.kvh * blk, elem))
+    vraw = tk.hip().download(view.v, np.empty(pages * case.kvh * blk, elem))
+    t = np.arange(16)[:, None]
+    d = np.arange(case.hd)[None, :]
+    kidx = ((((d >> 5) << 2) + ((d >> 2) & 3)) * 16 + t) * 8 + (((d >> 4) & 1) << 2) + (d & 3)
+    vidx = ((((d >> 5) << 2) + (t >> 2)) * 16 + (d & 15)) * 8 + (((d >> 4) & 1) << 2) + (t & 3)
+    k = np.empty((count, case.kv_dim), elem)
+    v = np.empty((count, case.kv_dim), elem)
+    for pos0 in range(0, count, 16):
+        page = case.pages[s][pos0 // 16]
+        n = min(16, count - pos0)
+        for h in range(case.kvh):
+            base = (page * case.kvh + h) * blk
+            k[pos0:pos0 + n, h * case.hd:(h + 1) * case.hd] = kraw[base + kidx][:n]
+            v[pos0:pos0 + n, h * case.hd:(h + 1) * case.hd] = vraw[base + vidx][:n]
+    return k, v
+
+
+def check_contents(case, layer=0):
+    b = tk.Batch().plan(case.pool, case.sessions(True), case.qh)
+    for s in range(len(case.contexts)):
+        total = case.contexts[s] + case.n_new[s]
+        fc = O.FlatCache({tk.KV_F16: O.F16, tk.KV_I8: O.I8}[case.fmt], case.k[s], case.v[s])
+        gk, gv, gks, gvs = b.gather(case.pool, layer, s, total)
+        assert np.array_equal(gk, fc.k.view(gk.dtype)), f"K bits differ, session {s}"
+        assert np.array_equal(gv, fc.v.view(gv.dtype)), f"V bits differ, session {s}"
+        if case.fmt == tk.KV_I8:
+            if case.sf == tk.SCALE_F32:
+                assert np.array_equal(bits(gks), bits(fc.ks)) and np.array_equal(bits(gvs), bits(fc.vs))
+            else:
+                assert np.array_equal(gks, O.float_to_half(fc.ks))
+                assert np.array_equal(gvs, O.float_to_half(fc.vs))
+        rk, rv = raw_pool_rows(case, layer, s, total)
+        assert np.array_equal(rk, gk) and np.array_equal(rv, gv)
+    b.close()
+
+
+# ---------------------------------------------------------------------------
+# append
+# ---------------------------------------------------------------------------
+@pytest.mark.parametrize("fmt,sf,kvh,hd", [(tk.KV_F16, 0, 2, 64), (tk.KV_F16, 0, 4, 128),
+                                           (tk.KV_I8, 0, 2, 64), (tk.KV_I8, 1, 4, 128),
+                                           (tk.KV_I8, 0, 4, 128)])
+def test_append_bitexact(gpu, fmt, sf, kvh, hd):
+    say(f"append fmt={fmt} sf={sf} kvh={kvh} hd={hd}")
+    case = PagedCase(kvh * 7, kvh, hd, fmt, [37, 0, 100], [3, 5, 1], scale_format=sf, seed=11,
+                     outlier_frac=0.01 if fmt == tk.KV_I8 else 0)
+    case.fill()
+    case.step()
+    check_contents(case)
+    case.close()
+
+
+def edge_values(n, rng):
+    f = lambda u: np.array(u, np.uint32).view(np.float32)
+    special = np.concatenate([
+        f([0x00000000, 0x80000000, 0x7F800000, 0xFF800000, 0x7FC00000, 0xFFC00001, 0x7F800001,
+           0x33000000, 0x33000001, 0x337FFFFF, 0x33800000, 0x33C00000, 0x387FE000, 0x38800000,
+           0x477FEFFF, 0x477FF000, 0x477FE000, 0x3F801000, 0x3F803000, 0x3F800FFF, 0x00000001]),
+        np.array([65504, 65519, 65520, 1e-8, -1e-8, 6e-5, 6.1e-5, 3.0e38, -3e38], np.float32)])
+    x = rng.standard_normal(n).astype(np.float32)
+    x[:special.size] = special
+    return x
+
+
+def test_append_f16_edge_and_structured_values(gpu):
+    """Rounding-critical inputs through the real append kernel: every sign,
+    exponent and top-10 mantissa bit pattern combined with dropped-bit
+    patterns {0, 0x0FFF, 0x1000, 0x1001, 0x1FFF}, plus NaN/inf/subnormal
+    specials; must equal the oracle's bits (which are pinned exhaustively
+    against the reference build)."""
+    hi = (np.arange(1 << 19, dtype=np.uint32) << 13)
+    low = np.array([0, 0x0FFF, 0x1000, 0x1001, 0x1FFF], np.uint32)
+    xs = (hi[:, None] | low[None, :]).reshape(-1).view(np.float32)
+    rng = np.random.default_rng(3)
+    xs = np.concatenate([edge_values(4096, rng), xs,
+                         rng.integers(0, 2 ** 32, 1 << 20, dtype=np.uint64).astype(np.uint32).view(np.float32)])
+    kv_dim = 128
+    rows = math.ceil(xs.size / kv_dim)
+    xs = np.resize(xs, rows * kv_dim).reshape(rows, kv_dim)
+    pages = math.ceil(rows / 16)
+    pool = tk.KvPool(1, pages, 1, 128, tk.KV_F16)
+    sess = [tk.Session(0, rows, list(range(pages)))]
+    b = tk.Batch().plan(pool, sess, 1)
+    dk = tk.DeviceArray.from_numpy(xs)
+    dv = tk.DeviceArray.from_numpy(-xs)
+    b.append(pool, 0, dk, dv)
+    tk.hip().sync()
+    gk, gv, _, _ = b.gather(pool, 0, 0, rows)
+    assert np.array_equal(gk, O.float_to_half(xs))
+    assert np.array_equal(gv, O.float_to_half(-xs))
+    pool.close()
+
+
+def test_append_i8_edge_blocks(gpu):
+    rng = np.random.default_rng(5)
+    rows, kv_dim = 64, 64
+    x = rng.standard_normal((rows, kv_dim)).astype(np.float32)
+    x[0] = 0.0
+    x[1] = 0.0
+    x[1, 31] = -0.0
+    x[1, 63] = -0.0
+    below = np.nextafter(np.float32(0.5), np.float32(0))
+    x[2, :] = 0
+    x[2, 0], x[2, 1], x[2, 2], x[2, 3], x[2, 4] = 127, below, -below, 2.5, -2.5
+    x[3] *= np.float32(1e-38)
+    x[4] *= np.float32(1e35)
+    x[5, 5] = np.inf
+    x[6, 40] = np.nan
+    x[7] = np.arange(64, dtype=np.float32) - 32
+    for sf in (tk.SCALE_F32, tk.SCALE_F16):
+        pool = tk.KvPool(1, 4, 1, 64, tk.KV_I8, sf)
+        b = tk.Batch().plan(pool, [tk.Session(0, rows, [3, 0, 2, 1])], 1)
+        dk, dv = tk.DeviceArray.from_numpy(x), tk.DeviceArray.from_numpy(x[::-1].copy())
+        b.append(pool, 0, dk, dv)
+        tk.hip().sync()
+        gk, gv, gks, gvs = b.gather(pool, 0, 0, rows)
+        ck, sk = O.quantize_rows(x)
+        cv, sv = O.quantize_rows(x[::-1].copy())
+        assert np.array_equal(gk, ck) and np.array_equal(gv, cv)
+        if sf == tk.SCALE_F32:
+            assert np.array_equal(bits(gks), bits(sk)) and np.array_equal(bits(gvs), bits(sv))
+        else:
+            assert np.array_equal(gks, O.float_to_half(sk)) and np.array_equal(gvs, O.float_to_half(sv))
+        pool.close()
+
+
+# ---------------------------------------------------------------------------
+# attention
+# ---------------------------------------------------------------------------
+ATTN_CASES = {
+    # name: (q_heads, kv_heads, hd, fmt, sf, contexts, n_new, outliers)
+    "c1_shape_f16": (14, 2, 64, tk.KV_F16, 0, [1024], 1, 0),
+    "c2_shape_i8": (14, 2, 64, tk.KV_I8, 0, [700], 1, 0.01),
+    "c3_shape_multi": (12, 2, 128, tk.KV_F16, 0, [31, 512, 1200, 16], 1, 0),
+    "c5_shape_verify": (28, 4, 128, tk.KV_I8, 0, [40, 1000, 17, 300], 4, 0.01),
+    "i8_f32_scales": (14, 2, 64, tk.KV_I8, 1, [257, 64], 2, 0),
+    "verify_six": (14, 2, 64, tk.KV_F16, 0, [90, 13], 6, 0),
+    "span_edges": (8, 2, 64, tk.KV_F16, 0, [0, 15, 16, 17, 31, 32], 1, 0),
+}
+
+
+@pytest.mark.parametrize("name", list(ATTN_CASES))
+def test_decode_matches_oracle(gpu, name):
+    qh, kvh, hd, fmt, sf, ctx, nn, out = ATTN_CASES[name]
+    say(f"decode case {name}")
+    case = PagedCase(qh, kvh, hd, fmt, ctx, nn, scale_format=sf, seed=21, outlier_frac=out)
+    case.fill()
+    got, b = case.step()
+    want = case.oracle_out()
+    err = assert_attention_close(got, want, name)
+    say(f"  max abs err {err:.2e}, plan {b.info()}")
+    case.close()
+
+
+def test_decode_span_one_is_exact(gpu):
+    case = PagedCase(14, 2, 64, tk.KV_F16, [0, 0], 1, seed=3)
+    got, _ = case.step()
+    want = case.oracle_out()
+    assert np.array_equal(got, want)
+    case.close()
+
+
+def test_decode_split_k_long_context(gpu):
+    """A long context is split over many workgroups and merged by the
+    reduction pass; the result still matches the oracle."""
+    case = PagedCase(28, 4, 128, tk.KV_F16, [20000], 1, seed=9)
+    case.fill()
+    got, b = case.step()
+    rows, items, splits = b.info()
+    assert splits > 1, b.info()
+    assert_attention_close(got, case.oracle_out(), "split-k")
+    case.close()
+
+
+def test_decode_64_rows(gpu):
+    """n_new * group = 64 rows (four 16-row groups per unit)."""
+    case = PagedCase(16, 2, 128, tk.KV_I8, [333, 50], 8, seed=4)
+    case.fill()
+    got, _ = case.step()
+    assert_attention_close(got, case.oracle_out(), "64 rows")
+    case.close()
+
+
+def test_decode_rejects_more_than_64_rows(gpu):
+    case = PagedCase(16, 2, 64, tk.KV_F16, [10], 9, seed=4)
+    with pytest.raises(tk.TgeError) as e:
+        case.step()
+    assert e.value.status == tk.ERR_INVALID
+    case.close()
+
+
+def test_page_permutation_invariance(gpu):
+    """The same logical rows stored in two different page assignments give
+    bit-identical attention outputs."""
+    outs = []
+    for tseed in (1, 2):
+        case = PagedCase(14, 2, 64, tk.KV_I8, [500, 77], 2, seed=30,
+                         table=synth.fragmented_table(64, tseed))
+        case.fill()
+        got, _ = case.step()
+        outs.append(got)
+        assert case.pages[0] != [] and tseed in (1, 2)
+        case.close()
+    assert np.array_equal(bits(outs[0]), bits(outs[1]))
+
+
+def test_prefill_chunks_match_oracle(gpu):
+    """Chunked prefill (7B shapes, reduced length): 3 causal chunks of 96
+    appended then block-attended over all prior pages."""
+    qh, kvh, hd = 28, 4, 128
+    rng = np.random.default_rng(8)
+    total, chunk = 288, 96
+    k = synth.to_bf16_representable(rng.standard_normal((total, kvh * hd)).astype(np.float32))
+    v = synth.to_bf16_representable(rng.standard_normal((total, kvh * hd)).astype(np.float32))
+    q = synth.to_bf16_representable(rng.standard_normal((total, qh * hd)).astype(np.float32))
+    table = synth.fragmented_table(32, 5)
+    pages = [table.allocate() for _ in range(total // 16)]
+    pool = tk.KvPool(1, 32, kvh, hd, tk.KV_F16)
+    fc = O.FlatCache(O.F16, k, v)
+    for c0 in range(0, total, chunk):
+        b = tk.Batch().plan(pool, [tk.Session(c0, chunk, pages)], qh)
+        dk = tk.DeviceArray.from_numpy(k[c0:c0 + chunk])
+        dv = tk.DeviceArray.from_numpy(v[c0:c0 + chunk])
+        dq = tk.DeviceArray.from_numpy(q[c0:c0 + chunk])
+        dout = tk.DeviceArray((chunk, qh * hd), np.float32).zero()
+        b.append(pool, 0, dk, dv)
+        b.prefill(pool, 0, dq, dout)
+        tk.hip().sync()
+        want = fc.attend(q[c0:c0 + chunk], qh, kvh, hd, c0)
+        err = assert_attention_close(dout.numpy(), want, f"prefill chunk at {c0}")
+        say(f"  prefill chunk {c0}: max abs err {err:.2e}")
+    pool.close()
+
+
+def test_prefill_i8_matches_oracle(gpu):
+    case = PagedCase(14, 2, 64, tk.KV_I8, [40], 70, seed=12)
+    case.fill()
+    got, _ = case.step(kind="prefill")
+    assert_attention_close(got, case.oracle_out(), "i8 prefill")
+    case.close()

@@ -1,0 +1,394 @@
+"""Pins the CPU oracle (oracle/) before it is trusted as the checker.
+
+Each oracle function is checked against something that is not its own
+formula: the reference engine's code built from /root/reference
+(oracle/_ref), the reference tests' known-answer values, hardware IEEE
+conversions with an exactly characterised difference set, closed forms and
+float64 truth. CPU only.
+"""
+import ctypes as C
+import json
+import math
+import os
+import shutil
+import subprocess
+import tempfile
+
+import numpy as np
+import pytest
+
+import oracle as O
+from _util import bits, make_values
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+needs_ref = pytest.mark.skipif(not O.ref_available(), reason="oracle/_ref not built here")
+
+
+def f2h(x):
+    return O.orc().orc_float_to_half(C.c_float(x))
+
+
+def _fp(a):
+    return None if a is None else a.ctypes.data_as(C.c_void_p)
+
+
+# ---------------------------------------------------------------------------
+# float <-> half
+# ---------------------------------------------------------------------------
+def test_half_round_trip_kats():
+    # test_attention.cpp:107-115
+    for v in [0.0, 1.0, -1.0, 0.5, 2.0, 1024.0, 65504.0]:
+        back = O.orc().orc_half_to_float(f2h(v))
+        assert abs(back - v) <= max(abs(v) * 0.001, 1e-6)
+    assert f2h(math.inf) == 0x7C00
+
+
+def test_float_to_half_bit_kats():
+    f32 = lambda u: float(np.uint32(u).view(np.float32))
+    assert f2h(1.0) == 0x3C00
+    assert f2h(-2.0) == 0xC000
+    assert f2h(65504.0) == 0x7BFF
+    assert f2h(65519.0) == 0x7BFF
+    assert f2h(65520.0) == 0x7C00          # guard-bit carry into the exponent
+    assert f2h(-math.inf) == 0xFC00
+    assert f2h(math.nan) == 0x7E00
+    assert f2h(f32(0xFFC00001)) == 0xFE00  # any payload -> sign|0x7E00
+    assert f2h(2.0 ** -24) == 0x0001
+    assert f2h(1.5 * 2.0 ** -24) == 0x0002  # subnormal guard rounding
+    assert f2h(2.0 ** -25) == 0x0000        # below 2^-24 flushes
+    assert f2h(-(2.0 ** -25) * 1.9) == 0x8000
+    assert f2h(2.0 ** -14) == 0x0400
+    # an exact tie with an even truncated result rounds up (RNE would not)
+    assert f2h(1.0 + 2.0 ** -11) == 0x3C01
+    assert np.float16(1.0 + 2.0 ** -11).view(np.uint16) == 0x3C00
+    assert f2h(1.0 + 3 * 2.0 ** -11) == 0x3C02
+
+
+def test_half_to_float_exhaustive():
+    h = np.arange(65536, dtype=np.uint32).astype(np.uint16)
+    got = O.half_to_float(h)
+    want = h.view(np.float16).astype(np.float32)
+    nan = np.isnan(want)
+    assert np.array_equal(bits(got)[~nan], bits(want)[~nan])
+    assert np.all(np.isnan(got[nan]))
+    assert np.array_equal(np.signbit(got[nan]), np.signbit(want[nan]))
+    if O.ref_available():
+        r = np.array([O.ref().ref_half_to_float(int(x)) for x in h[::97]], np.float32)
+        assert np.array_equal(bits(r)[~np.isnan(r)], bits(got[::97])[~np.isnan(r)])
+
+
+@pytest.fixture(scope="module")
+def sweep_tool():
+    gcc = shutil.which("gcc")
+    if gcc is None:
+        pytest.skip("gcc not available")
+    d = tempfile.mkdtemp(prefix="tge_f16_")
+    exe = os.path.join(d, "f16_sweep")
+    subprocess.run([gcc, "-O2", "-mf16c", "-fopenmp", "-o", exe,
+                    os.path.join(HERE, "native", "f16_sweep.c"), "-ldl"], check=True)
+    yield exe
+    shutil.rmtree(d, ignore_errors=True)
+
+
+def test_float_to_half_exhaustive(sweep_tool):
+    """All 2^32 inputs: the oracle equals the reference build bit for bit and
+    differs from hardware RNE exactly on the predicted set, whose sizes are
+    closed forms (ties with an even truncation: 2*(30*512 + 511) = 31742;
+    flushed (2^-25, 2^-24): 2*(2^23-1); NaN payloads: 2*(2^23-1))."""
+    args = [sweep_tool, O.ORACLE_PATH, "orc_float_to_half"]
+    if O.ref_available():
+        args += [O.REF_PATH, "ref_float_to_half"]
+    res = json.loads(subprocess.run(args, check=True, capture_output=True, text=True).stdout)
+    assert res["violations"] == 0, res
+    assert res["ties_up"] == 31742
+    assert res["tiny_flush"] == 2 * (2 ** 23 - 1)
+    assert res["nan"] == 2 * (2 ** 23 - 1)
+    if O.ref_available():
+        assert res["vs_other"] == 0, res
+
+
+# ---------------------------------------------------------------------------
+# int8 block quantizer (qwen2.cpp:88-104)
+# ---------------------------------------------------------------------------
+def quant(block):
+    x = np.ascontiguousarray(block, np.float32)
+    codes = np.empty(32, np.int8)
+    s = O.orc().orc_quantize_kv_block(_fp(x), _fp(codes))
+    return codes, np.float32(s)
+
+
+def test_quantize_exact_multiples():
+    ks = np.array([127, -127, 0, 1, -1, 64, -63, 100] * 4, np.int32)
+    for step in (0.125, 2.0, 2.0 ** -10):
+        codes, s = quant(ks.astype(np.float32) * np.float32(step))
+        assert s == np.float32(step)
+        assert np.array_equal(codes.astype(np.int32), ks)
+
+
+def test_quantize_all_zero_block_takes_sign_of_last():
+    z = np.zeros(32, np.float32)
+    codes, s = quant(z)
+    assert np.all(codes == 0) and s == 0 and not np.signbit(s)
+    z[31] = -0.0
+    codes, s = quant(z)
+    assert np.all(codes == 0) and s == 0 and np.signbit(s)
+    z[:] = -0.0
+    z[31] = 0.0
+    _, s = quant(z)
+    assert not np.signbit(s)
+
+
+def test_quantize_half_rounding_is_add_then_truncate():
+    # scale 1 (max 127): codes are trunc(x +- 0.5) in fp32, so the float just
+    # below 0.5 becomes 1 (0.49999997 + 0.5 rounds to 1.0f), unlike
+    # rintf/roundf which give 0.
+    below_half = np.float32(np.nextafter(np.float32(0.5), np.float32(0)))
+    x = np.zeros(32, np.float32)
+    x[0] = 127
+    x[1], x[2] = below_half, -below_half
+    x[3], x[4], x[5], x[6] = 0.5, 1.5, 2.5, -2.5
+    x[7] = np.nextafter(np.float32(0.25), np.float32(0))
+    codes, s = quant(x)
+    assert s == 1.0
+    assert list(codes[:8]) == [127, 1, -1, 1, 2, 3, -3, 0]
+    assert round(float(below_half)) == 0
+
+
+def test_quantize_properties_random():
+    rng = np.random.default_rng(7)
+    for trial in range(400):
+        kind = trial % 4
+        x = rng.standard_normal(32).astype(np.float32)
+        if kind == 1:
+            x[rng.integers(0, 32)] *= 8
+        elif kind == 2:
+            x *= np.float32(1e-30)
+        elif kind == 3:
+            x *= np.float32(1e30)
+        codes, s = quant(x)
+        m = np.max(np.abs(x))
+        assert s == np.float32(m) / np.float32(127)
+        c = codes.astype(np.float64)
+        assert np.all(np.abs(c) <= 127)
+        assert np.abs(c[np.argmax(np.abs(x))]) == 127
+        # each code is the nearest integer to x/scale (within fp32 slack)
+        err = np.abs(c * float(s) - x.astype(np.float64))
+        assert np.all(err <= 0.5 * float(s) * (1 + 1e-5) + 1e-45)
+        assert np.all((np.sign(c) == np.sign(x)) | (c == 0))
+
+
+# ---------------------------------------------------------------------------
+# attention oracle against the reference build
+# ---------------------------------------------------------------------------
+def flat_inputs(fmt, span, head_dim, seed=2):
+    keys = make_values(span * head_dim, seed)
+    vals = make_values(span * head_dim, seed + 1)
+    if fmt == O.F16:
+        return O.float_to_half(keys), O.float_to_half(vals), None, None
+    if fmt == O.I8:
+        kc, ks = O.quantize_rows(keys.reshape(span, head_dim))
+        vc, vs = O.quantize_rows(vals.reshape(span, head_dim))
+        return kc.reshape(-1), vc.reshape(-1), ks.reshape(-1), vs.reshape(-1)
+    return keys, vals, None, None
+
+
+@needs_ref
+@pytest.mark.parametrize("fmt", [O.F32, O.F16, O.I8])
+def test_head_matches_reference_scalar_bitexact(fmt):
+    for span in (1, 7, 64, 257):
+        for hd in (64, 128):
+            q = make_values(hd, 1)
+            k, v, ks, vs = flat_inputs(fmt, span, hd)
+            scale = np.float32(1.0) / np.sqrt(np.float32(hd))
+            so, oo = np.empty(span, np.float32), np.empty(hd, np.float32)
+            sr, orr = np.empty(span, np.float32), np.empty(hd, np.float32)
+            assert O.orc().orc_attention_head(fmt, _fp(q), _fp(k), _fp(v), _fp(ks), _fp(vs), hd,
+                                              span, hd, C.c_float(scale), _fp(so), _fp(oo)) == 0
+            assert O.ref().ref_attention_head(0, fmt, _fp(q), _fp(k), _fp(v), _fp(ks), _fp(vs), hd,
+                                              span, hd, C.c_float(scale), _fp(sr), _fp(orr)) == 0
+            assert np.array_equal(bits(oo), bits(orr)), (fmt, span, hd)
+            assert np.array_equal(bits(so), bits(sr))
+            # and the shipped AVX2 kernel is within the reference's own 1e-4
+            sa, oa = np.empty(span, np.float32), np.empty(hd, np.float32)
+            O.ref().ref_attention_head(1, fmt, _fp(q), _fp(k), _fp(v), _fp(ks), _fp(vs), hd, span,
+                                       hd, C.c_float(scale), _fp(sa), _fp(oa))
+            assert np.max(np.abs(oa - oo)) <= 1e-4
+
+
+@needs_ref
+@pytest.mark.parametrize("fmt", [O.F32, O.F16, O.I8])
+def test_group_matches_reference_scalar_bitexact(fmt):
+    for count in (1, 9, 130):
+        for g in (1, 7):
+            hd = 64
+            qs = make_values(g * hd, 11)
+            k, v, ks, vs = flat_inputs(fmt, count, hd, seed=5)
+            scale = C.c_float(0.125)
+            outs = []
+            for which in ("orc", "ref"):
+                mx, sm = np.empty(g, np.float32), np.empty(g, np.float32)
+                ac = np.empty(g * hd, np.float32)
+                if which == "orc":
+                    O.orc().orc_attention_group(fmt, _fp(qs), _fp(k), _fp(v), _fp(ks), _fp(vs), hd,
+                                                count, hd, g, scale, _fp(mx), _fp(sm), _fp(ac))
+                else:
+                    O.ref().ref_attention_group(0, fmt, _fp(qs), _fp(k), _fp(v), _fp(ks), _fp(vs),
+                                                hd, count, hd, g, scale, _fp(mx), _fp(sm), _fp(ac))
+                outs.append((mx, sm, ac))
+            for a, b in zip(*outs):
+                assert np.array_equal(bits(a), bits(b)), (fmt, count, g)
+
+
+def test_head_rejects_bad_arguments():
+    # attention_scalar.cpp:11-44: span 0, stride < head_dim, ragged q8
+    q = make_values(64, 1)
+    k, v, ks, vs = flat_inputs(O.I8, 4, 64)
+    sc, out = np.empty(4, np.float32), np.empty(64, np.float32)
+    f = O.orc().orc_attention_head
+    assert f(O.I8, _fp(q), _fp(k), _fp(v), _fp(ks), _fp(vs), 64, 0, 64, C.c_float(1), _fp(sc), _fp(out)) == -1
+    assert f(O.I8, _fp(q), _fp(k), _fp(v), _fp(ks), _fp(vs), 32, 4, 64, C.c_float(1), _fp(sc), _fp(out)) == -1
+    assert f(O.I8, _fp(q), _fp(k), _fp(v), _fp(ks), _fp(vs), 48, 1, 48, C.c_float(1), _fp(sc), _fp(out)) == -1
+    assert f(O.I8, _fp(q), _fp(k), _fp(v), None, _fp(vs), 64, 4, 64, C.c_float(1), _fp(sc), _fp(out)) == -1
+
+
+# ---------------------------------------------------------------------------
+# closed forms
+# ---------------------------------------------------------------------------
+def test_span_one_returns_first_value_row():
+    for fmt in (O.F32, O.F16, O.I8):
+        k, v, ks, vs = flat_inputs(fmt, 1, 64)
+        q = make_values(64, 3) * 50
+        out = O.attention_head(fmt, q, k, v, ks, vs, 64, 1, 64, 0.125)
+        if fmt == O.F16:
+            want = O.half_to_float(v)
+        elif fmt == O.I8:
+            want = v.astype(np.float32) * np.repeat(vs, 32)
+        else:
+            want = v
+        assert np.array_equal(out, want.astype(np.float32))
+
+
+def test_equal_keys_give_mean_of_values():
+    span, hd = 37, 64
+    key = make_values(hd, 9)
+    keys = np.tile(key, span)
+    vals = make_values(span * hd, 10)
+    out = O.attention_head(O.F32, make_values(hd, 4), keys, vals, None, None, hd, span, hd, 0.125)
+    want = vals.reshape(span, hd).astype(np.float64).mean(axis=0)
+    assert np.max(np.abs(out - want)) < 1e-6
+
+
+def test_dominant_key_selects_its_value():
+    span, hd = 50, 64
+    q = np.ones(hd, np.float32)
+    keys = np.zeros((span, hd), np.float32)
+    keys[23] = 10.0  # score 10*64*scale = 80 above the rest
+    vals = make_values(span * hd, 12).reshape(span, hd)
+    out = O.attention_head(O.F32, q, keys.reshape(-1), vals.reshape(-1), None, None, hd, span,
+                           hd, 0.125)
+    assert np.max(np.abs(out - vals[23])) < 1e-6
+
+
+def test_fp32_oracle_close_to_float64_truth():
+    rng = np.random.default_rng(3)
+    for fmt in (O.F32, O.F16, O.I8):
+        span, hd = 700, 128
+        kf = rng.standard_normal((span, hd)).astype(np.float32)
+        vf = rng.standard_normal((span, hd)).astype(np.float32)
+        cache = O.FlatCache(fmt, kf, vf)
+        q = rng.standard_normal(hd).astype(np.float32)
+        o32 = cache.head(q, 0, hd, span)
+        o64 = cache.head(q, 0, hd, span, f64=True)
+        assert np.max(np.abs(o32 - o64)) < 2e-6
+
+
+def test_gqa_split_invariance():
+    """qwen2.cpp attention_gqa (split-K + merge_gqa_chunks) equals the per-head
+    oracle for every chunk count the thread rule produces."""
+    rng = np.random.default_rng(4)
+    heads, kvh, hd = 14, 2, 64
+    for span in (256, 1024, 1500):
+        kf = rng.standard_normal((span, kvh * hd)).astype(np.float32)
+        vf = rng.standard_normal((span, kvh * hd)).astype(np.float32)
+        cache = O.FlatCache(O.F16, kf, vf)
+        q = rng.standard_normal(heads * hd).astype(np.float32)
+        want = np.concatenate([cache.head(q[h * hd:(h + 1) * hd], h // 7, hd, span)
+                               for h in range(heads)])
+        for threads in (1, 2, 6, 16):
+            out = np.empty(heads * hd, np.float32)
+            O.orc().orc_attention_gqa(O.F16, _fp(q), _fp(cache.k), _fp(cache.v), None, None, heads,
+                                      kvh, hd, span, threads, _fp(out))
+            assert np.max(np.abs(out - want)) < 1e-5, (span, threads)
+
+
+def test_gqa_chunk_rule():
+    cs = C.c_int()
+    assert O.orc().orc_gqa_chunks(300, 2, 6, C.byref(cs)) == 6 and cs.value == 50
+    assert O.orc().orc_gqa_chunks(2048, 2, 1, C.byref(cs)) == 4 and cs.value == 512
+    assert O.orc().orc_gqa_chunks(100000, 1, 64, C.byref(cs)) == 16
+
+
+def test_merge_skips_empty_chunks_and_zeroes_when_none():
+    hd = 4
+    mx = np.array([1.0, 5.0, 2.0], np.float32)
+    sm = np.array([2.0, 0.0, 3.0], np.float32)
+    ac = np.arange(12, dtype=np.float32)
+    out = np.empty(hd, np.float32)
+    O.orc().orc_merge_chunks(_fp(mx), _fp(sm), _fp(ac), 0, 3, 1, 0, hd, _fp(out))
+    a, b = math.exp(1 - 2), 1.0
+    want = (ac[0:4] * a + ac[8:12] * b) / (2 * a + 3 * b)
+    assert np.max(np.abs(out - want)) < 1e-6
+    sm[:] = 0
+    O.orc().orc_merge_chunks(_fp(mx), _fp(sm), _fp(ac), 0, 3, 1, 0, hd, _fp(out))
+    assert np.all(out == 0)
+
+
+def test_block_prefill_matches_per_head_oracle():
+    rng = np.random.default_rng(5)
+    heads, kvh, hd, start, tokens = 4, 2, 64, 40, 24
+    kv_dim, qd = kvh * hd, heads * hd
+    kf = rng.standard_normal((start + tokens, kv_dim)).astype(np.float32)
+    vf = rng.standard_normal((start + tokens, kv_dim)).astype(np.float32)
+    cache = O.FlatCache(O.F16, kf, vf)
+    q = rng.standard_normal((tokens, qd)).astype(np.float32)
+    out = np.zeros((tokens, qd), np.float32)
+    scores = np.empty(tokens * (start + tokens), np.float32)
+    for h in range(heads):
+        assert O.orc().orc_attention_block_head(O.F16, _fp(q), _fp(cache.k), _fp(cache.v), tokens,
+                                                start, hd, kv_dim, (h // 2) * hd, qd, h,
+                                                C.c_float(0.125), _fp(scores), _fp(out)) == 0
+    want = cache.attend(q, heads, kvh, hd, start)
+    assert np.max(np.abs(out - want)) < 1e-5
+    if O.ref_available():
+        ref_out = np.zeros((tokens, qd), np.float32)
+        ctx = start + tokens
+        sc = np.empty(tokens * heads * ctx, np.float32)
+        for h in range(heads):
+            O.ref().ref_attention_block_head(O.F16, _fp(q), _fp(cache.k), _fp(cache.v), tokens,
+                                             start, hd, kv_dim, (h // 2) * hd, qd, heads * ctx, ctx,
+                                             C.c_float(0.125), h,
+                                             _fp(sc[h * ctx:]), _fp(ref_out))
+        assert np.max(np.abs(ref_out - out)) < 1e-4
+
+
+# ---------------------------------------------------------------------------
+# flat layout and gather KATs
+# ---------------------------------------------------------------------------
+def test_kv_layer_offset_kats():
+    # test_gguf.cpp:842-846
+    f = O.orc().orc_kv_layer_offset
+    assert f(0, 0, 2, 16, 8) == 0
+    assert f(1, 0, 2, 16, 8) == 256
+    assert f(1, 1, 2, 16, 8) == 384
+
+
+@needs_ref
+def test_reference_gather_order_kat():
+    # test_block_table.cpp:121-136: table {2, 0} over {1,2},{3,4},{5,6}
+    pool = np.array([1, 2, 3, 4, 5, 6], np.float32)
+    out = np.empty(4, np.float32)
+    table = (C.c_int * 2)(2, 0)
+    assert O.ref().ref_gather_blocks(_fp(pool), 3, 2, table, 2, 2, _fp(out)) == 4
+    assert list(out) == [5, 6, 1, 2]
+    bad = (C.c_int * 1)(9)
+    assert O.ref().ref_gather_blocks(_fp(pool), 3, 2, bad, 1, 2, _fp(out)) == -1
