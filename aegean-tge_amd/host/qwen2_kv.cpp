@@ -5,6 +5,7 @@
 #include "../csrc/tge_error.h"
 
 #include <algorithm>
+#include <memory>
 #include <stdexcept>
 #include <string>
 
@@ -198,6 +199,14 @@ void Qwen2KvPath::layer(int layer, const float* q, const float* k, const float* 
   }
 }
 
+void Qwen2KvPath::store(int layer, const float* k, const float* v, void* stream) {
+  if (!begun_) throw std::runtime_error("store: no step begun");
+  if (layer < 0 || layer >= config_.layers) {
+    throw std::invalid_argument("store: layer out of range");
+  }
+  check(tge_kv_append(batch_, pool_, layer, k, v, stream), "store");
+}
+
 void Qwen2KvPath::reset_cache(int sequence) {
   // qwen2.cpp:2540-2543; zero-fill becomes page release.
   if (sequence < 0 || sequence >= config_.sequences) {
@@ -243,14 +252,20 @@ int guarded(F&& f) {
 
 }  // namespace
 
+// A table handle either owns its BlockTable or views the one a driver owns.
 struct tge_block_table {
-  tge::models::BlockTable impl;
-  tge_block_table(int blocks, int tokens) : impl(blocks, tokens) {}
+  std::unique_ptr<tge::models::BlockTable> owned;
+  tge::models::BlockTable* table;
+  tge_block_table(int blocks, int tokens)
+      : owned(std::make_unique<tge::models::BlockTable>(blocks, tokens)), table(owned.get()) {}
+  explicit tge_block_table(tge::models::BlockTable* view) : table(view) {}
 };
 
 struct tge_qwen2_kv {
   tge::models::Qwen2KvPath impl;
-  explicit tge_qwen2_kv(const tge::models::Qwen2KvConfig& c) : impl(c) {}
+  tge_block_table table_view;
+  explicit tge_qwen2_kv(const tge::models::Qwen2KvConfig& c)
+      : impl(c), table_view(&impl.mutable_table()) {}
 };
 
 extern "C" {
@@ -262,32 +277,32 @@ int tge_block_table_create(int blocks, int block_tokens, tge_block_table** out) 
 void tge_block_table_destroy(tge_block_table* t) { delete t; }
 int tge_block_table_allocate(tge_block_table* t, int* block) {
   if (!t || !block) return TGE_ERR_INVALID;
-  return guarded([&] { *block = t->impl.allocate(); });
+  return guarded([&] { *block = t->table->allocate(); });
 }
 int tge_block_table_share(tge_block_table* t, int block) {
   if (!t) return TGE_ERR_INVALID;
-  return guarded([&] { t->impl.share(block); });
+  return guarded([&] { t->table->share(block); });
 }
 int tge_block_table_release(tge_block_table* t, int block) {
   if (!t) return TGE_ERR_INVALID;
-  return guarded([&] { t->impl.release(block); });
+  return guarded([&] { t->table->release(block); });
 }
 int tge_block_table_refcount(const tge_block_table* t, int block, int* out) {
   if (!t || !out) return TGE_ERR_INVALID;
-  return guarded([&] { *out = t->impl.refcount(block); });
+  return guarded([&] { *out = t->table->refcount(block); });
 }
 int tge_block_table_free_count(const tge_block_table* t) {
-  return t ? t->impl.free_count() : TGE_ERR_INVALID;
+  return t ? t->table->free_count() : TGE_ERR_INVALID;
 }
 int tge_block_table_capacity(const tge_block_table* t) {
-  return t ? t->impl.capacity() : TGE_ERR_INVALID;
+  return t ? t->table->capacity() : TGE_ERR_INVALID;
 }
 int tge_block_table_remember_prefix(tge_block_table* t, uint64_t hash, int block) {
   if (!t) return TGE_ERR_INVALID;
-  return guarded([&] { t->impl.remember_prefix(hash, block); });
+  return guarded([&] { t->table->remember_prefix(hash, block); });
 }
 int tge_block_table_find_prefix(const tge_block_table* t, uint64_t hash) {
-  return t ? t->impl.find_prefix(hash) : TGE_ERR_INVALID;
+  return t ? t->table->find_prefix(hash) : TGE_ERR_INVALID;
 }
 int tge_slot_for(int logical_pos, int block_tokens, int* block, int* offset) {
   if (!block || !offset) return TGE_ERR_INVALID;
@@ -341,6 +356,11 @@ int tge_qwen2_kv_layer(tge_qwen2_kv* m, int layer, const float* q, const float* 
   if (!m) return TGE_ERR_INVALID;
   return guarded([&] { m->impl.layer(layer, q, k, v, out, stream); });
 }
+int tge_qwen2_kv_store(tge_qwen2_kv* m, int layer, const float* k, const float* v,
+                       void* stream) {
+  if (!m) return TGE_ERR_INVALID;
+  return guarded([&] { m->impl.store(layer, k, v, stream); });
+}
 int tge_qwen2_kv_reset(tge_qwen2_kv* m, int sequence) {
   if (!m) return TGE_ERR_INVALID;
   return guarded([&] { m->impl.reset_cache(sequence); });
@@ -363,6 +383,7 @@ int tge_qwen2_kv_pages(const tge_qwen2_kv* m, int sequence, int* ids, int cap) {
 }
 const tge_kv_pool* tge_qwen2_kv_pool(const tge_qwen2_kv* m) { return m ? m->impl.pool() : nullptr; }
 const tge_batch* tge_qwen2_kv_batch(const tge_qwen2_kv* m) { return m ? m->impl.batch() : nullptr; }
+tge_block_table* tge_qwen2_kv_table(tge_qwen2_kv* m) { return m ? &m->table_view : nullptr; }
 int tge_qwen2_kv_free_pages(const tge_qwen2_kv* m) {
   return m ? m->impl.table().free_count() : TGE_ERR_INVALID;
 }

@@ -100,12 +100,7 @@ def fragmented_table(pages, seed):
     """A BlockTable whose free list has been shuffled: allocate every page,
     then release them in a seeded random order. Later allocations pop the
     free list LIFO, so sessions receive scattered physical pages."""
-    t = tge_kv.BlockTable(pages)
-    ids = [t.allocate() for _ in range(pages)]
-    order = np.random.default_rng(seed).permutation(len(ids))
-    for i in order:
-        t.release(ids[int(i)])
-    return t
+    return tge_kv.BlockTable(pages).fragment(seed)
 
 
 def normal(rng, shape):

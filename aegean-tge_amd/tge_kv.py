@@ -96,12 +96,14 @@ SIGNATURES = [
     ("tge_qwen2_kv_begin_prefill", _I, [_VP, _I, _I, _I, _VP]),
     ("tge_qwen2_kv_begin_verify", _I, [_VP, _I, _I, _I, _VP]),
     ("tge_qwen2_kv_layer", _I, [_VP, _I, _VP, _VP, _VP, _VP, _VP]),
+    ("tge_qwen2_kv_store", _I, [_VP, _I, _VP, _VP, _VP]),
     ("tge_qwen2_kv_reset", _I, [_VP, _I]),
     ("tge_qwen2_kv_length", _I, [_VP, _I]),
     ("tge_qwen2_kv_pages", _I, [_VP, _I, _PI, _I]),
     ("tge_qwen2_kv_pool", _VP, [_VP]),
     ("tge_qwen2_kv_batch", _VP, [_VP]),
     ("tge_qwen2_kv_free_pages", _I, [_VP]),
+    ("tge_qwen2_kv_table", _VP, [_VP]),
 ]
 
 
@@ -270,7 +272,11 @@ def _ints(values):
 class BlockTable:
     """tge_block_table_*: the reference BlockTable's behaviour (host side)."""
 
-    def __init__(self, blocks, block_tokens=PAGE_TOKENS):
+    def __init__(self, blocks, block_tokens=PAGE_TOKENS, view=None):
+        self.owned = view is None
+        if view is not None:
+            self.h = C.c_void_p(view)
+            return
         h = C.c_void_p()
         check(lib().tge_block_table_create(blocks, block_tokens, C.byref(h)), "BlockTable")
         self.h = h
@@ -317,10 +323,18 @@ class BlockTable:
         check(lib().tge_hash_tokens(arr, len(tokens), C.byref(out)), "hash_tokens")
         return out.value
 
+    def fragment(self, seed):
+        """Allocate every free page, then release them in a seeded random
+        order: later allocations pop scattered ids (LIFO)."""
+        ids = [self.allocate() for _ in range(self.free_count())]
+        for i in np.random.default_rng(seed).permutation(len(ids)):
+            self.release(ids[int(i)])
+        return self
+
     def close(self):
-        if self.h:
+        if self.h and self.owned:
             lib().tge_block_table_destroy(self.h)
-            self.h = None
+        self.h = None
 
     def __del__(self):
         try:
@@ -365,6 +379,13 @@ class Session:
     pages: list
 
 
+def batch_info(handle):
+    """(rows, decode work items, max splits) of a planned tge_batch handle."""
+    r, w, s = C.c_int(), C.c_int(), C.c_int()
+    check(lib().tge_batch_info(handle, C.byref(r), C.byref(w), C.byref(s)), "batch_info")
+    return r.value, w.value, s.value
+
+
 class Batch:
     def __init__(self):
         h = C.c_void_p()
@@ -389,9 +410,7 @@ class Batch:
         return self
 
     def info(self):
-        r, w, s = C.c_int(), C.c_int(), C.c_int()
-        check(lib().tge_batch_info(self.h, C.byref(r), C.byref(w), C.byref(s)), "batch_info")
-        return r.value, w.value, s.value
+        return batch_info(self.h)
 
     def append(self, pool, layer, k, v, stream=None):
         check(lib().tge_kv_append(self.h, pool.h, layer, k.ptr, v.ptr, stream), "kv_append")
@@ -464,6 +483,21 @@ class Qwen2KvPath:
     def layer(self, layer, q, k, v, out):
         check(lib().tge_qwen2_kv_layer(self.h, layer, q.ptr, k.ptr, v.ptr, out.ptr, None), "layer")
 
+    def store(self, layer, k, v):
+        """Append-only (cache priming); k/v are DeviceArrays or raw device addresses."""
+        kp = k if isinstance(k, int) else k.ptr
+        vp = v if isinstance(v, int) else v.ptr
+        check(lib().tge_qwen2_kv_store(self.h, layer, kp, vp, None), "store")
+
+    def layer_ptrs(self, layer, q, k, v, out):
+        check(lib().tge_qwen2_kv_layer(self.h, layer, q, k, v, out, None), "layer")
+
+    def pool_handle(self):
+        return lib().tge_qwen2_kv_pool(self.h)
+
+    def batch_handle(self):
+        return lib().tge_qwen2_kv_batch(self.h)
+
     def reset(self, sequence):
         check(lib().tge_qwen2_kv_reset(self.h, sequence), "reset_cache")
 
@@ -482,6 +516,10 @@ class Qwen2KvPath:
 
     def free_pages(self):
         return lib().tge_qwen2_kv_free_pages(self.h)
+
+    def table(self):
+        """A view of the driver's BlockTable (not owned)."""
+        return BlockTable(0, view=lib().tge_qwen2_kv_table(self.h))
 
     def close(self):
         if self.h:

@@ -64,6 +64,11 @@ class Qwen2KvPath {
   void layer(int layer, const float* q, const float* k, const float* v, float* out,
              void* stream = nullptr);
 
+  // Store this step's K/V rows for `layer` without attending: the cache-
+  // priming path (prime_cache_from_table, qwen2.hpp:283-288 and
+  // qwen2.cpp:1973-2026, copies rows into a slot with no recompute).
+  void store(int layer, const float* k, const float* v, void* stream = nullptr);
+
   // reset_cache(sequence): the sequence's pages go back to the table in
   // logical order; reset_cache() does every sequence.
   void reset_cache(int sequence);
@@ -72,6 +77,10 @@ class Qwen2KvPath {
   int length(int sequence) const;
   const std::vector<int>& pages(int sequence) const;
   const BlockTable& table() const { return *table_; }
+  // The page allocator itself, e.g. to pre-shape its free list before the
+  // first step (fragmented pools). Pages a sequence holds must not be
+  // released through it.
+  BlockTable& mutable_table() { return *table_; }
   const tge_kv_pool* pool() const { return pool_; }
   const tge_batch* batch() const { return batch_; }
   int step_rows() const { return step_rows_; }

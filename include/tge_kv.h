@@ -260,6 +260,10 @@ int tge_qwen2_kv_begin_verify(tge_qwen2_kv* model, int sequence,
 int tge_qwen2_kv_layer(tge_qwen2_kv* model, int layer, const float* q,
                        const float* k, const float* v, float* out,
                        void* stream);
+/* Store the step's K/V rows for `layer` without attending: cache priming
+ * (prime_cache_from_table, qwen2.hpp:283-288). */
+int tge_qwen2_kv_store(tge_qwen2_kv* model, int layer, const float* k,
+                       const float* v, void* stream);
 /* reset_cache(sequence): release the sequence's pages in logical order. */
 int tge_qwen2_kv_reset(tge_qwen2_kv* model, int sequence);
 /* Positions currently cached for a sequence; its page ids (logical order). */
@@ -269,6 +273,10 @@ int tge_qwen2_kv_pages(const tge_qwen2_kv* model, int sequence, int* ids,
 const tge_kv_pool* tge_qwen2_kv_pool(const tge_qwen2_kv* model);
 const tge_batch* tge_qwen2_kv_batch(const tge_qwen2_kv* model);
 int tge_qwen2_kv_free_pages(const tge_qwen2_kv* model);
+/* The driver's own block table (a view, owned by the driver; do not destroy).
+ * Lets a caller pre-shape the free list before the first step; pages held by
+ * sequences must not be released through it. */
+tge_block_table* tge_qwen2_kv_table(tge_qwen2_kv* model);
 
 #ifdef __cplusplus
 }
