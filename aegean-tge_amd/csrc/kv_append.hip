@@ -57,12 +57,12 @@ __global__ __launch_bounds__(256) void kv_append_kernel(AppendParams p) {
         w.y = hx[4 * g + 2] | ((uint32_t)hx[4 * g + 3] << 16);
         w.z = hx[16 + 4 * g + 0] | ((uint32_t)hx[16 + 4 * g + 1] << 16);
         w.w = hx[16 + 4 * g + 2] | ((uint32_t)hx[16 + 4 * g + 3] << 16);
-        *reinterpret_cast<uint4*>(dst + k_index(t, 32 * b + 4 * g)) = w;
+        *reinterpret_cast<uint4*>(dst + k_index_np(t, 32 * b + 4 * g, nb)) = w;
       }
     } else {
       uint16_t* dst = static_cast<uint16_t*>(p.vpool) + block * elems;
 #pragma unroll
-      for (int d = 0; d < 32; ++d) dst[v_index(t, 32 * b + d)] = hx[d];
+      for (int d = 0; d < 32; ++d) dst[v_index_np(t, 32 * b + d, nb)] = hx[d];
     }
   } else {
     int8_t c[32];
@@ -77,19 +77,19 @@ __global__ __launch_bounds__(256) void kv_append_kernel(AppendParams p) {
         w.y = (uint8_t)c[16 + 4 * g] | ((uint32_t)(uint8_t)c[16 + 4 * g + 1] << 8) |
               ((uint32_t)(uint8_t)c[16 + 4 * g + 2] << 16) |
               ((uint32_t)(uint8_t)c[16 + 4 * g + 3] << 24);
-        *reinterpret_cast<uint2*>(dst + k_index(t, 32 * b + 4 * g)) = w;
+        *reinterpret_cast<uint2*>(dst + k_index_np(t, 32 * b + 4 * g, nb)) = w;
       }
     } else {
       int8_t* dst = static_cast<int8_t*>(p.vpool) + block * elems;
 #pragma unroll
-      for (int d = 0; d < 32; ++d) dst[v_index(t, 32 * b + d)] = c[d];
+      for (int d = 0; d < 32; ++d) dst[v_index_np(t, 32 * b + d, nb)] = c[d];
     }
     const size_t sblock = block * (size_t)(16 * nb);
     void* sp = which ? p.vscale : p.kscale;
     if (p.scale_f32) {
-      static_cast<float*>(sp)[sblock + scale_index(t, b)] = scale;
+      static_cast<float*>(sp)[sblock + scale_index_np(t, b, nb)] = scale;
     } else {
-      static_cast<uint16_t*>(sp)[sblock + scale_index(t, b)] = float_to_half_ref(scale);
+      static_cast<uint16_t*>(sp)[sblock + scale_index_np(t, b, nb)] = float_to_half_ref(scale);
     }
   }
 }
@@ -105,13 +105,14 @@ __global__ __launch_bounds__(256) void kv_gather_kernel(GatherParams p) {
   const int c = (int)(idx % kv_dim);
   const int h = c / p.head_dim, d = c % p.head_dim;
   const int page = p.table[pos >> 4], t = pos & 15;
+  const int np = p.head_dim >> 5;
   const size_t block = ((size_t)page * p.kv_heads + h) * (size_t)(16 * p.head_dim);
-  static_cast<T*>(p.k_rows)[idx] = static_cast<const T*>(p.kpool)[block + k_index(t, d)];
-  static_cast<T*>(p.v_rows)[idx] = static_cast<const T*>(p.vpool)[block + v_index(t, d)];
+  static_cast<T*>(p.k_rows)[idx] = static_cast<const T*>(p.kpool)[block + k_index_np(t, d, np)];
+  static_cast<T*>(p.v_rows)[idx] = static_cast<const T*>(p.vpool)[block + v_index_np(t, d, np)];
   if (p.k_scales && (d & 31) == 0) {
     const size_t sb = ((size_t)page * p.kv_heads + h) * (size_t)(16 * (p.head_dim >> 5));
     const size_t o = (size_t)pos * (kv_dim >> 5) + (c >> 5);
-    const int si = scale_index(t, d >> 5);
+    const int si = scale_index_np(t, d >> 5, np);
     if (p.scale_bytes == 4) {
       static_cast<float*>(p.k_scales)[o] = static_cast<const float*>(p.kscale)[sb + si];
       static_cast<float*>(p.v_scales)[o] = static_cast<const float*>(p.vscale)[sb + si];

@@ -162,8 +162,15 @@ const char* tge_backend_arch(void) {
   return g_backend.arch.c_str();
 }
 
-int tge_kv_k_index(int token, int dim) { return tge::k_index(token, dim); }
-int tge_kv_v_index(int token, int dim) { return tge::v_index(token, dim); }
+int tge_kv_k_index(int token, int dim, int head_dim) {
+  return tge::k_index_np(token, dim, head_dim / 32);
+}
+int tge_kv_v_index(int token, int dim, int head_dim) {
+  return tge::v_index_np(token, dim, head_dim / 32);
+}
+int tge_kv_scale_index(int token, int block, int head_dim) {
+  return tge::scale_index_np(token, block, head_dim / 32);
+}
 
 // ---------------------------------------------------------------------------
 // Pool
@@ -191,6 +198,12 @@ int tge_kv_pool_create(const tge_kv_pool_desc* desc, tge_kv_pool** out) {
       d.format == TGE_KV_I8 ? (size_t)16 * (d.head_dim / 32) * (d.scale_format == TGE_SCALE_F32 ? 4 : 2)
                             : 0;
   p->layer_blocks = (size_t)d.pages * d.kv_heads;
+  // Attention kernels address one layer's K, V and scale arrays with 32-bit
+  // buffer offsets.
+  if (p->kv_block_bytes * p->layer_blocks >= (size_t(1) << 31)) {
+    delete p;
+    return fail(TGE_ERR_CAPACITY, "kv_pool_create: one layer's K array must stay below 2 GiB");
+  }
   const size_t kv_total = p->kv_block_bytes * p->layer_blocks * d.layers;
   const size_t sc_total = p->scale_block_bytes * p->layer_blocks * d.layers;
   hipError_t e = hipMalloc(&p->k, kv_total);
@@ -525,6 +538,8 @@ tge::AttnParams attn_params(const tge_batch* b, const tge_kv_pool* p, int layer,
   a.vpool = v.v;
   a.kscale = v.k_scales;
   a.vscale = v.v_scales;
+  a.kv_array_bytes = (uint32_t)(p->kv_block_bytes * p->layer_blocks);
+  a.scale_array_bytes = (uint32_t)(p->scale_block_bytes * p->layer_blocks);
   a.sessions = reinterpret_cast<const tge::SessionRec*>(b->dev + b->off_sessions);
   a.work = reinterpret_cast<const tge::WorkRec*>(pl.dev);
   a.tables = reinterpret_cast<const int*>(b->dev + b->off_tables);

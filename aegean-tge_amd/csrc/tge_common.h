@@ -14,32 +14,35 @@ constexpr int kMaxRows = 64;     // query rows (n_new * group) per decode unit
 enum Format { kF16 = 1, kI8 = 2 };
 
 // ---------------------------------------------------------------------------
-// Page layout. One page block = 16 tokens x head_dim of one KV head. The
-// in-block order is the register order of the CDNA4 matrix-core operands, so
-// that every lane of a wave fetches its operand with one contiguous 16-byte
-// (f16) or 8-byte (int8) load and a wave's load covers a contiguous 1 KiB:
+// Page layout. One page block = 16 tokens x head_dim (D) of one KV head; NP =
+// D/32. The in-block order is the register order of the CDNA4 matrix-core
+// operands, arranged so that each lane of a wave owns one contiguous chunk of
+// NP*8 elements (D=128: 64 B f16, 32 B int8) that it fetches with 16-byte
+// loads, and a wave's chunks tile the whole block:
 //
-//  K (A operand of S^T = K Q^T, v_mfma_f32_16x16x16_f16, row = token):
-//    dim d -> pair p = d/32, half h = (d/16)&1, group g = (d/4)&3, e = d&3
-//    index = ((p*4 + g)*16 + t)*8 + h*4 + e
-//    lane (g, t) of a wave reads the 8 elements at ((p*4+g)*16+t)*8: the
-//    operand for dims 32p+4g.. (h=0) and 32p+16+4g.. (h=1).
-//  V (A operand of O^T = V^T P^T, row = dim):
+//  K (A operand of S^T = K.Q^T, row = token t):
+//    d -> pair p = d/32, half h = (d/16)&1, group g = (d/4)&3, e = d&3
+//    index = ((g*16 + t)*NP + p)*8 + h*4 + e
+//    lane (g, t) holds, per pair p, dims 32p+4g+e and 32p+16+4g+e: the
+//    v_mfma_f32_16x16x32_f16 A operand of the 32-dim block p (k = 8g + j).
+//  V (A operand of O^T = V^T.P^T, row = dim):
 //    tile j = d/16, pair p = j/2, h = j&1, dl = d&15, g = t/4, e = t&3
-//    index = ((p*4 + g)*16 + dl)*8 + h*4 + e
-//    lane (g, dl) reads tokens 4g..4g+3 of dims 32p+dl (h=0), 32p+16+dl (h=1).
-//  Scales (I8): one per (token, 32-dim block b): index b*16 + t, so the four
-//    tokens a lane's accumulator rows cover are 4 consecutive scales.
+//    index = ((g*16 + dl)*NP + p)*8 + h*4 + e
+//    lane (g, dl) holds tokens 4g..4g+3 of dims 32p+dl (h=0), 32p+16+dl
+//    (h=1): the v_mfma_f32_16x16x16_f16 A operand of tile j.
+//  Scales (I8), one per (token t, 32-dim block b):
+//    index = ((t/4)*NP + b)*4 + (t&3)
+//    lanes of group g read the 4*NP scales of their four tokens at once.
 // ---------------------------------------------------------------------------
-__host__ __device__ inline int k_index(int t, int d) {
-  return ((((d >> 5) << 2) + ((d >> 2) & 3)) * 16 + t) * 8 + (((d >> 4) & 1) << 2) +
-         (d & 3);
+__host__ __device__ inline int k_index_np(int t, int d, int np) {
+  return ((((d >> 2) & 3) * 16 + t) * np + (d >> 5)) * 8 + (((d >> 4) & 1) << 2) + (d & 3);
 }
-__host__ __device__ inline int v_index(int t, int d) {
-  return ((((d >> 5) << 2) + (t >> 2)) * 16 + (d & 15)) * 8 + (((d >> 4) & 1) << 2) +
-         (t & 3);
+__host__ __device__ inline int v_index_np(int t, int d, int np) {
+  return (((t >> 2) * 16 + (d & 15)) * np + (d >> 5)) * 8 + (((d >> 4) & 1) << 2) + (t & 3);
 }
-__host__ __device__ inline int scale_index(int t, int b) { return b * 16 + t; }
+__host__ __device__ inline int scale_index_np(int t, int b, int np) {
+  return ((t >> 2) * np + b) * 4 + (t & 3);
+}
 
 // ---------------------------------------------------------------------------
 // Plan records (built on the host once per step, read by every layer).

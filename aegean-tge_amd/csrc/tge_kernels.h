@@ -40,6 +40,8 @@ struct GatherParams {
 
 struct AttnParams {
   const void* kpool;  // layer base pointers
+  uint32_t kv_array_bytes;     // bytes of one layer's K (= V) array, < 2^31
+  uint32_t scale_array_bytes;  // bytes of one layer's scale array (I8)
   const void* vpool;
   const void* kscale;
   const void* vscale;

@@ -61,6 +61,7 @@ class Config:
     churn_every: int = 0
     churn_sessions: int = 0
     churn_context: int = 0
+    fragmented: bool = True   # pool free list shuffled before the first session
     seed: int = 0
     note: str = field(default="")
 
@@ -73,7 +74,7 @@ def configs():
         "c1": Config("c1", QWEN2_0_5B, tge_kv.KV_F16, [1024], steps=64, pool_pages=128, seed=1,
                      note="1 seq, f16, ctx 1024 + 64 decode steps, 128-page permuted pool"),
         "c2": Config("c2", QWEN2_0_5B, tge_kv.KV_I8, [4096], steps=128, pool_pages=272,
-                     outlier_frac=0.01, seed=2,
+                     outlier_frac=0.01, fragmented=False, seed=2,
                      note="1 seq, int8+f16 scales, ctx 4096 + 128 steps, 1% outlier k channels x8"),
         "c3": Config("c3", QWEN2_1_5B, tge_kv.KV_F16, [512, 2048, 4096, 8192], steps=32,
                      pool_pages=1024, seed=3,
@@ -83,7 +84,7 @@ def configs():
                      note="2048-token prompt in 4 causal chunks of 512, f16, MFMA"),
         "c5": Config("c5", QWEN2_7B, tge_kv.KV_I8, c5_ctx, steps=32, n_new=4,
                      pool_pages=0, outlier_frac=0.01, churn_every=16, churn_sessions=8,
-                     churn_context=2048, seed=5,
+                     churn_context=2048, fragmented=False, seed=5,
                      note="64 sessions log-uniform 1k-32k, int8+f16 scales, 4-query verify, "
                           "churn 8 sessions / 16 steps"),
     }

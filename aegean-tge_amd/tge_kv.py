@@ -67,8 +67,9 @@ SIGNATURES = [
     ("tge_kv_pool_destroy", None, [_VP]),
     ("tge_kv_pool_layer", _I, [_VP, _I, C.POINTER(LayerView)]),
     ("tge_kv_pool_bytes", C.c_size_t, [_VP]),
-    ("tge_kv_k_index", _I, [_I, _I]),
-    ("tge_kv_v_index", _I, [_I, _I]),
+    ("tge_kv_k_index", _I, [_I, _I, _I]),
+    ("tge_kv_v_index", _I, [_I, _I, _I]),
+    ("tge_kv_scale_index", _I, [_I, _I, _I]),
     ("tge_batch_create", _I, [C.POINTER(_VP)]),
     ("tge_batch_destroy", None, [_VP]),
     ("tge_batch_plan", _I, [_VP, _VP, C.POINTER(BatchDesc), _VP]),

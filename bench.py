@@ -60,6 +60,8 @@ def parse():
     ap.add_argument("--no-cpu", dest="cpu", action="store_false")
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
     ap.add_argument("--only", default="", help="run one config key (c1..c5) and print it")
+    ap.add_argument("--fragment-c5", action="store_true",
+                    help="shuffle the c5 pool's free list before the sessions fill it")
     return ap.parse_args()
 
 
@@ -85,7 +87,8 @@ class DecodeBench:
         self.model = tk.Qwen2KvPath(sh.layers, sh.q_heads, sh.kv_heads, sh.head_dim,
                                     context=context, sequences=self.n_seq, pages=pages,
                                     fmt=cfg.fmt, scale_format=tk.SCALE_F16)
-        self.model.table().fragment(cfg.seed + 1000)
+        if cfg.fragmented:
+            self.model.table().fragment(cfg.seed + 1000)
         rng = np.random.default_rng(cfg.seed)
         self.rng = rng
         rows = self.n_seq * cfg.n_new
@@ -340,7 +343,9 @@ def main():
         print(json.dumps({args.only: others[args.only]}))
         return
     cfg = cfgs["c5"]
-    log(f"[bench] c5: {cfg.note}")
+    if args.fragment_c5:
+        cfg.fragmented = True
+    log(f"[bench] c5: {cfg.note}{' (fragmented pool)' if cfg.fragmented else ''}")
     bench = DecodeBench(tk, synth, cfg, args.warmup + args.steps)
     log(f"[bench] c5 filled {sum(cfg.contexts)} positions x {cfg.shape.layers} layers in "
         f"{bench.fill_s:.1f} s; pool {bench.pages} pages")
@@ -377,6 +382,7 @@ def main():
             "attn_launch_us": round(r["attn_launch_us"], 3),
             "append_launch_us": round(r["append_launch_us"], 3),
             "decode_work_items": r["work_items"], "max_splits": r["max_splits"],
+            "pool": "fragmented" if cfg.fragmented else "fresh (LIFO reuse after churn)",
         },
         "roofline": {
             "bound": "hbm",

@@ -79,8 +79,8 @@ const char* tge_backend_arch(void);
  *   K and V: 16 * head_dim elements (f16 bits or int8 codes)
  *   I8 only, K and V scales: 16 * head_dim/32 scales (f16 bits or fp32)
  * Element (token t, dim d) of a block sits at:
- *   K: tge_kv_k_index(t, d)      V: tge_kv_v_index(t, d)
- *   scale of (t, block b = d/32): b*16 + t
+ *   K: tge_kv_k_index(t, d, head_dim)      V: tge_kv_v_index(t, d, head_dim)
+ *   scale of (t, block b = d/32): tge_kv_scale_index(t, b, head_dim)
  * head_dim must be 64 or 128 (the configurations' head sizes).
  * ------------------------------------------------------------------------ */
 typedef struct tge_kv_pool tge_kv_pool;
@@ -110,9 +110,14 @@ int tge_kv_pool_layer(const tge_kv_pool* pool, int layer,
 /* Device bytes the pool holds. */
 size_t tge_kv_pool_bytes(const tge_kv_pool* pool);
 
-/* In-page element index of (token, dim) for K and V blocks. */
-int tge_kv_k_index(int token, int dim);
-int tge_kv_v_index(int token, int dim);
+/* In-page element index of (token, dim) for K and V blocks, and of the
+ * scale of (token, 32-dim block). With NP = head_dim/32:
+ *   K:     ((((d/4)&3)*16 + t)*NP + d/32)*8 + ((d/16)&1)*4 + (d&3)
+ *   V:     ((t/4*16 + (d&15))*NP + d/32)*8 + ((d/16)&1)*4 + (t&3)
+ *   scale: ((t/4)*NP + b)*4 + (t&3) */
+int tge_kv_k_index(int token, int dim, int head_dim);
+int tge_kv_v_index(int token, int dim, int head_dim);
+int tge_kv_scale_index(int token, int block, int head_dim);
 
 /* ---------------------------------------------------------------------------
  * Batch: the sessions one step works on. A plan is built once per step on the

@@ -65,17 +65,26 @@ def test_pool_argument_checks(tk):
 
 
 def test_page_layout_is_a_bijection(tk):
+    L = tk.lib()
     for hd in (64, 128):
-        ks = {tk.lib().tge_kv_k_index(t, d) for t in range(16) for d in range(hd)}
-        vs = {tk.lib().tge_kv_v_index(t, d) for t in range(16) for d in range(hd)}
+        np_ = hd // 32
+        ks = {L.tge_kv_k_index(t, d, hd) for t in range(16) for d in range(hd)}
+        vs = {L.tge_kv_v_index(t, d, hd) for t in range(16) for d in range(hd)}
+        ss = {L.tge_kv_scale_index(t, b, hd) for t in range(16) for b in range(np_)}
         assert ks == set(range(16 * hd)) and vs == set(range(16 * hd))
-    # operand contiguity: lane (g, t) of pair p reads 8 consecutive elements
-    for p in range(4):
+        assert ss == set(range(16 * np_))
+        # operand contiguity: lane (g, t) owns NP*8 consecutive K elements:
+        # per pair p, dims 32p+4g+e then 32p+16+4g+e
         for g in range(4):
             for t in range(16):
-                dims = [32 * p + 4 * g + e for e in range(4)] + [32 * p + 16 + 4 * g + e for e in range(4)]
-                idx = [tk.lib().tge_kv_k_index(t, d) for d in dims]
-                assert idx == list(range(idx[0], idx[0] + 8)) and idx[0] == ((p * 4 + g) * 16 + t) * 8
+                dims = [32 * p + 16 * h + 4 * g + e for p in range(np_) for h in range(2)
+                        for e in range(4)]
+                idx = [L.tge_kv_k_index(t, d, hd) for d in dims]
+                assert idx == list(range((g * 16 + t) * np_ * 8, (g * 16 + t + 1) * np_ * 8))
+                # and of V: tokens 4g..4g+3 of dims 32p+t (h=0), 32p+16+t (h=1)
+                vidx = [L.tge_kv_v_index(4 * g + e, 32 * p + 16 * h + t, hd) for p in range(np_)
+                        for h in range(2) for e in range(4)]
+                assert vidx == list(range((g * 16 + t) * np_ * 8, (g * 16 + t + 1) * np_ * 8))
 
 
 # ---------------------------------------------------------------------------

@@ -31,8 +31,9 @@ def raw_pool_rows(case, layer, s, count):
     vraw = tk.hip().download(view.v, np.empty(pages * case.kvh * blk, elem))
     t = np.arange(16)[:, None]
     d = np.arange(case.hd)[None, :]
-    kidx = ((((d >> 5) << 2) + ((d >> 2) & 3)) * 16 + t) * 8 + (((d >> 4) & 1) << 2) + (d & 3)
-    vidx = ((((d >> 5) << 2) + (t >> 2)) * 16 + (d & 15)) * 8 + (((d >> 4) & 1) << 2) + (t & 3)
+    n = case.hd // 32
+    kidx = ((((d >> 2) & 3) * 16 + t) * n + (d >> 5)) * 8 + (((d >> 4) & 1) << 2) + (d & 3)
+    vidx = (((t >> 2) * 16 + (d & 15)) * n + (d >> 5)) * 8 + (((d >> 4) & 1) << 2) + (t & 3)
     k = np.empty((count, case.kv_dim), elem)
     v = np.empty((count, case.kv_dim), elem)
     for pos0 in range(0, count, 16):
