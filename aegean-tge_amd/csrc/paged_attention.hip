@@ -94,10 +94,10 @@ struct PageRegs {
 
 // Buffer resources of one layer's K, V and scale arrays. Loads address a
 // page block with a wave-uniform byte offset (SGPR) plus the lane's fixed
-// chunk offset (VGPR), so fetching a page costs no per-lane address math;
-// offsets past the end of an array read zeros instead of faulting.
+// chunk offset (VGPR); offsets past the end of an array read zeros instead
+// of faulting.
 struct LayerRsrc {
-  __amdgpu_buffer_rsrc_t k, v, ks, vs;
+  __amdgpu_buffer_rsrc_t k, v;
 };
 
 __device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void* base, uint32_t bytes) {
@@ -105,33 +105,110 @@ __device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void* base, ui
                                            0x00020000);
 }
 
-template <int N>
-__device__ __forceinline__ void buffer_dwords(uint32_t (&dst)[N], __amdgpu_buffer_rsrc_t r,
-                                              int voff, int soff) {
-  static_assert(N % 4 == 0, "16-byte loads");
+typedef __attribute__((address_space(3))) void lds_void_t;
+typedef const __attribute__((address_space(1))) void global_void_t;
+typedef const __attribute__((address_space(4))) int sconst_int;  // scalar (constant) loads
+
+// Per-wave LDS ring of page slots filled by direct-to-LDS loads. A slot
+// holds the K and V chunks of every lane (piece i of lane l at
+// i*1024 + 16*l, the order the lane reads them back) and, for int8 pools,
+// the page block's K and V scales as stored.
+template <int FMT, bool SF32, int D>
+struct Ring {
+  using R = PageRegs<FMT, SF32, D>;
+  static constexpr int PIECES = R::KW / 4;                   // 16-byte pieces per lane
+  static constexpr int KV_BYTES = PIECES * 1024;             // one operand per slot
+  static constexpr int SC_BYTES = FMT == kI8 ? 16 * (D / 32) * (SF32 ? 4 : 2) : 0;
+  static constexpr int SC_LOADS = (2 * SC_BYTES + 255) / 256;  // dword loads: K then V scales
+  static constexpr int SLOT = 2 * KV_BYTES + 256 * SC_LOADS;
+  static constexpr int LOADS = 2 * PIECES + SC_LOADS;        // loads per page
+};
+
+// Waves per SIMD each variant is compiled for: the register budget that keeps
+// every live value in the 256 architectural VGPRs (no AGPR round trips on
+// the accumulators) while leaving room for a second wave to hide latency.
+template <int FMT, int D, int NRG, bool QSPLIT>
+constexpr int waves_per_eu() {
+  return D == 64 ? (NRG <= 2 ? 3 : 2) : (NRG <= 2 ? 2 : 1);
+}
+
+// Ring slots per wave: as many as the workgroups resident on a CU (one per
+// wave per SIMD) leave room for in the 160 KiB of LDS, between 2 and 4.
+// NB slots keep NB-1 pages in flight while the wave consumes one.
+template <int FMT, bool SF32, int D, int NRG, bool QSPLIT>
+constexpr int ring_slots() {
+  constexpr int budget = 160 * 1024 / waves_per_eu<FMT, D, NRG, QSPLIT>();
+  constexpr int n = budget / (kWaves * Ring<FMT, SF32, D>::SLOT);
+  return n < 2 ? 2 : (n > 4 ? 4 : n);
+}
+
+// Issue the direct-to-LDS loads of page block `blk` into `slot`.
+template <int FMT, bool SF32, int D>
+__device__ __forceinline__ void fetch_page(char* slot, const LayerRsrc& rs, const AttnParams& p,
+                                           int blk, int lane) {
+#if defined(__HIP_DEVICE_COMPILE__)  // the LDS-load builtins exist for the device pass only
+  using RG = Ring<FMT, SF32, D>;
+  const int kv_block = RG::KV_BYTES;  // bytes of one K (or V) page block
 #pragma unroll
-  for (int i = 0; i < N / 4; ++i) {
-    const u32x4_t x = __builtin_amdgcn_raw_buffer_load_b128(r, voff + 16 * i, soff, 0);
-    dst[4 * i] = x.x;
-    dst[4 * i + 1] = x.y;
-    dst[4 * i + 2] = x.z;
-    dst[4 * i + 3] = x.w;
+  for (int i = 0; i < RG::PIECES; ++i) {
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(rs.k, (lds_void_t*)(slot + i * 1024), 16,
+                                             lane * RG::PIECES * 16 + i * 16, blk * kv_block, 0, 0);
+  }
+#pragma unroll
+  for (int i = 0; i < RG::PIECES; ++i) {
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(rs.v, (lds_void_t*)(slot + RG::KV_BYTES + i * 1024), 16,
+                                             lane * RG::PIECES * 16 + i * 16, blk * kv_block, 0, 0);
+  }
+  if constexpr (FMT == kI8) {
+    // dword d of the slot's scale area (K scales then V scales)
+    char* sdst = slot + 2 * RG::KV_BYTES;
+#pragma unroll
+    for (int i = 0; i < RG::SC_LOADS; ++i) {
+      // dword d of [K scales | V scales]; lanes past the end re-read the
+      // first K scale dword into the slot's padding.
+      const int d = i * 64 + lane;
+      const int per = RG::SC_BYTES / 4;
+      const char* kb = static_cast<const char*>(p.kscale) + (size_t)blk * RG::SC_BYTES;
+      const char* vb = static_cast<const char*>(p.vscale) + (size_t)blk * RG::SC_BYTES;
+      const char* src = d < per ? kb + 4 * d : (d < 2 * per ? vb + 4 * (d - per) : kb);
+      __builtin_amdgcn_global_load_lds((global_void_t*)src, (lds_void_t*)(sdst + i * 256), 4, 0, 0);
+    }
+  }
+#endif
+}
+
+// Read a landed page back into registers (the lane's own chunk and its
+// group's scales).
+template <int FMT, bool SF32, int D>
+__device__ __forceinline__ void read_page(PageRegs<FMT, SF32, D>& r, const char* slot, int lane,
+                                          int grp) {
+  using RG = Ring<FMT, SF32, D>;
+  using R = PageRegs<FMT, SF32, D>;
+#pragma unroll
+  for (int i = 0; i < RG::PIECES; ++i) {
+    const u32x4_t k = *reinterpret_cast<const u32x4_t*>(slot + i * 1024 + 16 * lane);
+    const u32x4_t v = *reinterpret_cast<const u32x4_t*>(slot + RG::KV_BYTES + i * 1024 + 16 * lane);
+    r.k[4 * i] = k.x; r.k[4 * i + 1] = k.y; r.k[4 * i + 2] = k.z; r.k[4 * i + 3] = k.w;
+    r.v[4 * i] = v.x; r.v[4 * i + 1] = v.y; r.v[4 * i + 2] = v.z; r.v[4 * i + 3] = v.w;
+  }
+  if constexpr (FMT == kI8) {
+    const char* sk = slot + 2 * RG::KV_BYTES + grp * R::SW * 4;
+    const char* sv = sk + RG::SC_BYTES;
+#pragma unroll
+    for (int i = 0; i < R::SW / 4; ++i) {
+      const u32x4_t a = *reinterpret_cast<const u32x4_t*>(sk + 16 * i);
+      const u32x4_t b = *reinterpret_cast<const u32x4_t*>(sv + 16 * i);
+      r.ks[4 * i] = a.x; r.ks[4 * i + 1] = a.y; r.ks[4 * i + 2] = a.z; r.ks[4 * i + 3] = a.w;
+      r.vs[4 * i] = b.x; r.vs[4 * i + 1] = b.y; r.vs[4 * i + 2] = b.z; r.vs[4 * i + 3] = b.w;
+    }
   }
 }
 
-// Fetch page block `blk` (page * kv_heads + kv_head) into registers.
-template <int FMT, bool SF32, int D>
-__device__ __forceinline__ void load_page(PageRegs<FMT, SF32, D>& r, const LayerRsrc& rs, int blk,
-                                          int chunk, int grp) {
-  using R = PageRegs<FMT, SF32, D>;
-  const int kv_bytes = R::KW * 4 * 64;
-  buffer_dwords(r.k, rs.k, chunk * R::KW * 4, blk * kv_bytes);
-  buffer_dwords(r.v, rs.v, chunk * R::KW * 4, blk * kv_bytes);
-  if constexpr (FMT == kI8) {
-    const int sc_bytes = R::SW * 4 * 4;
-    buffer_dwords(r.ks, rs.ks, grp * R::SW * 4, blk * sc_bytes);
-    buffer_dwords(r.vs, rs.vs, grp * R::SW * 4, blk * sc_bytes);
-  }
+// s_waitcnt vmcnt(n) (other counters untouched), n <= 63.
+template <int N>
+__device__ __forceinline__ void wait_vmcnt() {
+  static_assert(N >= 0 && N < 64, "vmcnt range");
+  __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | (7 << 4) | (15 << 8));
 }
 
 // K operand (16x16x32 A) of 32-dim block pp.
@@ -167,9 +244,8 @@ struct Unit {
   static constexpr int NT = D / 16;
   using Regs = PageRegs<FMT, SF32, D>;
 
-  // Q^T operands in LDS: [rg][pp][hi/lo][lane] half8, one ds_read_b128 each
-  const half8_t* qs;
-  int lane;
+  half8_t qhi[NRG][NP];
+  half8_t qlo[NRG][NP];
   int lim[NRG];
   // Online softmax state per row, log2 domain. Scores are kept relative to
   // `base`; the weights exp2(s - base) never exceed 2^kLazyMax because base
@@ -180,7 +256,7 @@ struct Unit {
   float4_t o[NRG][NT];
 
   __device__ __forceinline__ half8_t qop(int rg, int pp, int part) const {
-    return qs[((rg * NP + pp) * 2 + part) * 64 + lane];
+    return part ? qlo[rg][pp] : qhi[rg][pp];
   }
 
   // One page: scores relative to base, online softmax, value accumulation.
@@ -272,83 +348,79 @@ struct Unit {
   }
 };
 
-template <int FMT, bool SF32, int D, int NRG, bool QSPLIT, int WPE>
-__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(WPE, WPE)))
-void paged_attention_kernel(AttnParams p) {
+// Workgroup LDS: the four waves' page rings; after the page loop the same
+// bytes hold the merge buffers.
+template <int FMT, bool SF32, int D, int NRG, bool QSPLIT>
+struct Shared {
+  static constexpr int ROWS = 16 * NRG;
+  static constexpr int OPAD = D + 4;
+  static constexpr int MERGE_BYTES = (2 * kWaves * ROWS + ROWS * OPAD) * 4;
+  static constexpr int RING_BYTES =
+      kWaves * ring_slots<FMT, SF32, D, NRG, QSPLIT>() * Ring<FMT, SF32, D>::SLOT;
+  static constexpr int BYTES = RING_BYTES > MERGE_BYTES ? RING_BYTES : MERGE_BYTES;
+  alignas(16) char raw[BYTES];
+};
+
+// One work item (unit) by the whole workgroup.
+template <int FMT, bool SF32, int D, int NRG, bool QSPLIT>
+__device__ __forceinline__ void attend_unit(const AttnParams& p, const WorkRec& w,
+                                            Shared<FMT, SF32, D, NRG, QSPLIT>& sh) {
   using U = Unit<FMT, SF32, D, NRG, QSPLIT>;
   using Regs = typename U::Regs;
+  using RG = Ring<FMT, SF32, D>;
   constexpr int NP = D / 32;
   constexpr int NT = D / 16;
   constexpr int ROWS = 16 * NRG;
   constexpr int OPAD = D + 4;
-
-  __shared__ float lds_m[kWaves][ROWS];
-  __shared__ float lds_l[kWaves][ROWS];
-  __shared__ float lds_o[ROWS * OPAD];
-  __shared__ half8_t lds_q[NRG * NP * 2 * 64];
+  constexpr int NB = ring_slots<FMT, SF32, D, NRG, QSPLIT>();
 
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int col = lane & 15;
   const int grp = lane >> 4;
-  const int chunk = grp * 16 + col;
 
-  const WorkRec w = p.work[blockIdx.x];
   const SessionRec s = p.sessions[w.session];
   const int q_stride = p.q_heads * D;
   const int geff = w.rows_per_query;
 
   U u;
-  u.lane = lane;
-  u.qs = lds_q;
   // Q^T operands: lane (g, c) of row group rg holds row c, dims
   // {32pp+4g+e, 32pp+16+4g+e} (the K operand's dim order), pre-multiplied by
   // log2(e)/sqrt(D) and split into f16 hi + lo.
-  for (int slot = threadIdx.x; slot < NRG * NP * 64; slot += 256) {
-    const int ln = slot & 63, pp = (slot >> 6) % NP, rg = (slot >> 6) / NP;
-    const int r = rg * 16 + (ln & 15), g = ln >> 4;
-    const bool valid = r < w.rows;
-    const int qi = w.row_begin + (valid ? r / geff : 0);
-    const int head = w.head_base + (valid ? r % geff : 0);
-    const float* qp = p.q + (size_t)(s.q_row + qi) * q_stride + (size_t)head * D + 4 * g + 32 * pp;
-    float4 a = make_float4(0, 0, 0, 0), b = make_float4(0, 0, 0, 0);
-    if (valid) {
-      a = *reinterpret_cast<const float4*>(qp);
-      b = *reinterpret_cast<const float4*>(qp + 16);
-    }
-    const float c = p.scale_log2;
-    const float x[8] = {a.x * c, a.y * c, a.z * c, a.w * c, b.x * c, b.y * c, b.z * c, b.w * c};
-    half8_t hi, lo;
-#pragma unroll
-    for (int j = 0; j < 8; ++j) {
-      hi[j] = (_Float16)x[j];
-      lo[j] = QSPLIT ? (_Float16)(x[j] - (float)hi[j]) : (_Float16)0.0f;
-    }
-    lds_q[((rg * NP + pp) * 2 + 0) * 64 + ln] = hi;
-    lds_q[((rg * NP + pp) * 2 + 1) * 64 + ln] = lo;
-  }
 #pragma unroll
   for (int rg = 0; rg < NRG; ++rg) {
     const int r = rg * 16 + col;
-    u.lim[rg] = r < w.rows ? s.ctx + w.row_begin + r / geff : -1;
+    const bool valid = r < w.rows;
+    const int qi = w.row_begin + (valid ? r / geff : 0);
+    const int head = w.head_base + (valid ? r % geff : 0);
+    const float* qp = p.q + (size_t)(s.q_row + qi) * q_stride + (size_t)head * D + 4 * grp;
+#pragma unroll
+    for (int pp = 0; pp < NP; ++pp) {
+      float4 a = make_float4(0, 0, 0, 0), b = make_float4(0, 0, 0, 0);
+      if (valid) {
+        a = *reinterpret_cast<const float4*>(qp + 32 * pp);
+        b = *reinterpret_cast<const float4*>(qp + 32 * pp + 16);
+      }
+      const float c = p.scale_log2;
+      const float x[8] = {a.x * c, a.y * c, a.z * c, a.w * c, b.x * c, b.y * c, b.z * c, b.w * c};
+#pragma unroll
+      for (int j = 0; j < 8; ++j) {
+        const _Float16 hi = (_Float16)x[j];
+        u.qhi[rg][pp][j] = hi;
+        u.qlo[rg][pp][j] = QSPLIT ? (_Float16)(x[j] - (float)hi) : (_Float16)0.0f;
+      }
+    }
+    u.lim[rg] = valid ? s.ctx + w.row_begin + r / geff : -1;
     u.base[rg] = 0.0f;
     u.thr[rg] = -INFINITY;
     u.l4[rg] = float4_t{0, 0, 0, 0};
 #pragma unroll
     for (int t = 0; t < NT; ++t) u.o[rg][t] = float4_t{0, 0, 0, 0};
   }
-  __syncthreads();
 
   LayerRsrc rs;
   rs.k = make_rsrc(p.kpool, p.kv_array_bytes);
   rs.v = make_rsrc(p.vpool, p.kv_array_bytes);
-  if constexpr (FMT == kI8) {
-    rs.ks = make_rsrc(p.kscale, p.scale_array_bytes);
-    rs.vs = make_rsrc(p.vscale, p.scale_array_bytes);
-  } else {
-    rs.ks = rs.k;
-    rs.vs = rs.v;
-  }
 
   // This wave's pages j = 0 .. mine-1 are pages page_begin + wave + 4j; the
   // first `clean` of them hold no position any row of the unit may not see.
@@ -363,34 +435,42 @@ void paged_attention_kernel(AttnParams p) {
     clean = (unmasked_pages - w.page_begin - wave + kWaves - 1) / kWaves;
     clean = clean < mine ? clean : mine;
   }
+  char* ring = sh.raw + wave * NB * RG::SLOT;
   if (mine > 0) {
-    // Page id of this wave's j-th page lives in lane j % 64 of `ids`.
-    auto fetch_ids = [&](int j0) {
-      const int j = j0 + lane;
-      return j < mine ? table[w.page_begin + wave + kWaves * j] : 0;
-    };
-    auto block_of = [&](int ids_reg, int j) {
-      return __builtin_amdgcn_readlane(ids_reg, j & 63) * p.kv_heads + w.kv_head;
-    };
-    int ids = fetch_ids(0);
-    // Two register sets in turn: page j+1 is in flight while page j is used.
-    Regs ra, rb;
-    load_page<FMT, SF32, D>(ra, rs, block_of(ids, 0), chunk, grp);
-    for (int j = 0; j < mine; j += 2) {
-      if (j + 1 < mine) {
-        if (((j + 1) & 63) == 0) ids = fetch_ids(j + 1);
-        load_page<FMT, SF32, D>(rb, rs, block_of(ids, j + 1), chunk, grp);
+    // Page ids come through the scalar cache (read-only constant loads), one
+    // page ahead of their use, so no vector-memory wait is tied to them.
+    const sconst_int* ids = (const sconst_int*)(table + w.page_begin + wave);
+    auto block_of = [&](int id) -> int { return id * p.kv_heads + w.kv_head; };
+#pragma unroll
+    for (int b = 0; b < NB - 1; ++b) {
+      if (b < mine) fetch_page<FMT, SF32, D>(ring + b * RG::SLOT, rs, p, block_of(ids[kWaves * b]), lane);
+    }
+    int id_next = NB - 1 < mine ? ids[kWaves * (NB - 1)] : 0;
+    int slot = 0;
+    for (int j = 0; j < mine; ++j) {
+      const int jn = j + NB - 1;
+      if (jn < mine) {
+        const int id = id_next;
+        id_next = jn + 1 < mine ? ids[kWaves * (jn + 1)] : 0;
+        int sn = slot + NB - 1;
+        sn = sn >= NB ? sn - NB : sn;
+        fetch_page<FMT, SF32, D>(ring + sn * RG::SLOT, rs, p, block_of(id), lane);
+        wait_vmcnt<(NB - 1) * RG::LOADS>();  // page j has landed
+      } else {
+        wait_vmcnt<0>();
       }
-      u.consume(ra, w.page_begin + wave + kWaves * j, grp, j >= clean);
-      if (j + 1 < mine) {
-        if (j + 2 < mine) {
-          if (((j + 2) & 63) == 0) ids = fetch_ids(j + 2);
-          load_page<FMT, SF32, D>(ra, rs, block_of(ids, j + 2), chunk, grp);
-        }
-        u.consume(rb, w.page_begin + wave + kWaves * (j + 1), grp, j + 1 >= clean);
-      }
+      Regs r;
+      read_page<FMT, SF32, D>(r, ring + slot * RG::SLOT, lane, grp);
+      u.consume(r, w.page_begin + wave + kWaves * j, grp, j >= clean);
+      slot = slot + 1 == NB ? 0 : slot + 1;
     }
   }
+
+  float* lds_base = reinterpret_cast<float*>(sh.raw);
+  float (*lds_m)[ROWS] = reinterpret_cast<float (*)[ROWS]>(lds_base);
+  float (*lds_l)[ROWS] = reinterpret_cast<float (*)[ROWS]>(lds_base + kWaves * ROWS);
+  float* lds_o = lds_base + 2 * kWaves * ROWS;
+  __syncthreads();  // every wave is done with its ring before it is reused
 
   // ---- merge the four waves (fixed order) and write --------------------
   // Each wave's state for a row is (base, l, o): o and l are sums of
@@ -461,6 +541,25 @@ void paged_attention_kernel(AttnParams p) {
   }
 }
 
+// The workgroup runs its work items in turn: items [first[g], first[g+1])
+// for workgroup g under a balanced schedule (every workgroup of the launch
+// gets the same number of pages), or item g alone when `first` is null.
+template <int FMT, bool SF32, int D, int NRG, bool QSPLIT, int WPE>
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(WPE, WPE)))
+void paged_attention_kernel(AttnParams p) {
+  __shared__ Shared<FMT, SF32, D, NRG, QSPLIT> sh;
+  int it = blockIdx.x, end = blockIdx.x + 1;
+  if (p.wg_first) {
+    it = p.wg_first[blockIdx.x];
+    end = p.wg_first[blockIdx.x + 1];
+  }
+  for (; it < end; ++it) {
+    const WorkRec w = p.work[it];
+    attend_unit<FMT, SF32, D, NRG, QSPLIT>(p, w, sh);
+    __syncthreads();  // LDS is reused by the next item
+  }
+}
+
 // Merge the partial states of the splits of one unit (merge_gqa_chunks:
 // splits with no visible position are skipped, none at all gives zeros).
 // One thread per (row, 4 dims), blockIdx.y selecting a 256-slot slice of
@@ -509,14 +608,6 @@ __global__ __launch_bounds__(256) void split_reduce_kernel(ReduceParams p) {
   }
 }
 
-// Waves per SIMD each variant is compiled for: the register budget that keeps
-// every live value in the 256 architectural VGPRs (no AGPR round trips on
-// the accumulators) while leaving room for a second wave to hide latency.
-template <int FMT, int D, int NRG, bool QSPLIT>
-constexpr int waves_per_eu() {
-  return D == 64 ? (NRG <= 2 ? 3 : 2) : (NRG <= 2 ? 2 : 1);
-}
-
 template <int FMT, bool SF32, int D, bool QSPLIT>
 hipError_t launch_rg(int row_groups, int n_work, const AttnParams& p, hipStream_t stream) {
   const dim3 grid((unsigned)n_work), block(256);
@@ -555,6 +646,35 @@ hipError_t launch_attention(int format, int scale_f32, int head_dim, int row_gro
   if (!qsplit) return hipErrorInvalidValue;
   return scale_f32 ? launch_d<kI8, true, true>(head_dim, row_groups, n_work, p, stream)
                    : launch_d<kI8, false, true>(head_dim, row_groups, n_work, p, stream);
+}
+
+template <int FMT, bool SF32, int D, bool QSPLIT>
+int blocks_rg(int row_groups) {
+  int n = 0;
+  hipError_t e = hipErrorInvalidValue;
+  switch (row_groups) {
+#define TGE_OCC(r)                                                                           \
+  case r:                                                                                    \
+    e = hipOccupancyMaxActiveBlocksPerMultiprocessor(                                        \
+        &n, paged_attention_kernel<FMT, SF32, D, r, QSPLIT, waves_per_eu<FMT, D, r, QSPLIT>()>, \
+        256, 0);                                                                             \
+    break;
+    TGE_OCC(1)
+    TGE_OCC(2)
+    TGE_OCC(3)
+    TGE_OCC(4)
+#undef TGE_OCC
+  }
+  return e == hipSuccess ? n : 0;
+}
+
+int attention_blocks_per_cu(int format, int scale_f32, int head_dim, int row_groups, bool qsplit) {
+  if (format == kF16) {
+    if (head_dim == 64) return qsplit ? blocks_rg<kF16, false, 64, true>(row_groups) : blocks_rg<kF16, false, 64, false>(row_groups);
+    return qsplit ? blocks_rg<kF16, false, 128, true>(row_groups) : blocks_rg<kF16, false, 128, false>(row_groups);
+  }
+  if (head_dim == 64) return scale_f32 ? blocks_rg<kI8, true, 64, true>(row_groups) : blocks_rg<kI8, false, 64, true>(row_groups);
+  return scale_f32 ? blocks_rg<kI8, true, 128, true>(row_groups) : blocks_rg<kI8, false, 128, true>(row_groups);
 }
 
 hipError_t launch_reduce(int head_dim, int n_items, const ReduceParams& p, hipStream_t stream) {

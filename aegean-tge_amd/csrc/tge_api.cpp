@@ -86,14 +86,17 @@ struct tge_kv_pool {
 struct AttnPlan {
   std::vector<tge::WorkRec> work;
   std::vector<tge::ReduceRec> reduce;
+  std::vector<int> wg_first;  // empty: one item per workgroup
+  int groups = 0;             // workgroups of the launch
   int row_groups = 1;
   int parts = 0;
   int max_splits = 0;
   bool built = false;
-  // device image: work | reduce
+  // device image: work | reduce | wg_first
   char* dev = nullptr;
   size_t dev_bytes = 0;
   size_t off_reduce = 0;
+  size_t off_first = 0;
   char* host = nullptr;
   size_t host_bytes = 0;
   hipEvent_t staged = nullptr;
@@ -263,17 +266,6 @@ void tge_batch_destroy(tge_batch* b) { delete b; }
 
 namespace {
 
-// Pages per decode unit: enough units to cover the 256 CUs several times
-// over, at least 8 pages (2 per wave) so a unit amortises its Q load and
-// merge, rounded to whole rounds of the 4 waves.
-int decode_pages_per_unit(long total_unit_pages) {
-  constexpr long kTargetUnits = 1024;
-  long pps = (total_unit_pages + kTargetUnits - 1) / kTargetUnits;
-  pps = std::max<long>(pps, 8);
-  pps = (pps + tge::kWaves - 1) / tge::kWaves * tge::kWaves;
-  return (int)pps;
-}
-
 // Splits [0, pages) into n nearly equal ranges and appends one unit each.
 void add_units(std::vector<tge::WorkRec>& work, std::vector<tge::ReduceRec>& red,
                int& parts, int& max_splits, tge::WorkRec base, int pages, int pps) {
@@ -341,13 +333,18 @@ int stage_upload(char*& host, size_t& host_bytes, char*& dev, size_t& dev_bytes,
 int upload_plan(AttnPlan& pl, int head_dim, hipStream_t st) {
   const size_t wbytes = pl.work.size() * sizeof(tge::WorkRec);
   pl.off_reduce = align256(wbytes);
-  const size_t total = pl.off_reduce + pl.reduce.size() * sizeof(tge::ReduceRec);
+  pl.off_first = align256(pl.off_reduce + pl.reduce.size() * sizeof(tge::ReduceRec));
+  const size_t total = pl.off_first + pl.wg_first.size() * sizeof(int);
+  if (pl.groups == 0) pl.groups = (int)pl.work.size();
   int s = stage_upload(pl.host, pl.host_bytes, pl.dev, pl.dev_bytes, pl.staged, total, st,
                        [&](char* h) {
                          if (wbytes) std::memcpy(h, pl.work.data(), wbytes);
                          if (!pl.reduce.empty())
                            std::memcpy(h + pl.off_reduce, pl.reduce.data(),
                                        pl.reduce.size() * sizeof(tge::ReduceRec));
+                         if (!pl.wg_first.empty())
+                           std::memcpy(h + pl.off_first, pl.wg_first.data(),
+                                       pl.wg_first.size() * sizeof(int));
                        });
   if (s != TGE_OK) return s;
   const size_t rows_cap = 16 * (size_t)pl.row_groups;
@@ -367,29 +364,89 @@ int upload_plan(AttnPlan& pl, int head_dim, hipStream_t st) {
   return TGE_OK;
 }
 
-void build_decode(tge_batch* b) {
+// Resident workgroups of an attention variant on this device (cached).
+int resident_groups(int format, int scale_f32, int head_dim, int row_groups, bool qsplit) {
+  static std::mutex mu;
+  static std::vector<std::pair<int, int>> cache;  // key -> groups
+  const int key = (((format * 2 + scale_f32) * 256 + head_dim) * 8 + row_groups) * 2 + qsplit;
+  std::lock_guard<std::mutex> lock(mu);
+  for (const auto& kv : cache)
+    if (kv.first == key) return kv.second;
+  int dev = 0, cus = 0;
+  if (hipGetDevice(&dev) != hipSuccess ||
+      hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess)
+    cus = 256;
+  int per_cu = tge::attention_blocks_per_cu(format, scale_f32, head_dim, row_groups, qsplit);
+  if (per_cu <= 0) per_cu = 1;
+  const int groups = per_cu * cus;
+  cache.emplace_back(key, groups);
+  return groups;
+}
+
+// Decode schedule. Every (session, kv head) is a segment of pages whose rows
+// are the GQA group of each new token. The segments are laid end to end and
+// cut into one equal share of pages per resident workgroup, so all
+// workgroups of the launch finish together; a segment cut into several
+// items is merged by the split reduction.
+void build_decode(tge_batch* b, int groups) {
   AttnPlan& pl = b->decode;
   pl.work.clear();
   pl.reduce.clear();
+  pl.wg_first.clear();
   pl.parts = pl.max_splits = 0;
   pl.row_groups = std::max(1, std::min(4, (b->max_rows + 15) / 16));
-  long unit_pages = 0;
-  for (const auto& sr : b->sessions) unit_pages += (long)((sr.ctx + sr.n_new + 15) / 16) * b->kv_heads;
-  const int pps = decode_pages_per_unit(unit_pages);
+  long total = 0;
+  for (const auto& sr : b->sessions) total += (long)((sr.ctx + sr.n_new + 15) / 16) * b->kv_heads;
+  // At least 8 pages (two per wave) per workgroup.
+  const long g_eff = std::max<long>(1, std::min<long>(groups, (total + 7) / 8));
+  const long share = (total + g_eff - 1) / g_eff;
+  long room = share;
+  pl.wg_first.push_back(0);
   for (int s = 0; s < (int)b->sessions.size(); ++s) {
     const tge::SessionRec& sr = b->sessions[s];
     const int pages = (sr.ctx + sr.n_new + 15) / 16;
     for (int h = 0; h < b->kv_heads; ++h) {
-      tge::WorkRec w{};
-      w.session = s;
-      w.kv_head = h;
-      w.row_begin = 0;
-      w.rows = sr.n_new * b->group;
-      w.rows_per_query = b->group;
-      w.head_base = h * b->group;
-      add_units(pl.work, pl.reduce, pl.parts, pl.max_splits, w, pages, pps);
+      tge::WorkRec base{};
+      base.session = s;
+      base.kv_head = h;
+      base.row_begin = 0;
+      base.rows = sr.n_new * b->group;
+      base.rows_per_query = b->group;
+      base.head_base = h * b->group;
+      const int first_item = (int)pl.work.size();
+      for (int pos = 0; pos < pages;) {
+        const int take = (int)std::min<long>(room, pages - pos);
+        tge::WorkRec w = base;
+        w.page_begin = pos;
+        w.page_end = pos + take;
+        pl.work.push_back(w);
+        pos += take;
+        room -= take;
+        if (room == 0) {
+          pl.wg_first.push_back((int)pl.work.size());
+          room = share;
+        }
+      }
+      const int n = (int)pl.work.size() - first_item;
+      pl.max_splits = std::max(pl.max_splits, n);
+      if (n == 1) {
+        pl.work[first_item].part = -1;
+      } else {
+        tge::ReduceRec r{};
+        r.session = s;
+        r.row_begin = 0;
+        r.rows = base.rows;
+        r.rows_per_query = base.rows_per_query;
+        r.head_base = base.head_base;
+        r.first_part = pl.parts;
+        r.n_parts = n;
+        for (int i = first_item; i < first_item + n; ++i) pl.work[i].part = pl.parts++;
+        pl.reduce.push_back(r);
+      }
     }
   }
+  if (pl.wg_first.back() != (int)pl.work.size()) pl.wg_first.push_back((int)pl.work.size());
+  pl.groups = (int)pl.wg_first.size() - 1;
 }
 
 // Prefill units: (session, query head, 32-query tile) x splits of 64 pages.
@@ -397,6 +454,8 @@ void build_prefill(tge_batch* b) {
   AttnPlan& pl = b->prefill;
   pl.work.clear();
   pl.reduce.clear();
+  pl.wg_first.clear();
+  pl.groups = 0;
   pl.parts = pl.max_splits = 0;
   pl.row_groups = 2;
   const int tile = 16 * pl.row_groups;
@@ -500,7 +559,9 @@ int tge_batch_plan(tge_batch* b, const tge_kv_pool* pool, const tge_batch_desc* 
   // Decode lists are built eagerly when the rows fit a decode unit (the
   // common case: one upload per step serves every layer).
   if (max_rows <= tge::kMaxRows) {
-    build_decode(b);
+    const int rg = std::max(1, std::min(4, (max_rows + 15) / 16));
+    build_decode(b, resident_groups(pool->desc.format, pool->desc.scale_format == TGE_SCALE_F32,
+                                    hd, rg, true));
     s = upload_plan(b->decode, hd, st);
     if (s != TGE_OK) return s;
   }
@@ -512,6 +573,7 @@ int tge_batch_info(const tge_batch* b, int* rows, int* work_items, int* max_spli
   if (!b || !b->planned) return fail(TGE_ERR_INVALID, "batch_info: batch not planned");
   if (rows) *rows = (int)b->rows.size();
   if (work_items) *work_items = (int)b->decode.work.size();
+  // (workgroups of the decode launch: b->decode.groups)
   if (max_splits) *max_splits = b->decode.max_splits;
   return TGE_OK;
 }
@@ -542,6 +604,7 @@ tge::AttnParams attn_params(const tge_batch* b, const tge_kv_pool* p, int layer,
   a.scale_array_bytes = (uint32_t)(p->scale_block_bytes * p->layer_blocks);
   a.sessions = reinterpret_cast<const tge::SessionRec*>(b->dev + b->off_sessions);
   a.work = reinterpret_cast<const tge::WorkRec*>(pl.dev);
+  a.wg_first = pl.wg_first.empty() ? nullptr : reinterpret_cast<const int*>(pl.dev + pl.off_first);
   a.tables = reinterpret_cast<const int*>(b->dev + b->off_tables);
   a.q = q;
   a.out = out;
@@ -559,7 +622,7 @@ int run_attention(const tge_batch* b, const tge_kv_pool* p, int layer, const flo
   hipStream_t st = static_cast<hipStream_t>(stream);
   const tge::AttnParams a = attn_params(b, p, layer, q, out, pl);
   TGE_HIP(tge::launch_attention(p->desc.format, p->desc.scale_format == TGE_SCALE_F32,
-                                b->head_dim, pl.row_groups, qsplit, (int)pl.work.size(), a, st));
+                                b->head_dim, pl.row_groups, qsplit, pl.groups, a, st));
   if (!pl.reduce.empty()) {
     tge::ReduceParams r{};
     r.sessions = a.sessions;

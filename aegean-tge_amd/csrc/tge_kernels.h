@@ -47,6 +47,7 @@ struct AttnParams {
   const void* vscale;
   const SessionRec* sessions;
   const WorkRec* work;
+  const int* wg_first;  // [grid+1] first work item of each workgroup, or null
   const int* tables;
   const float* q;
   float* out;
@@ -71,10 +72,14 @@ struct ReduceParams {
 hipError_t launch_kv_append(int format, const AppendParams& p, hipStream_t stream);
 hipError_t launch_kv_gather(int format, const GatherParams& p, hipStream_t stream);
 // row_groups: 16-row groups per unit (1..4). qsplit: Q as f16 hi + lo.
+// n_groups workgroups; with p.wg_first set each runs a range of the items.
 hipError_t launch_attention(int format, int scale_f32, int head_dim, int row_groups,
-                            bool qsplit, int n_work, const AttnParams& p,
+                            bool qsplit, int n_groups, const AttnParams& p,
                             hipStream_t stream);
 hipError_t launch_reduce(int head_dim, int n_items, const ReduceParams& p,
                          hipStream_t stream);
+// Resident 256-thread workgroups per CU of one attention variant (0 if the
+// query fails).
+int attention_blocks_per_cu(int format, int scale_f32, int head_dim, int row_groups, bool qsplit);
 
 }  // namespace tge
