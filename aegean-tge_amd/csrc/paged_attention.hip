@@ -562,50 +562,93 @@ void paged_attention_kernel(AttnParams p) {
 
 // Merge the partial states of the splits of one unit (merge_gqa_chunks:
 // splits with no visible position are skipped, none at all gives zeros).
-// One thread per (row, 4 dims), blockIdx.y selecting a 256-slot slice of
-// the item's rows; the split states are read in batches of 8 independent
-// loads.
-template <int D>
+// A row's D/4 lanes (4 dims each) are replicated over S slots; slot j folds
+// splits j, j+S, ... (loads issued in batches of 8) into a running
+// (max, sum, acc) state, and slot 0 combines the S states in slot order, so
+// the result does not depend on timing. Rows per block = 256 / (D/4 * S).
+template <int D, int S>
 __global__ __launch_bounds__(256) void split_reduce_kernel(ReduceParams p) {
+  constexpr int L = D / 4;
+  constexpr int RPB = 256 / (L * S);
+  static_assert(RPB >= 1 && RPB * L * S == 256, "block shape");
+  __shared__ float sh_m[RPB][S];
+  __shared__ float sh_l[RPB][S];
+  __shared__ float4_t sh_o[RPB][S][L];
+
   const ReduceRec it = p.items[blockIdx.x];
-  const SessionRec s = p.sessions[it.session];
-  const int q_stride = p.q_heads * D;
-  {
-    const int idx = blockIdx.y * 256 + threadIdx.x;
-    if (idx >= it.rows * (D / 4)) return;
-    const int r = idx / (D / 4);
-    const int d4 = idx % (D / 4);
+  const int t = threadIdx.x;
+  const int d4 = t % L;
+  const int slot = (t / L) % S;
+  const int rr = t / (L * S);
+  const int r = blockIdx.y * RPB + rr;
+  const bool active = r < it.rows;
+
+  float m = -INFINITY, sum = 0.0f;
+  float4_t acc = float4_t{0, 0, 0, 0};
+  if (active) {
     const float2* ml = reinterpret_cast<const float2*>(p.part_ml) + (size_t)it.first_part * p.rows_cap + r;
     const float* po = p.part_o + ((size_t)it.first_part * p.rows_cap + r) * D + 4 * d4;
     const size_t stride_ml = p.rows_cap;
     const size_t stride_o = (size_t)p.rows_cap * D;
-    float mm = -INFINITY;
-    for (int k = 0; k < it.n_parts; ++k) {
-      const float2 x = ml[k * stride_ml];
-      if (x.y > 0.0f) mm = fmaxf(mm, x.x);
-    }
-    float sum = 0.0f;
-    float4_t acc = float4_t{0, 0, 0, 0};
-    for (int k0 = 0; k0 < it.n_parts; k0 += 8) {
+    for (int k0 = slot; k0 < it.n_parts; k0 += 8 * S) {
+      float2 x[8];
       float4_t v[8];
-      float f[8];
 #pragma unroll
-      for (int k = 0; k < 8; ++k) {
-        const bool ok = k0 + k < it.n_parts;
-        const float2 x = ok ? ml[(k0 + k) * stride_ml] : make_float2(0.0f, 0.0f);
-        f[k] = x.y > 0.0f ? __builtin_amdgcn_exp2f(x.x - mm) : 0.0f;
-        sum += x.y * f[k];
-        v[k] = ok ? *reinterpret_cast<const float4_t*>(po + (k0 + k) * stride_o) : float4_t{0, 0, 0, 0};
+      for (int i = 0; i < 8; ++i) {
+        const int k = k0 + S * i;
+        const bool ok = k < it.n_parts;
+        x[i] = ok ? ml[k * stride_ml] : make_float2(-INFINITY, 0.0f);
+        v[i] = ok ? *reinterpret_cast<const float4_t*>(po + k * stride_o) : float4_t{0, 0, 0, 0};
       }
+      float bm = m;
 #pragma unroll
-      for (int k = 0; k < 8; ++k) acc += v[k] * f[k];
+      for (int i = 0; i < 8; ++i)
+        if (x[i].y > 0.0f) bm = fmaxf(bm, x[i].x);
+      if (bm == -INFINITY) continue;  // nothing visible in this batch yet
+      const float c = m == -INFINITY ? 0.0f : __builtin_amdgcn_exp2f(m - bm);
+      sum *= c;
+      acc *= c;
+#pragma unroll
+      for (int i = 0; i < 8; ++i) {
+        const float f = x[i].y > 0.0f ? __builtin_amdgcn_exp2f(x[i].x - bm) : 0.0f;
+        sum += x[i].y * f;
+        acc += v[i] * f;
+      }
+      m = bm;
     }
-    const int qi = it.row_begin + r / it.rows_per_query;
-    const int head = it.head_base + r % it.rows_per_query;
-    float4_t res = float4_t{0, 0, 0, 0};
-    if (sum > 0.0f) res = acc * (1.0f / sum);
-    *reinterpret_cast<float4_t*>(p.out + (size_t)(s.q_row + qi) * q_stride + (size_t)head * D + 4 * d4) = res;
   }
+  if constexpr (S > 1) {
+    sh_o[rr][slot][d4] = acc;
+    if (d4 == 0) {
+      sh_m[rr][slot] = m;
+      sh_l[rr][slot] = sum;
+    }
+    __syncthreads();
+    if (slot != 0 || !active) return;
+    float mm = -INFINITY;
+#pragma unroll
+    for (int j = 0; j < S; ++j) mm = fmaxf(mm, sh_m[rr][j]);
+    sum = 0.0f;
+    acc = float4_t{0, 0, 0, 0};
+    if (mm != -INFINITY) {
+#pragma unroll
+      for (int j = 0; j < S; ++j) {
+        const float mj = sh_m[rr][j];
+        const float f = mj == -INFINITY ? 0.0f : __builtin_amdgcn_exp2f(mj - mm);
+        sum += sh_l[rr][j] * f;
+        acc += sh_o[rr][j][d4] * f;
+      }
+    }
+  } else {
+    if (!active) return;
+  }
+  const SessionRec s = p.sessions[it.session];
+  const int q_stride = p.q_heads * D;
+  const int qi = it.row_begin + r / it.rows_per_query;
+  const int head = it.head_base + r % it.rows_per_query;
+  float4_t res = float4_t{0, 0, 0, 0};
+  if (sum > 0.0f) res = acc * (1.0f / sum);
+  *reinterpret_cast<float4_t*>(p.out + (size_t)(s.q_row + qi) * q_stride + (size_t)head * D + 4 * d4) = res;
 }
 
 template <int FMT, bool SF32, int D, bool QSPLIT>
@@ -677,17 +720,29 @@ int attention_blocks_per_cu(int format, int scale_f32, int head_dim, int row_gro
   return scale_f32 ? blocks_rg<kI8, true, 128, true>(row_groups) : blocks_rg<kI8, false, 128, true>(row_groups);
 }
 
-hipError_t launch_reduce(int head_dim, int n_items, const ReduceParams& p, hipStream_t stream) {
-  if (n_items == 0) return hipSuccess;
-  const dim3 grid((unsigned)n_items, (unsigned)((p.rows_cap * head_dim / 4 + 255) / 256)), block(256);
-  if (head_dim == 64) {
-    hipLaunchKernelGGL(split_reduce_kernel<64>, grid, block, 0, stream, p);
-  } else if (head_dim == 128) {
-    hipLaunchKernelGGL(split_reduce_kernel<128>, grid, block, 0, stream, p);
-  } else {
-    return hipErrorInvalidValue;
+template <int D>
+hipError_t launch_reduce_d(int n_items, int max_parts, const ReduceParams& p, hipStream_t stream) {
+  // Slots per row: about one per 4 splits, at most 8.
+  const int want = (max_parts + 3) / 4;
+  const int slots = want <= 1 ? 1 : (want <= 2 ? 2 : (want <= 4 ? 4 : 8));
+  const int rpb = 256 / (D / 4 * slots);
+  const dim3 grid((unsigned)n_items, (unsigned)((p.rows_cap + rpb - 1) / rpb)), block(256);
+  switch (slots) {
+    case 1: hipLaunchKernelGGL((split_reduce_kernel<D, 1>), grid, block, 0, stream, p); break;
+    case 2: hipLaunchKernelGGL((split_reduce_kernel<D, 2>), grid, block, 0, stream, p); break;
+    case 4: hipLaunchKernelGGL((split_reduce_kernel<D, 4>), grid, block, 0, stream, p); break;
+    default: hipLaunchKernelGGL((split_reduce_kernel<D, 8>), grid, block, 0, stream, p); break;
   }
   return hipGetLastError();
 }
+
+hipError_t launch_reduce(int head_dim, int n_items, int max_parts, const ReduceParams& p,
+                         hipStream_t stream) {
+  if (n_items == 0) return hipSuccess;
+  if (head_dim == 64) return launch_reduce_d<64>(n_items, max_parts, p, stream);
+  if (head_dim == 128) return launch_reduce_d<128>(n_items, max_parts, p, stream);
+  return hipErrorInvalidValue;
+}
+
 
 }  // namespace tge

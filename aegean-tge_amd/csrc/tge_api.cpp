@@ -12,6 +12,7 @@
 #include <mutex>
 #include <stdexcept>
 #include <string>
+#include <array>
 #include <vector>
 
 #include "tge_common.h"
@@ -131,10 +132,20 @@ struct tge_batch {
   hipEvent_t staged = nullptr;
   size_t off_sessions = 0, off_tables = 0, off_rows = 0;
 
+  // Kernel timing (tge_batch_set_profiling): per attention call since
+  // enabling, events before the attention kernel, between it and the merge,
+  // and after the merge. Triples are created on demand and reused.
+  bool profiling = false;
+  std::vector<std::array<hipEvent_t, 3>> prof;
+  size_t prof_used = 0;
+
   ~tge_batch() {
     if (dev) (void)hipFree(dev);
     if (host) (void)hipHostFree(host);
     if (staged) (void)hipEventDestroy(staged);
+    for (auto& t : prof)
+      for (hipEvent_t e : t)
+        if (e) (void)hipEventDestroy(e);
   }
 };
 
@@ -578,6 +589,33 @@ int tge_batch_info(const tge_batch* b, int* rows, int* work_items, int* max_spli
   return TGE_OK;
 }
 
+int tge_batch_set_profiling(tge_batch* b, int enable) {
+  if (!b) return fail(TGE_ERR_INVALID, "batch_set_profiling: null batch");
+  b->profiling = enable != 0;
+  b->prof_used = 0;
+  return TGE_OK;
+}
+
+int tge_batch_kernel_times(const tge_batch* b, int* calls, float* attention_us,
+                           float* merge_us) {
+  if (!b || !calls || !attention_us || !merge_us)
+    return fail(TGE_ERR_INVALID, "batch_kernel_times: null argument");
+  double att = 0.0, mrg = 0.0;
+  for (size_t i = 0; i < b->prof_used; ++i) {
+    const auto& t = b->prof[i];
+    TGE_HIP(hipEventSynchronize(t[2]));
+    float x = 0.0f, y = 0.0f;
+    TGE_HIP(hipEventElapsedTime(&x, t[0], t[1]));
+    TGE_HIP(hipEventElapsedTime(&y, t[1], t[2]));
+    att += x;
+    mrg += y;
+  }
+  *calls = (int)b->prof_used;
+  *attention_us = (float)(1e3 * att);
+  *merge_us = (float)(1e3 * mrg);
+  return TGE_OK;
+}
+
 namespace {
 
 int check_use(const tge_batch* b, const tge_kv_pool* p, int layer, const char* who) {
@@ -621,8 +659,27 @@ int run_attention(const tge_batch* b, const tge_kv_pool* p, int layer, const flo
                   float* out, void* stream, const AttnPlan& pl, bool qsplit) {
   hipStream_t st = static_cast<hipStream_t>(stream);
   const tge::AttnParams a = attn_params(b, p, layer, q, out, pl);
+  std::array<hipEvent_t, 3>* ev = nullptr;
+  if (b->profiling) {
+    tge_batch* mb = const_cast<tge_batch*>(b);
+    if (mb->prof_used == mb->prof.size()) {
+      std::array<hipEvent_t, 3> t{nullptr, nullptr, nullptr};
+      for (hipEvent_t& e : t) {
+        const hipError_t err = hipEventCreate(&e);
+        if (err != hipSuccess) {
+          for (hipEvent_t x : t)
+            if (x) (void)hipEventDestroy(x);
+          return fail(TGE_ERR_DEVICE, std::string("hipEventCreate: ") + hipGetErrorString(err));
+        }
+      }
+      mb->prof.push_back(t);
+    }
+    ev = &mb->prof[mb->prof_used++];
+    TGE_HIP(hipEventRecord((*ev)[0], st));
+  }
   TGE_HIP(tge::launch_attention(p->desc.format, p->desc.scale_format == TGE_SCALE_F32,
                                 b->head_dim, pl.row_groups, qsplit, pl.groups, a, st));
+  if (ev) TGE_HIP(hipEventRecord((*ev)[1], st));
   if (!pl.reduce.empty()) {
     tge::ReduceParams r{};
     r.sessions = a.sessions;
@@ -632,8 +689,9 @@ int run_attention(const tge_batch* b, const tge_kv_pool* p, int layer, const flo
     r.out = out;
     r.rows_cap = a.rows_cap;
     r.q_heads = b->q_heads;
-    TGE_HIP(tge::launch_reduce(b->head_dim, (int)pl.reduce.size(), r, st));
+    TGE_HIP(tge::launch_reduce(b->head_dim, (int)pl.reduce.size(), pl.max_splits, r, st));
   }
+  if (ev) TGE_HIP(hipEventRecord((*ev)[2], st));
   return TGE_OK;
 }
 

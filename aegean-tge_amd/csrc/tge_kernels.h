@@ -76,7 +76,7 @@ hipError_t launch_kv_gather(int format, const GatherParams& p, hipStream_t strea
 hipError_t launch_attention(int format, int scale_f32, int head_dim, int row_groups,
                             bool qsplit, int n_groups, const AttnParams& p,
                             hipStream_t stream);
-hipError_t launch_reduce(int head_dim, int n_items, const ReduceParams& p,
+hipError_t launch_reduce(int head_dim, int n_items, int max_parts, const ReduceParams& p,
                          hipStream_t stream);
 // Resident 256-thread workgroups per CU of one attention variant (0 if the
 // query fails).

@@ -74,6 +74,8 @@ SIGNATURES = [
     ("tge_batch_destroy", None, [_VP]),
     ("tge_batch_plan", _I, [_VP, _VP, C.POINTER(BatchDesc), _VP]),
     ("tge_batch_info", _I, [_VP, _PI, _PI, _PI]),
+    ("tge_batch_set_profiling", _I, [_VP, _I]),
+    ("tge_batch_kernel_times", _I, [_VP, _PI, C.POINTER(C.c_float), C.POINTER(C.c_float)]),
     ("tge_kv_append", _I, [_VP, _VP, _I, _VP, _VP, _VP]),
     ("tge_decode_attention", _I, [_VP, _VP, _I, _VP, _VP, _VP]),
     ("tge_prefill_attention", _I, [_VP, _VP, _I, _VP, _VP, _VP]),
@@ -412,6 +414,17 @@ class Batch:
 
     def info(self):
         return batch_info(self.h)
+
+    def set_profiling(self, enable):
+        check(lib().tge_batch_set_profiling(self.h, int(bool(enable))), "batch_set_profiling")
+
+    def kernel_times(self):
+        """(calls, attention kernel us, merge kernel us) summed over the
+        attention calls since profiling was enabled."""
+        n, a, m = C.c_int(), C.c_float(), C.c_float()
+        check(lib().tge_batch_kernel_times(self.h, C.byref(n), C.byref(a), C.byref(m)),
+              "batch_kernel_times")
+        return n.value, a.value, m.value
 
     def append(self, pool, layer, k, v, stream=None):
         check(lib().tge_kv_append(self.h, pool.h, layer, k.ptr, v.ptr, stream), "kv_append")

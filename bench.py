@@ -13,9 +13,11 @@ reduction), through the product's Qwen2 KV driver.
 
 value = algorithmic bytes (append + attention, per the formulas in
 synth.algorithmic_bytes_*) of the timed steps / their wall time, GB/s.
-roofline = the decode-attention launch (paged attention + split reduce) of the
-last step replayed over all layers, timed with HIP events on the launch
-stream. cpu_baseline = the reference's own AVX2 attention kernel
+roofline = the paged attention kernel alone (the dominant kernel; the split
+merge kernel is timed beside it): the last step's decode attention replayed
+over all layers, each kernel bracketed by HIP events that the library records
+on the launch stream (tge_batch_set_profiling). traffic = HBM bytes per
+dispatch from the committed rocprofv3 counter summary for this workload. cpu_baseline = the reference's own AVX2 attention kernel
 (oracle/_ref, built from the reference sources) under the reference's
 forward_batch schedule, on a bounded sample of the same workload.
 The other four configurations are measured briefly and reported under
@@ -40,6 +42,9 @@ for sub in ("aegean-tge_amd", "oracle"):
 
 HBM_PEAK_GBS = 8000.0       # MI355X HBM3E
 MFMA_F16_PEAK_TFLOPS = 2500.0  # dense f16/bf16
+WORKLOAD_C5 = ("c5: Qwen2-7B-shaped serving stress, 64 sessions, log-uniform 1k-32k "
+               "contexts, int8 KV + f16 scales, 16-token pages, 4-query verify "
+               "decode, churn 8 sessions / 16 steps")
 METRIC = ("paged-KV decode attention: achieved HBM GB/s (% of peak), "
           "µs per layer-step")
 
@@ -60,6 +65,8 @@ def parse():
     ap.add_argument("--no-cpu", dest="cpu", action="store_false")
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
     ap.add_argument("--only", default="", help="run one config key (c1..c5) and print it")
+    ap.add_argument("--calibrate-copy", action="store_true",
+                    help="only time 1 GiB device-to-device copies (counter calibration)")
     ap.add_argument("--fragment-c5", action="store_true",
                     help="shuffle the c5 pool's free list before the sessions fill it")
     return ap.parse_args()
@@ -169,6 +176,17 @@ class DecodeBench:
         lib = tk.lib()
         pool, batch = self.model.pool_handle(), self.model.batch_handle()
         L = self.sh.layers
+        # Per-kernel durations (paged attention kernel alone, split merge
+        # alone) from the library's timing events, calls issued back to back.
+        tk.check(lib.tge_batch_set_profiling(batch, 1))
+        for _ in range(replay):
+            for layer in range(L):
+                tk.check(lib.tge_decode_attention(batch, pool, layer, self.q.ptr, self.out.ptr, None))
+        n_calls, a_us, mg_us = C.c_int(), C.c_float(), C.c_float()
+        tk.check(lib.tge_batch_kernel_times(batch, C.byref(n_calls), C.byref(a_us), C.byref(mg_us)))
+        tk.check(lib.tge_batch_set_profiling(batch, 0))
+        k_us = [a_us.value / n_calls.value]
+        m_us = [mg_us.value / n_calls.value]
         e0, e1, e2 = hip.event(), hip.event(), hip.event()
         hip.record(e0)
         for _ in range(replay):
@@ -190,8 +208,11 @@ class DecodeBench:
             "gbs": total_bytes / step_s / 1e9,
             "tokens_per_s": self.rows * steps / step_s,
             "attn_launch_us": att_ms * 1e3,
+            "attn_kernel_us": float(np.mean(k_us)),
+            "merge_kernel_us": float(np.mean(m_us)),
             "attn_bytes_per_launch": att_b,
             "attn_gbs": att_b / (att_ms * 1e-3) / 1e9,
+            "attn_kernel_gbs": att_b / (float(np.mean(k_us)) * 1e-6) / 1e9,
             "append_launch_us": app_ms * 1e3,
             "append_bytes_per_launch": app_b,
             "append_gbs": app_b / (app_ms * 1e-3) / 1e9,
@@ -312,8 +333,48 @@ def cpu_baseline_c5(synth, cfg, seconds):
     }
 
 
+def measured_traffic(workload):
+    """HBM bytes per dispatch of the paged attention kernel on this workload,
+    from the committed rocprofv3 counter summary (FETCH_SIZE and WRITE_SIZE
+    per dispatch, each scaled by what the counter reads for a copy of known
+    size), or None when no summary covers the workload."""
+    path = os.path.join(ROOT, "profiles", "decode_attention_c5_traffic.json")
+    if not os.path.exists(path):
+        return None
+    with open(path) as f:
+        t = json.load(f)
+    if t.get("workload") != workload:
+        return None
+    return t.get("traffic_bytes_per_dispatch")
+
+
+def calibrate_copy(nbytes=1 << 30, reps=3):
+    """Device-to-device copies of a known size: the reference point that
+    scales FETCH_SIZE / WRITE_SIZE readings to bytes (run under rocprofv3)."""
+    import tge_kv as tk
+    tk.require_gpu()
+    hip = tk.hip()
+    src, dst = hip.malloc(nbytes), hip.malloc(nbytes)
+    hip.memset(src, 1, nbytes)
+    hip.sync()
+    e0, e1 = hip.event(), hip.event()
+    hip.record(e0)
+    for _ in range(reps):
+        hip.ok(hip.h.hipMemcpyAsync(C.c_void_p(dst), C.c_void_p(src), nbytes, hip.D2D, None),
+               "hipMemcpyAsync D2D")
+    hip.record(e1)
+    ms = hip.elapsed_ms(e0, e1) / reps
+    hip.free(src)
+    hip.free(dst)
+    print(json.dumps({"copy_bytes": nbytes, "reps": reps, "ms_per_copy": round(ms, 4),
+                      "read_plus_write_gbs": round(2 * nbytes / (ms * 1e-3) / 1e9, 1)}))
+
+
 def main():
     args = parse()
+    if args.calibrate_copy:
+        calibrate_copy()
+        return
     if args.gpus != 1:
         print(f"bench.py runs on one GPU only: this build measures the single-GPU hot path "
               f"(asked for --gpus {args.gpus}); how it would shard is described in DESIGN.md.",
@@ -369,9 +430,7 @@ def main():
         "dtype": "int8 KV (f16 scales) -> f16 MFMA, fp32 accumulate",
         "data": "synthetic (seeded N(0,1) q/k/v, 1% k outlier channels x8)",
         "config": {
-            "workload": "c5: Qwen2-7B-shaped serving stress, 64 sessions, log-uniform 1k-32k "
-                        "contexts, int8 KV + f16 scales, 16-token pages, 4-query verify "
-                        "decode, churn 8 sessions / 16 steps",
+            "workload": WORKLOAD_C5,
             "layers": cfg.shape.layers, "q_heads": cfg.shape.q_heads,
             "kv_heads": cfg.shape.kv_heads, "head_dim": cfg.shape.head_dim,
             "sessions": len(cfg.contexts), "queries_per_session": cfg.n_new,
@@ -380,17 +439,22 @@ def main():
             "tokens_per_s": round(r["tokens_per_s"], 1),
             "frac_of_hbm_peak": round(r["gbs"] / HBM_PEAK_GBS, 4),
             "attn_launch_us": round(r["attn_launch_us"], 3),
+            "attn_kernel_us": round(r["attn_kernel_us"], 3),
+            "merge_kernel_us": round(r["merge_kernel_us"], 3),
             "append_launch_us": round(r["append_launch_us"], 3),
             "decode_work_items": r["work_items"], "max_splits": r["max_splits"],
             "pool": "fragmented" if cfg.fragmented else "fresh (LIFO reuse after churn)",
         },
         "roofline": {
             "bound": "hbm",
-            "achieved": round(r["attn_gbs"], 2),
+            "kernel": "paged_attention_kernel (decode, int8 KV, head_dim 128)",
+            "achieved": round(r["attn_kernel_gbs"], 2),
             "peak": HBM_PEAK_GBS,
             "unit": "GB/s",
-            "frac": round(r["attn_gbs"] / HBM_PEAK_GBS, 4),
-            "traffic": None,
+            "frac": round(r["attn_kernel_gbs"] / HBM_PEAK_GBS, 4),
+            "traffic": measured_traffic(WORKLOAD_C5),
+            "kernel_us": round(r["attn_kernel_us"], 3),
+            "algorithmic_bytes": r["attn_bytes_per_launch"],
         },
         "cpu_baseline": cpu,
         "configs": others,

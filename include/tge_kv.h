@@ -156,6 +156,19 @@ int tge_batch_plan(tge_batch* batch, const tge_kv_pool* pool,
 int tge_batch_info(const tge_batch* batch, int* rows, int* work_items,
                    int* max_splits);
 
+/* Kernel timing of attention calls (no counterpart in the reference: it is
+ * for benchmarks and telemetry). Enabling clears the record; while enabled,
+ * each decode or prefill attention call on `batch` records HIP timing events
+ * on its stream before the paged attention kernel, between it and the split
+ * merge kernel, and after the merge. tge_batch_kernel_times waits for every
+ * recorded call and returns their number and the summed durations in
+ * microseconds (a call without splits adds only the gap between its two
+ * events to merge_us). Calls issued back to back keep the launch latency of
+ * the host out of the bracketed intervals. */
+int tge_batch_set_profiling(tge_batch* batch, int enable);
+int tge_batch_kernel_times(const tge_batch* batch, int* calls, float* attention_us,
+                           float* merge_us);
+
 /*
  * Fused quantize-and-scatter of every new token's K and V rows into its page
  * slot (the store sites above). F16: bits of the reference float_to_half

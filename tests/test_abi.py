@@ -55,6 +55,18 @@ def test_backend_forced_unavailable(tmp_path):
     assert r.returncode == 0 and "ok" in r.stdout, r.stderr
 
 
+def test_kernel_timing_argument_checks(tk):
+    L = tk.lib()
+    assert L.tge_batch_set_profiling(None, 1) == tk.ERR_INVALID
+    n, a, m = C.c_int(), C.c_float(), C.c_float()
+    assert L.tge_batch_kernel_times(None, C.byref(n), C.byref(a), C.byref(m)) == tk.ERR_INVALID
+    b = tk.Batch()
+    assert L.tge_batch_kernel_times(b.h, None, C.byref(a), C.byref(m)) == tk.ERR_INVALID
+    # nothing recorded yet: zero calls, zero time
+    assert b.kernel_times() == (0, 0.0, 0.0)
+    b.close()
+
+
 def test_pool_argument_checks(tk):
     h = C.c_void_p()
     for desc in [(0, 4, 1, 64, 1, 0), (1, 4, 1, 96, 1, 0), (1, 4, 1, 64, 7, 0),

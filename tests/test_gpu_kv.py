@@ -203,6 +203,41 @@ def test_decode_split_k_long_context(gpu):
     case.close()
 
 
+def test_decode_many_splits_merge(gpu):
+    """Contexts from one page to 30k tokens in one batch: the merge runs
+    over hundreds of splits per unit (eight slots per row) next to unsplit
+    sessions."""
+    case = PagedCase(14, 2, 64, tk.KV_F16, [30000, 5, 700, 3000], 1, seed=12)
+    case.fill()
+    got, b = case.step()
+    rows, items, splits = b.info()
+    assert splits >= 32, b.info()
+    assert_attention_close(got, case.oracle_out(), "many splits")
+    case.close()
+
+
+def test_kernel_timing_record(gpu):
+    """tge_batch_set_profiling / tge_batch_kernel_times: calls issued back
+    to back are all recorded; enabling again clears the record."""
+    case = PagedCase(14, 2, 64, tk.KV_I8, [2000, 300], 2, seed=13)
+    case.fill()
+    got, b = case.step()
+    dq = tk.DeviceArray.from_numpy(case.q)
+    dout = tk.DeviceArray((case.q.shape[0], case.qh * case.hd), np.float32).zero()
+    b.set_profiling(True)
+    for _ in range(3):
+        b.decode(case.pool, 0, dq, dout)
+    n, att_us, merge_us = b.kernel_times()
+    assert n == 3 and att_us > 0.0 and merge_us >= 0.0, (n, att_us, merge_us)
+    assert np.array_equal(bits(dout.numpy()), bits(got))
+    b.set_profiling(True)
+    assert b.kernel_times() == (0, 0.0, 0.0)
+    b.set_profiling(False)
+    dq.close()
+    dout.close()
+    case.close()
+
+
 def test_decode_64_rows(gpu):
     """n_new * group = 64 rows (four 16-row groups per unit)."""
     case = PagedCase(16, 2, 128, tk.KV_I8, [333, 50], 8, seed=4)
