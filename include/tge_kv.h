@@ -46,7 +46,9 @@ enum tge_status {
   TGE_ERR_RUNTIME = -2,     /* misuse of model/table state (std::runtime_error) */
   TGE_ERR_UNAVAILABLE = -3, /* no usable gfx950 device, or forced off */
   TGE_ERR_DEVICE = -4,      /* a HIP runtime call failed */
-  TGE_ERR_CAPACITY = -5     /* page pool or table full */
+  TGE_ERR_CAPACITY = -5     /* out of device/host memory, or a layer array
+                               beyond 2 GiB (a full BlockTable is
+                               TGE_ERR_RUNTIME, as the reference throws) */
 };
 
 enum tge_kv_format {
@@ -181,11 +183,14 @@ int tge_kv_append(const tge_batch* batch, tge_kv_pool* pool, int layer,
 
 /*
  * Decode attention for every session of the batch (n_new small: decode and
- * speculative verify). One workgroup per (session, kv head, position split)
- * shares each K/V page across the whole query-head group; splits of long
- * contexts are merged by a reduction pass (merge_gqa_chunks,
- * qwen2.cpp:1469-1522). softmax scale = 1/sqrt(head_dim) (qwen2.cpp:1278).
- * Requires n_new*group <= 64 for every session.
+ * speculative verify; the reference's attention_head / attention_group
+ * plugins, kernels.hpp:231,285, under the schedules of qwen2.cpp:1243-1467
+ * and 1705-1747). Each (session, kv head) is one stream of pages read once
+ * for its whole query-head group; the streams are cut into equal page shares
+ * over the resident workgroups, and a stream cut into several pieces is
+ * merged by a reduction pass (merge_gqa_chunks, qwen2.cpp:1469-1522).
+ * softmax scale = 1/sqrt(head_dim) (qwen2.cpp:1278). Requires
+ * n_new*group <= 64 for every session.
  */
 int tge_decode_attention(const tge_batch* batch, const tge_kv_pool* pool,
                          int layer, const float* q, float* out, void* stream);
