@@ -55,6 +55,21 @@ typedef uint32_t u32x4_t __attribute__((ext_vector_type(4)));
 
 constexpr float kLazyMax = 8.0f;  // log2 of the largest tolerated weight
 
+// acc / sum per component, correctly rounded: a row with one visible
+// position (weight w) yields exactly (w*v)/w = v.
+__device__ __forceinline__ float4_t div4(float4_t a, float b) {
+  return float4_t{__fdiv_rn(a[0], b), __fdiv_rn(a[1], b), __fdiv_rn(a[2], b), __fdiv_rn(a[3], b)};
+}
+
+// 2^e for an integer-valued float e (exact; 0 for very negative e). Every
+// row base is an integer, so rescaling a state by the difference of two
+// bases is exact and the f16 weights exp2(s - base) round the same way
+// whatever base a wave happened to pick: results do not depend on how the
+// pages were split between waves beyond fp32 summation order.
+__device__ __forceinline__ float pow2i(float e) {
+  return __builtin_amdgcn_ldexpf(1.0f, (int)fmaxf(e, -300.0f));
+}
+
 template <typename T, typename F>
 __device__ __forceinline__ T bitcast(F x) {
   static_assert(sizeof(T) == sizeof(F), "size");
@@ -264,7 +279,7 @@ struct Unit {
   __device__ __forceinline__ void consume(const Regs& r, int pi, int grp, bool masked) {
     float4_t sacc[NRG];
 #pragma unroll
-    for (int rg = 0; rg < NRG; ++rg) sacc[rg] = float4_t{-base[rg], -base[rg], -base[rg], -base[rg]};
+    for (int rg = 0; rg < NRG; ++rg) sacc[rg] = float4_t{0, 0, 0, 0};
 #pragma unroll
     for (int pp = 0; pp < NP; ++pp) {
       const half8_t ka = k_operand<FMT, SF32, D>(r, pp);
@@ -289,6 +304,7 @@ struct Unit {
     half4_t pw[NRG];
 #pragma unroll
     for (int rg = 0; rg < NRG; ++rg) {
+      sacc[rg] -= base[rg];  // exact: base is an integer
       if (masked) {
 #pragma unroll
         for (int e = 0; e < 4; ++e) {
@@ -301,8 +317,8 @@ struct Unit {
         float rmax = fmaxf(lmax, __shfl_xor(lmax, 16));
         rmax = fmaxf(rmax, __shfl_xor(rmax, 32));
         const bool grow = rmax > thr[rg];
-        const float delta = grow ? rmax : 0.0f;
-        const float alpha = (grow && thr[rg] != -INFINITY) ? __builtin_amdgcn_exp2f(-rmax) : 1.0f;
+        const float delta = grow ? ceilf(rmax) : 0.0f;  // integer steps keep base integral
+        const float alpha = (grow && thr[rg] != -INFINITY) ? pow2i(-delta) : 1.0f;
         base[rg] += delta;
         thr[rg] = grow ? kLazyMax : thr[rg];
 #pragma unroll
@@ -490,7 +506,7 @@ __device__ __forceinline__ void attend_unit(const AttnParams& p, const WorkRec& 
 #pragma unroll
     for (int k = 1; k < kWaves; ++k) mm = fmaxf(mm, lds_m[k][r]);
     const float mine_m = lds_m[wave][r];
-    const float f = (mine_m == -INFINITY) ? 0.0f : __builtin_amdgcn_exp2f(mine_m - mm);
+    const float f = (mine_m == -INFINITY) ? 0.0f : pow2i(mine_m - mm);
 #pragma unroll
     for (int t = 0; t < NT; ++t) u.o[rg][t] *= f;
   }
@@ -522,14 +538,14 @@ __device__ __forceinline__ void attend_unit(const AttnParams& p, const WorkRec& 
 #pragma unroll
     for (int k = 0; k < kWaves; ++k) {
       const float mk = lds_m[k][r];
-      if (mk != -INFINITY) sum += lds_l[k][r] * __builtin_amdgcn_exp2f(mk - mm);
+      if (mk != -INFINITY) sum += lds_l[k][r] * pow2i(mk - mm);
     }
     const float4_t acc = *reinterpret_cast<const float4_t*>(&lds_o[r * OPAD + 4 * d4]);
     if (w.part < 0) {
       const int qi = w.row_begin + r / geff;
       const int head = w.head_base + r % geff;
       float4_t res = float4_t{0, 0, 0, 0};
-      if (sum > 0.0f) res = acc * (1.0f / sum);
+      if (sum > 0.0f) res = div4(acc, sum);
       *reinterpret_cast<float4_t*>(p.out + (size_t)(s.q_row + qi) * q_stride + (size_t)head * D + 4 * d4) = res;
     } else {
       *reinterpret_cast<float4_t*>(p.part_o + ((size_t)w.part * p.rows_cap + r) * D + 4 * d4) = acc;
@@ -557,6 +573,327 @@ void paged_attention_kernel(AttnParams p) {
     const WorkRec w = p.work[it];
     attend_unit<FMT, SF32, D, NRG, QSPLIT>(p, w, sh);
     __syncthreads();  // LDS is reused by the next item
+  }
+}
+
+// ---------------------------------------------------------------------------
+// Decode kernel: persistent workgroups of four waves (as many per CU as the
+// registers allow), each covering a contiguous share of the plan's page
+// sequence (its work items in order).
+//
+// Within a unit the waves take pages round-robin (wave w: pages w, w+4,
+// ...). Each wave streams its pages through a private LDS ring and crosses
+// unit boundaries without draining: the next unit's first pages are already
+// in flight while the current unit is merged. A unit ends for a wave when
+// its next page belongs to a later unit (or the share is exhausted); the
+// four waves then merge their states for that unit in wave order, so every
+// wave passes the same barriers. The page split is fixed by the plan, so
+// results are bit-reproducible.
+// ---------------------------------------------------------------------------
+template <int FMT, bool SF32, int D, int NRG, int WPE>
+struct DecodeShared {
+  static constexpr int ROWS = 16 * NRG;
+  static constexpr int OPAD = D + 4;
+  static constexpr int MERGE_FLOATS = 2 * kWaves * ROWS + ROWS * OPAD;
+  static constexpr int SLOT = Ring<FMT, SF32, D>::SLOT;
+  // LDS of one of the WPE workgroups that share a CU.
+  static constexpr int BUDGET = 160 * 1024 / WPE - 4 * MERGE_FLOATS - 64;
+  static constexpr int NB_FIT = BUDGET / (kWaves * SLOT);
+  static constexpr int NB = NB_FIT > 4 ? 4 : NB_FIT;
+  static_assert(NB >= 2, "the decode ring needs two slots per wave");
+  alignas(16) char ring[kWaves * NB * SLOT];
+  alignas(16) float merge[MERGE_FLOATS];
+};
+
+typedef const __attribute__((address_space(4))) WorkRec sconst_work;
+
+// Workgroup barrier ordering LDS only: this wave's LDS accesses complete,
+// then all waves meet. Direct-to-LDS page loads stay in flight across it
+// (they fill the wave's own ring, which no other wave reads); the
+// __syncthreads fence would wait for them.
+__device__ __forceinline__ void lds_barrier() {
+  asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
+}
+
+// A work record read through the scalar cache.
+__device__ __forceinline__ WorkRec load_work(const sconst_work* w) {
+  const sconst_int* q = (const sconst_int*)w;
+  WorkRec r;
+  r.session = q[0];
+  r.kv_head = q[1];
+  r.page_begin = q[2];
+  r.page_end = q[3];
+  r.part = q[4];
+  r.row_begin = q[5];
+  r.rows = q[6];
+  r.rows_per_query = q[7];
+  r.head_base = q[8];
+  r.ctx = q[9];
+  r.q_row = q[10];
+  r.table_off = q[11];
+  return r;
+}
+
+// Share indices of the pages in a wave's ring, oldest first (a FIFO of at
+// most four wave-uniform values kept in scalar registers).
+struct PageFifo {
+  int t0 = 0, t1 = 0, t2 = 0, t3 = 0;
+  __device__ __forceinline__ void push(int n, int g) {  // n = entries before the push
+    t0 = n == 0 ? g : t0;
+    t1 = n == 1 ? g : t1;
+    t2 = n == 2 ? g : t2;
+    t3 = n == 3 ? g : t3;
+  }
+  __device__ __forceinline__ void pop() {
+    t0 = t1;
+    t1 = t2;
+    t2 = t3;
+  }
+};
+
+template <int FMT, bool SF32, int D, int NRG, bool QSPLIT, int WPE>
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(WPE, WPE)))
+void paged_decode_kernel(AttnParams p) {
+  constexpr int W = kWaves;
+  using SH = DecodeShared<FMT, SF32, D, NRG, WPE>;
+  using U = Unit<FMT, SF32, D, NRG, QSPLIT>;
+  using Regs = typename U::Regs;
+  using RG = Ring<FMT, SF32, D>;
+  constexpr int NB = SH::NB;
+  constexpr int NP = D / 32;
+  constexpr int NT = D / 16;
+  constexpr int ROWS = 16 * NRG;
+  constexpr int OPAD = D + 4;
+  __shared__ SH sh;
+
+  const int first = p.wg_first[blockIdx.x];
+  const int last = p.wg_first[blockIdx.x + 1];
+  if (first >= last) return;  // the whole workgroup leaves together
+
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int col = lane & 15;
+  const int grp = lane >> 4;
+  const sconst_work* work = (const sconst_work*)p.work;
+  const int q_stride = p.q_heads * D;
+
+  LayerRsrc rs;
+  rs.k = make_rsrc(p.kpool, p.kv_array_bytes);
+  rs.v = make_rsrc(p.vpool, p.kv_array_bytes);
+  char* ring = sh.ring + wave * NB * RG::SLOT;
+
+  // ---- issue side: this wave's next page, its block, its fetch -------------
+  // Cursor over the share's units: unit `ik` covers share pages
+  // [ibase, ibase + its page count); `jn` is this wave's next page in it.
+  int ik = first, ibase = 0, jn = wave;
+  WorkRec iw = load_work(work + first);
+  WorkRec iw_next = load_work(work + (first + 1 < last ? first + 1 : first));
+  int pend_g = -1, pend_block = 0;  // next page to fetch (share index, block)
+  auto request = [&]() __attribute__((always_inline)) -> void {
+    bool ok = true;
+    while (ok && jn >= iw.page_end - iw.page_begin) {
+      if (ik + 1 >= last) {
+        ok = false;  // past the share: the cursor stays on its last unit
+      } else {
+        const int np = iw.page_end - iw.page_begin;
+        ibase += np;
+        ++ik;
+        jn = wave;
+        iw = iw_next;
+        iw_next = load_work(work + (ik + 1 < last ? ik + 1 : ik));
+      }
+    }
+    // (index 0 when past the share keeps the table read inside the unit)
+    const sconst_int* t = (const sconst_int*)(p.tables + iw.table_off + iw.page_begin);
+    const int id = t[ok ? jn : 0];
+    pend_g = ok ? ibase + jn : -1;
+    pend_block = id * p.kv_heads + iw.kv_head;
+    jn += W;
+  };
+  // Fetch the pending page into `slot` and take the next; returns the
+  // fetched page's share index, or -1 when the share is exhausted.
+  auto issue = [&](int slot) __attribute__((always_inline)) -> int {
+    const int g = pend_g;
+    if (g >= 0) {
+      fetch_page<FMT, SF32, D>(ring + slot * RG::SLOT, rs, p, pend_block, lane);
+      request();
+    }
+    return g;
+  };
+
+  // ---- consume side: unit state --------------------------------------------
+  int ck = first, cbase = 0;
+  WorkRec cw = load_work(work + first);
+  U u;
+  int unmasked = 0;
+  auto reset_unit = [&]() __attribute__((always_inline)) -> void {
+#pragma unroll
+    for (int rg = 0; rg < NRG; ++rg) {
+      const int r = rg * 16 + col;
+      u.lim[rg] = r < cw.rows ? cw.ctx + cw.row_begin + r / cw.rows_per_query : -1;
+      u.base[rg] = 0.0f;
+      u.thr[rg] = -INFINITY;
+      u.l4[rg] = float4_t{0, 0, 0, 0};
+#pragma unroll
+      for (int t = 0; t < NT; ++t) u.o[rg][t] = float4_t{0, 0, 0, 0};
+    }
+    unmasked = (cw.ctx + cw.row_begin + 1) / 16;  // pages with no masked position
+  };
+  // Q^T operands of the unit (see attend_unit), loaded before its first page.
+  auto load_q = [&]() __attribute__((always_inline)) -> void {
+#pragma unroll
+    for (int rg = 0; rg < NRG; ++rg) {
+      const int r = rg * 16 + col;
+      const bool valid = r < cw.rows;
+      const int qi = cw.row_begin + (valid ? r / cw.rows_per_query : 0);
+      const int head = cw.head_base + (valid ? r % cw.rows_per_query : 0);
+      const float* qp = p.q + (size_t)(cw.q_row + qi) * q_stride + (size_t)head * D + 4 * grp;
+#pragma unroll
+      for (int pp = 0; pp < NP; ++pp) {
+        float4 a = make_float4(0, 0, 0, 0), b = make_float4(0, 0, 0, 0);
+        if (valid) {
+          a = *reinterpret_cast<const float4*>(qp + 32 * pp);
+          b = *reinterpret_cast<const float4*>(qp + 32 * pp + 16);
+        }
+        const float c = p.scale_log2;
+        const float x[8] = {a.x * c, a.y * c, a.z * c, a.w * c, b.x * c, b.y * c, b.z * c, b.w * c};
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+          const _Float16 hi = (_Float16)x[j];
+          u.qhi[rg][pp][j] = hi;
+          u.qlo[rg][pp][j] = QSPLIT ? (_Float16)(x[j] - (float)hi) : (_Float16)0.0f;
+        }
+      }
+    }
+  };
+  // Merge the W waves' states of unit `cw` in wave order and write the
+  // output rows (or the unit's partial). Every wave calls this once per unit.
+  float* mbase = sh.merge;
+  float (*lds_m)[ROWS] = reinterpret_cast<float (*)[ROWS]>(mbase);
+  float (*lds_l)[ROWS] = reinterpret_cast<float (*)[ROWS]>(mbase + W * ROWS);
+  float* lds_o = mbase + 2 * W * ROWS;
+  auto finalize = [&]() __attribute__((always_inline)) -> void {
+#pragma unroll
+    for (int rg = 0; rg < NRG; ++rg) {
+      if (grp == 0) {
+        lds_m[wave][rg * 16 + col] = u.thr[rg] == -INFINITY ? -INFINITY : u.base[rg];
+        lds_l[wave][rg * 16 + col] = u.l4[rg][0];
+      }
+    }
+    lds_barrier();
+#pragma unroll
+    for (int rg = 0; rg < NRG; ++rg) {
+      const int r = rg * 16 + col;
+      float mm = lds_m[0][r];
+#pragma unroll
+      for (int k = 1; k < W; ++k) mm = fmaxf(mm, lds_m[k][r]);
+      const float mine_m = lds_m[wave][r];
+      const float f = (mine_m == -INFINITY) ? 0.0f : pow2i(mine_m - mm);
+#pragma unroll
+      for (int t = 0; t < NT; ++t) u.o[rg][t] *= f;
+    }
+    for (int k = 0; k < W; ++k) {
+      if (wave == k) {
+#pragma unroll
+        for (int rg = 0; rg < NRG; ++rg) {
+#pragma unroll
+          for (int t = 0; t < NT; ++t) {
+            float4_t* dst = reinterpret_cast<float4_t*>(&lds_o[(rg * 16 + col) * OPAD + 16 * t + 4 * grp]);
+            if (k == 0) {
+              *dst = u.o[rg][t];
+            } else {
+              *dst += u.o[rg][t];
+            }
+          }
+        }
+      }
+      lds_barrier();
+    }
+    for (int idx = threadIdx.x; idx < cw.rows * (D / 4); idx += 64 * W) {
+      const int r = idx / (D / 4);
+      const int d4 = idx % (D / 4);
+      float mm = lds_m[0][r];
+#pragma unroll
+      for (int k = 1; k < W; ++k) mm = fmaxf(mm, lds_m[k][r]);
+      float sum = 0.0f;
+#pragma unroll
+      for (int k = 0; k < W; ++k) {
+        const float mk = lds_m[k][r];
+        if (mk != -INFINITY) sum += lds_l[k][r] * pow2i(mk - mm);
+      }
+      const float4_t acc = *reinterpret_cast<const float4_t*>(&lds_o[r * OPAD + 4 * d4]);
+      if (cw.part < 0) {
+        const int qi = cw.row_begin + r / cw.rows_per_query;
+        const int head = cw.head_base + r % cw.rows_per_query;
+        float4_t res = float4_t{0, 0, 0, 0};
+        if (sum > 0.0f) res = div4(acc, sum);
+        *reinterpret_cast<float4_t*>(p.out + (size_t)(cw.q_row + qi) * q_stride + (size_t)head * D + 4 * d4) = res;
+      } else {
+        *reinterpret_cast<float4_t*>(p.part_o + ((size_t)cw.part * p.rows_cap + r) * D + 4 * d4) = acc;
+        if (d4 == 0) {
+          p.part_ml[((size_t)cw.part * p.rows_cap + r) * 2] = mm;
+          p.part_ml[((size_t)cw.part * p.rows_cap + r) * 2 + 1] = sum;
+        }
+      }
+    }
+    lds_barrier();  // the merge area is free for the next unit
+  };
+  auto next_unit = [&]() __attribute__((always_inline)) -> void {
+    cbase += cw.page_end - cw.page_begin;
+    ++ck;
+    cw = load_work(work + (ck < last ? ck : last - 1));
+    reset_unit();
+  };
+  // Q^T of the unit is loaded when the wave starts it, so the previous
+  // unit's Q is dead while that unit is merged.
+
+  // ---- the page loop -----------------------------------------------------------
+  reset_unit();
+  load_q();
+  request();
+  PageFifo fifo;
+  int head = 0, count = 0;
+#pragma unroll
+  for (int b = 0; b < NB - 1; ++b) {
+    if (count == b) {
+      const int g = issue(b);
+      if (g >= 0) {
+        fifo.push(count, g);
+        ++count;
+      }
+    }
+  }
+  while (count > 0) {
+    int nslot = head + count;
+    nslot = nslot >= NB ? nslot - NB : nslot;
+    const int gn = issue(nslot);
+    if (gn >= 0) {
+      fifo.push(count, gn);
+      ++count;
+      wait_vmcnt<(NB - 1) * RG::LOADS>();  // the ring is full: the oldest page has landed
+    } else {
+      wait_vmcnt<0>();
+    }
+    const int g = fifo.t0;
+    if (g >= cbase + (cw.page_end - cw.page_begin)) {
+      do {
+        finalize();
+        next_unit();
+      } while (g >= cbase + (cw.page_end - cw.page_begin));
+      load_q();
+    }
+    Regs r;
+    read_page<FMT, SF32, D>(r, ring + head * RG::SLOT, lane, grp);
+    const int pi = cw.page_begin + (g - cbase);
+    u.consume(r, pi, grp, pi >= unmasked);
+    head = head + 1 == NB ? 0 : head + 1;
+    --count;
+    fifo.pop();
+  }
+  // The share is exhausted: close this wave's remaining units.
+  while (ck < last) {
+    finalize();
+    next_unit();
   }
 }
 
@@ -605,12 +942,12 @@ __global__ __launch_bounds__(256) void split_reduce_kernel(ReduceParams p) {
       for (int i = 0; i < 8; ++i)
         if (x[i].y > 0.0f) bm = fmaxf(bm, x[i].x);
       if (bm == -INFINITY) continue;  // nothing visible in this batch yet
-      const float c = m == -INFINITY ? 0.0f : __builtin_amdgcn_exp2f(m - bm);
+      const float c = m == -INFINITY ? 0.0f : pow2i(m - bm);
       sum *= c;
       acc *= c;
 #pragma unroll
       for (int i = 0; i < 8; ++i) {
-        const float f = x[i].y > 0.0f ? __builtin_amdgcn_exp2f(x[i].x - bm) : 0.0f;
+        const float f = x[i].y > 0.0f ? pow2i(x[i].x - bm) : 0.0f;
         sum += x[i].y * f;
         acc += v[i] * f;
       }
@@ -634,7 +971,7 @@ __global__ __launch_bounds__(256) void split_reduce_kernel(ReduceParams p) {
 #pragma unroll
       for (int j = 0; j < S; ++j) {
         const float mj = sh_m[rr][j];
-        const float f = mj == -INFINITY ? 0.0f : __builtin_amdgcn_exp2f(mj - mm);
+        const float f = mj == -INFINITY ? 0.0f : pow2i(mj - mm);
         sum += sh_l[rr][j] * f;
         acc += sh_o[rr][j][d4] * f;
       }
@@ -647,7 +984,7 @@ __global__ __launch_bounds__(256) void split_reduce_kernel(ReduceParams p) {
   const int qi = it.row_begin + r / it.rows_per_query;
   const int head = it.head_base + r % it.rows_per_query;
   float4_t res = float4_t{0, 0, 0, 0};
-  if (sum > 0.0f) res = acc * (1.0f / sum);
+  if (sum > 0.0f) res = div4(acc, sum);
   *reinterpret_cast<float4_t*>(p.out + (size_t)(s.q_row + qi) * q_stride + (size_t)head * D + 4 * d4) = res;
 }
 
@@ -718,6 +1055,98 @@ int attention_blocks_per_cu(int format, int scale_f32, int head_dim, int row_gro
   }
   if (head_dim == 64) return scale_f32 ? blocks_rg<kI8, true, 64, true>(row_groups) : blocks_rg<kI8, false, 64, true>(row_groups);
   return scale_f32 ? blocks_rg<kI8, true, 128, true>(row_groups) : blocks_rg<kI8, false, 128, true>(row_groups);
+}
+
+// Whether a variant's decode ring (two or more slots per wave) and merge
+// area fit its share of LDS; the others run the unit-at-a-time kernel.
+template <int FMT, bool SF32, int D, int NRG>
+constexpr bool decode_fits() {
+  constexpr int wpe = waves_per_eu<FMT, D, NRG, true>();
+  constexpr int rows = 16 * NRG;
+  constexpr int merge = 4 * (2 * kWaves * rows + rows * (D + 4));
+  return (160 * 1024 / wpe - merge - 64) / (kWaves * Ring<FMT, SF32, D>::SLOT) >= 2;
+}
+
+template <int FMT, bool SF32, int D>
+hipError_t launch_decode_d(int row_groups, int n_groups, const AttnParams& p, hipStream_t stream) {
+  switch (row_groups) {
+#define TGE_DEC(n)                                                                                 \
+  case n: {                                                                                        \
+    constexpr int wpe = waves_per_eu<FMT, D, n, true>();                                           \
+    if constexpr (decode_fits<FMT, SF32, D, n>()) {                                                \
+      hipLaunchKernelGGL((paged_decode_kernel<FMT, SF32, D, n, true, wpe>),                        \
+                         dim3((unsigned)n_groups), dim3(256), 0, stream, p);                       \
+    } else {                                                                                       \
+      hipLaunchKernelGGL((paged_attention_kernel<FMT, SF32, D, n, true, wpe>),                     \
+                         dim3((unsigned)n_groups), dim3(256), 0, stream, p);                       \
+    }                                                                                              \
+    break;                                                                                         \
+  }
+    TGE_DEC(1)
+    TGE_DEC(2)
+    TGE_DEC(3)
+    TGE_DEC(4)
+#undef TGE_DEC
+    default:
+      return hipErrorInvalidValue;
+  }
+  return hipGetLastError();
+}
+
+template <int FMT, bool SF32, int D>
+int decode_blocks_d(int row_groups) {
+  int n = 0;
+  hipError_t e = hipErrorInvalidValue;
+  switch (row_groups) {
+#define TGE_DOCC(r)                                                                          \
+  case r: {                                                                                  \
+    constexpr int wpe = waves_per_eu<FMT, D, r, true>();                                     \
+    if constexpr (decode_fits<FMT, SF32, D, r>()) {                                          \
+      e = hipOccupancyMaxActiveBlocksPerMultiprocessor(                                      \
+          &n, paged_decode_kernel<FMT, SF32, D, r, true, wpe>, 256, 0);                      \
+    } else {                                                                                 \
+      e = hipOccupancyMaxActiveBlocksPerMultiprocessor(                                      \
+          &n, paged_attention_kernel<FMT, SF32, D, r, true, wpe>, 256, 0);                   \
+    }                                                                                        \
+    break;                                                                                   \
+  }
+    TGE_DOCC(1)
+    TGE_DOCC(2)
+    TGE_DOCC(3)
+    TGE_DOCC(4)
+#undef TGE_DOCC
+    default:
+      break;
+  }
+  return e == hipSuccess ? n : 0;
+}
+
+hipError_t launch_decode(int format, int scale_f32, int head_dim, int row_groups, int n_groups,
+                         const AttnParams& p, hipStream_t stream) {
+  if (n_groups <= 0) return hipSuccess;
+  if (!p.wg_first) return hipErrorInvalidValue;
+  if (format == kF16) {
+    if (head_dim == 64) return launch_decode_d<kF16, false, 64>(row_groups, n_groups, p, stream);
+    if (head_dim == 128) return launch_decode_d<kF16, false, 128>(row_groups, n_groups, p, stream);
+  } else if (format == kI8) {
+    if (head_dim == 64)
+      return scale_f32 ? launch_decode_d<kI8, true, 64>(row_groups, n_groups, p, stream)
+                       : launch_decode_d<kI8, false, 64>(row_groups, n_groups, p, stream);
+    if (head_dim == 128)
+      return scale_f32 ? launch_decode_d<kI8, true, 128>(row_groups, n_groups, p, stream)
+                       : launch_decode_d<kI8, false, 128>(row_groups, n_groups, p, stream);
+  }
+  return hipErrorInvalidValue;
+}
+
+int decode_blocks_per_cu(int format, int scale_f32, int head_dim, int row_groups) {
+  if (format == kF16) {
+    return head_dim == 64 ? decode_blocks_d<kF16, false, 64>(row_groups)
+                          : decode_blocks_d<kF16, false, 128>(row_groups);
+  }
+  if (head_dim == 64)
+    return scale_f32 ? decode_blocks_d<kI8, true, 64>(row_groups) : decode_blocks_d<kI8, false, 64>(row_groups);
+  return scale_f32 ? decode_blocks_d<kI8, true, 128>(row_groups) : decode_blocks_d<kI8, false, 128>(row_groups);
 }
 
 template <int D>

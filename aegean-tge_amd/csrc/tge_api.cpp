@@ -376,10 +376,17 @@ int upload_plan(AttnPlan& pl, int head_dim, hipStream_t st) {
 }
 
 // Resident workgroups of an attention variant on this device (cached).
-int resident_groups(int format, int scale_f32, int head_dim, int row_groups, bool qsplit) {
+// Workgroups of a decode launch: one per CU (the decode kernel's workgroup
+// holds all of a CU's waves), times what the occupancy query allows.
+struct Residency {
+  int groups;  // resident workgroups of the launch
+  int cus;     // compute units
+};
+
+Residency resident_groups(int format, int scale_f32, int head_dim, int row_groups) {
   static std::mutex mu;
-  static std::vector<std::pair<int, int>> cache;  // key -> groups
-  const int key = (((format * 2 + scale_f32) * 256 + head_dim) * 8 + row_groups) * 2 + qsplit;
+  static std::vector<std::pair<int, Residency>> cache;  // key -> residency
+  const int key = ((format * 2 + scale_f32) * 256 + head_dim) * 8 + row_groups;
   std::lock_guard<std::mutex> lock(mu);
   for (const auto& kv : cache)
     if (kv.first == key) return kv.second;
@@ -387,76 +394,134 @@ int resident_groups(int format, int scale_f32, int head_dim, int row_groups, boo
   if (hipGetDevice(&dev) != hipSuccess ||
       hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess)
     cus = 256;
-  int per_cu = tge::attention_blocks_per_cu(format, scale_f32, head_dim, row_groups, qsplit);
+  int per_cu = tge::decode_blocks_per_cu(format, scale_f32, head_dim, row_groups);
   if (per_cu <= 0) per_cu = 1;
-  const int groups = per_cu * cus;
-  cache.emplace_back(key, groups);
-  return groups;
+  const Residency r{per_cu * cus, cus};
+  cache.emplace_back(key, r);
+  return r;
 }
+
+// Relative speed of the k-th workgroup that lands on a CU. Workgroups are
+// dispatched one per CU before a CU gets a second, and on a shared SIMD the
+// older wave wins issue, so equal page shares finish far apart (measured:
+// ~25 % slower for the second). Shares are weighted by rank^k.
+#ifndef TGE_DECODE_RANK_WEIGHT
+#define TGE_DECODE_RANK_WEIGHT 0.8
+#endif
+// Fixed cost of one unit of a share (start-up and merge), in pages.
+#ifndef TGE_DECODE_UNIT_COST
+#define TGE_DECODE_UNIT_COST 16
+#endif
 
 // Decode schedule. Every (session, kv head) is a segment of pages whose rows
 // are the GQA group of each new token. The segments are laid end to end and
 // cut into one equal share of pages per resident workgroup, so all
 // workgroups of the launch finish together; a segment cut into several
 // items is merged by the split reduction.
-void build_decode(tge_batch* b, int groups) {
+void build_decode(tge_batch* b, Residency res) {
   AttnPlan& pl = b->decode;
   pl.work.clear();
   pl.reduce.clear();
   pl.wg_first.clear();
   pl.parts = pl.max_splits = 0;
   pl.row_groups = std::max(1, std::min(4, (b->max_rows + 15) / 16));
+
+  struct Seg {
+    int session, head, pages;
+  };
+  std::vector<Seg> segs;
   long total = 0;
-  for (const auto& sr : b->sessions) total += (long)((sr.ctx + sr.n_new + 15) / 16) * b->kv_heads;
-  // At least 8 pages (two per wave) per workgroup.
-  const long g_eff = std::max<long>(1, std::min<long>(groups, (total + 7) / 8));
-  const long share = (total + g_eff - 1) / g_eff;
-  long room = share;
-  pl.wg_first.push_back(0);
   for (int s = 0; s < (int)b->sessions.size(); ++s) {
     const tge::SessionRec& sr = b->sessions[s];
     const int pages = (sr.ctx + sr.n_new + 15) / 16;
-    for (int h = 0; h < b->kv_heads; ++h) {
-      tge::WorkRec base{};
-      base.session = s;
-      base.kv_head = h;
-      base.row_begin = 0;
-      base.rows = sr.n_new * b->group;
-      base.rows_per_query = b->group;
-      base.head_base = h * b->group;
-      const int first_item = (int)pl.work.size();
-      for (int pos = 0; pos < pages;) {
-        const int take = (int)std::min<long>(room, pages - pos);
-        tge::WorkRec w = base;
-        w.page_begin = pos;
-        w.page_end = pos + take;
-        pl.work.push_back(w);
-        pos += take;
-        room -= take;
-        if (room == 0) {
-          pl.wg_first.push_back((int)pl.work.size());
-          room = share;
-        }
-      }
-      const int n = (int)pl.work.size() - first_item;
-      pl.max_splits = std::max(pl.max_splits, n);
-      if (n == 1) {
-        pl.work[first_item].part = -1;
-      } else {
-        tge::ReduceRec r{};
-        r.session = s;
-        r.row_begin = 0;
-        r.rows = base.rows;
-        r.rows_per_query = base.rows_per_query;
-        r.head_base = base.head_base;
-        r.first_part = pl.parts;
-        r.n_parts = n;
-        for (int i = first_item; i < first_item + n; ++i) pl.work[i].part = pl.parts++;
-        pl.reduce.push_back(r);
-      }
-    }
+    for (int h = 0; h < b->kv_heads; ++h) segs.push_back(Seg{s, h, pages});
+    total += (long)pages * b->kv_heads;
   }
-  if (pl.wg_first.back() != (int)pl.work.size()) pl.wg_first.push_back((int)pl.work.size());
+  // At least 16 pages per workgroup.
+  const long g_eff = std::max<long>(1, std::min<long>(res.groups, (total + 15) / 16));
+  std::vector<double> w((size_t)g_eff);
+  double wrem = 0.0;
+  for (long g = 0; g < g_eff; ++g) {
+    w[(size_t)g] = std::pow(TGE_DECODE_RANK_WEIGHT, (double)(g / std::max(1, res.cus)));
+    wrem += w[(size_t)g];
+  }
+
+  // Cut the segments, end to end, into one share per workgroup. A share's
+  // cost is its pages plus TGE_DECODE_UNIT_COST per piece (the fixed cost
+  // of starting and merging a unit); each share gets the remaining cost in
+  // proportion to its rank weight, the last one takes what is left.
+  const double unit_cost = TGE_DECODE_UNIT_COST;
+  std::vector<int> seg_of;  // segment of each work item
+  long pages_rem = total, segs_rem = (long)segs.size();
+  size_t si = 0;
+  int pos = 0;
+  pl.wg_first.push_back(0);
+  for (long g = 0; g < g_eff && si < segs.size(); ++g) {
+    const bool last_wg = g + 1 == g_eff;
+    double target =
+        ((double)pages_rem + unit_cost * (double)(segs_rem + (g_eff - g))) * w[(size_t)g] / wrem;
+    wrem -= w[(size_t)g];
+    bool started = false;
+    while (si < segs.size()) {
+      const Seg& sg = segs[si];
+      const int left = sg.pages - pos;
+      int take = left;
+      if (!last_wg) {
+        const double room = target - unit_cost;
+        if (started && room < 1.0) break;
+        take = (int)std::min<double>(left, std::max(1.0, std::floor(room)));
+      }
+      const tge::SessionRec& sr = b->sessions[sg.session];
+      tge::WorkRec it{};
+      it.session = sg.session;
+      it.kv_head = sg.head;
+      it.page_begin = pos;
+      it.page_end = pos + take;
+      it.part = -1;
+      it.row_begin = 0;
+      it.rows = sr.n_new * b->group;
+      it.rows_per_query = b->group;
+      it.head_base = sg.head * b->group;
+      it.ctx = sr.ctx;
+      it.q_row = sr.q_row;
+      it.table_off = sr.table_off;
+      pl.work.push_back(it);
+      seg_of.push_back((int)si);
+      started = true;
+      target -= take + unit_cost;
+      pos += take;
+      pages_rem -= take;
+      if (pos == sg.pages) {
+        ++si;
+        pos = 0;
+        --segs_rem;
+      }
+      if (!last_wg && target < unit_cost + 1.0) break;
+    }
+    pl.wg_first.push_back((int)pl.work.size());
+  }
+
+  // Segments cut into several items are merged by the split reduction.
+  for (size_t i = 0; i < pl.work.size();) {
+    size_t j = i + 1;
+    while (j < pl.work.size() && seg_of[j] == seg_of[i]) ++j;
+    const int n = (int)(j - i);
+    pl.max_splits = std::max(pl.max_splits, n);
+    if (n > 1) {
+      const tge::WorkRec& w0 = pl.work[i];
+      tge::ReduceRec r{};
+      r.session = w0.session;
+      r.row_begin = w0.row_begin;
+      r.rows = w0.rows;
+      r.rows_per_query = w0.rows_per_query;
+      r.head_base = w0.head_base;
+      r.first_part = pl.parts;
+      r.n_parts = n;
+      for (size_t k = i; k < j; ++k) pl.work[k].part = pl.parts++;
+      pl.reduce.push_back(r);
+    }
+    i = j;
+  }
   pl.groups = (int)pl.wg_first.size() - 1;
 }
 
@@ -478,6 +543,9 @@ void build_prefill(tge_batch* b) {
         tge::WorkRec w{};
         w.session = s;
         w.kv_head = hq / b->group;
+        w.ctx = sr.ctx;
+        w.q_row = sr.q_row;
+        w.table_off = sr.table_off;
         w.row_begin = a;
         w.rows = std::min(tile, sr.n_new - a);
         w.rows_per_query = 1;
@@ -572,7 +640,7 @@ int tge_batch_plan(tge_batch* b, const tge_kv_pool* pool, const tge_batch_desc* 
   if (max_rows <= tge::kMaxRows) {
     const int rg = std::max(1, std::min(4, (max_rows + 15) / 16));
     build_decode(b, resident_groups(pool->desc.format, pool->desc.scale_format == TGE_SCALE_F32,
-                                    hd, rg, true));
+                                    hd, rg));
     s = upload_plan(b->decode, hd, st);
     if (s != TGE_OK) return s;
   }
@@ -656,7 +724,7 @@ tge::AttnParams attn_params(const tge_batch* b, const tge_kv_pool* p, int layer,
 }
 
 int run_attention(const tge_batch* b, const tge_kv_pool* p, int layer, const float* q,
-                  float* out, void* stream, const AttnPlan& pl, bool qsplit) {
+                  float* out, void* stream, const AttnPlan& pl, bool qsplit, bool decode) {
   hipStream_t st = static_cast<hipStream_t>(stream);
   const tge::AttnParams a = attn_params(b, p, layer, q, out, pl);
   std::array<hipEvent_t, 3>* ev = nullptr;
@@ -677,8 +745,13 @@ int run_attention(const tge_batch* b, const tge_kv_pool* p, int layer, const flo
     ev = &mb->prof[mb->prof_used++];
     TGE_HIP(hipEventRecord((*ev)[0], st));
   }
-  TGE_HIP(tge::launch_attention(p->desc.format, p->desc.scale_format == TGE_SCALE_F32,
-                                b->head_dim, pl.row_groups, qsplit, pl.groups, a, st));
+  if (decode) {
+    TGE_HIP(tge::launch_decode(p->desc.format, p->desc.scale_format == TGE_SCALE_F32, b->head_dim,
+                               pl.row_groups, pl.groups, a, st));
+  } else {
+    TGE_HIP(tge::launch_attention(p->desc.format, p->desc.scale_format == TGE_SCALE_F32,
+                                  b->head_dim, pl.row_groups, qsplit, pl.groups, a, st));
+  }
   if (ev) TGE_HIP(hipEventRecord((*ev)[1], st));
   if (!pl.reduce.empty()) {
     tge::ReduceParams r{};
@@ -727,7 +800,7 @@ int tge_decode_attention(const tge_batch* b, const tge_kv_pool* p, int layer,
   if (!q || !out) return fail(TGE_ERR_INVALID, "decode_attention: null q/out");
   if (!b->decode.built)
     return fail(TGE_ERR_INVALID, "decode_attention: n_new * group exceeds 64 rows");
-  return run_attention(b, p, layer, q, out, stream, b->decode, true);
+  return run_attention(b, p, layer, q, out, stream, b->decode, true, true);
 }
 
 int tge_prefill_attention(const tge_batch* b, const tge_kv_pool* p, int layer,
@@ -743,7 +816,8 @@ int tge_prefill_attention(const tge_batch* b, const tge_kv_pool* p, int layer,
     s = upload_plan(mb->prefill, b->head_dim, static_cast<hipStream_t>(stream));
     if (s != TGE_OK) return s;
   }
-  return run_attention(b, p, layer, q, out, stream, b->prefill, p->desc.format == TGE_KV_I8);
+  return run_attention(b, p, layer, q, out, stream, b->prefill, p->desc.format == TGE_KV_I8,
+                       false);
 }
 
 int tge_kv_gather(const tge_batch* b, const tge_kv_pool* p, int layer, int session,

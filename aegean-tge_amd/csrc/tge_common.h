@@ -68,8 +68,13 @@ struct WorkRec {
   int rows;
   int rows_per_query;
   int head_base;
-  int pad0, pad1, pad2;
+  // copies of the session record, so a unit needs no second lookup
+  int ctx;
+  int q_row;
+  int table_off;
 };
+
+static_assert(sizeof(WorkRec) == 12 * sizeof(int), "WorkRec is read as 12 ints");
 
 // One row set whose context was split over several units.
 struct ReduceRec {

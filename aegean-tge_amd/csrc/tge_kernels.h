@@ -76,6 +76,12 @@ hipError_t launch_kv_gather(int format, const GatherParams& p, hipStream_t strea
 hipError_t launch_attention(int format, int scale_f32, int head_dim, int row_groups,
                             bool qsplit, int n_groups, const AttnParams& p,
                             hipStream_t stream);
+// Decode attention over a balanced plan (p.wg_first required): n_groups
+// persistent workgroups of four waves.
+hipError_t launch_decode(int format, int scale_f32, int head_dim, int row_groups, int n_groups,
+                         const AttnParams& p, hipStream_t stream);
+// Resident decode workgroups per CU.
+int decode_blocks_per_cu(int format, int scale_f32, int head_dim, int row_groups);
 hipError_t launch_reduce(int head_dim, int n_items, int max_parts, const ReduceParams& p,
                          hipStream_t stream);
 // Resident 256-thread workgroups per CU of one attention variant (0 if the

@@ -186,9 +186,11 @@ int tge_kv_append(const tge_batch* batch, tge_kv_pool* pool, int layer,
  * speculative verify; the reference's attention_head / attention_group
  * plugins, kernels.hpp:231,285, under the schedules of qwen2.cpp:1243-1467
  * and 1705-1747). Each (session, kv head) is one stream of pages read once
- * for its whole query-head group; the streams are cut into equal page shares
- * over the resident workgroups, and a stream cut into several pieces is
- * merged by a reduction pass (merge_gqa_chunks, qwen2.cpp:1469-1522).
+ * for its whole query-head group; the streams are laid end to end and cut
+ * into one share per resident workgroup (balanced by pages, per-piece cost
+ * and the workgroup's dispatch rank on its CU), and a stream cut into
+ * several pieces is merged by a reduction pass (merge_gqa_chunks,
+ * qwen2.cpp:1469-1522).
  * softmax scale = 1/sqrt(head_dim) (qwen2.cpp:1278). Requires
  * n_new*group <= 64 for every session.
  */
