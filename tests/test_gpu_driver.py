@@ -1,0 +1,200 @@
+"""GPU tests of the Qwen2-shaped KV driver (tge_qwen2_kv_*): the
+store-then-attend flows of Qwen2::forward / forward_batch / prefill_run /
+verify_draft / reset_cache (qwen2.cpp:2032-2095, 1613-1747, 2130-2335,
+2502-2577) over paged device memory, checked against the CPU oracle's flat
+cache, plus the driver's validation rules and page reuse order."""
+import math
+import sys
+
+import numpy as np
+import pytest
+
+import oracle as O
+import tge_kv as tk
+from _util import assert_attention_close
+
+pytestmark = pytest.mark.gpu
+
+
+def say(*a):
+    print(*a, flush=True)
+    sys.stdout.flush()
+
+
+class Model:
+    """A driver plus the host copy of every row it was given, per layer and
+    sequence, so the oracle can replay the same cache."""
+
+    def __init__(self, layers, qh, kvh, hd, fmt, sequences, pages, context=4096, seed=0,
+                 fragment=None):
+        self.layers, self.qh, self.kvh, self.hd, self.fmt = layers, qh, kvh, hd, fmt
+        self.m = tk.Qwen2KvPath(layers, qh, kvh, hd, context=context, sequences=sequences,
+                                pages=pages, fmt=fmt, scale_format=tk.SCALE_F16)
+        if fragment is not None:
+            self.m.table().fragment(fragment)
+        self.rng = np.random.default_rng(seed)
+        self.k = {}  # (layer, seq) -> rows in position order
+        self.v = {}
+
+    def rows(self, n):
+        kv_dim = self.kvh * self.hd
+        k = [self.rng.standard_normal((n, kv_dim), dtype=np.float32) for _ in range(self.layers)]
+        v = [self.rng.standard_normal((n, kv_dim), dtype=np.float32) for _ in range(self.layers)]
+        q = [self.rng.standard_normal((n, self.qh * self.hd), dtype=np.float32)
+             for _ in range(self.layers)]
+        return q, k, v
+
+    def keep(self, seq, start, k, v):
+        for l in range(self.layers):
+            old_k = self.k.get((l, seq), np.zeros((0, k[l].shape[1]), np.float32))
+            old_v = self.v.get((l, seq), np.zeros((0, v[l].shape[1]), np.float32))
+            assert old_k.shape[0] >= start
+            self.k[(l, seq)] = np.concatenate([old_k[:start], k[l]])
+            self.v[(l, seq)] = np.concatenate([old_v[:start], v[l]])
+
+    def run_layers(self, q, k, v, attend=True):
+        """Run every layer of the begun step; returns the outputs per layer."""
+        outs = []
+        for l in range(self.layers):
+            dk, dv = tk.DeviceArray.from_numpy(k[l]), tk.DeviceArray.from_numpy(v[l])
+            if attend:
+                dq = tk.DeviceArray.from_numpy(q[l])
+                dout = tk.DeviceArray(q[l].shape, np.float32).zero()
+                self.m.layer(l, dq, dk, dv, dout)
+                tk.hip().sync()
+                outs.append(dout.numpy())
+                dq.close()
+                dout.close()
+            else:
+                self.m.store(l, dk, dv)
+                tk.hip().sync()
+            dk.close()
+            dv.close()
+        return outs
+
+    def oracle(self, l, seq, q_rows, ctx):
+        fc = O.FlatCache({tk.KV_F16: O.F16, tk.KV_I8: O.I8}[self.fmt], self.k[(l, seq)],
+                         self.v[(l, seq)])
+        if self.fmt == tk.KV_I8:
+            fc.with_scales(O.half_to_float(O.float_to_half(fc.ks)),
+                           O.half_to_float(O.float_to_half(fc.vs)))
+        return fc.attend(q_rows, self.qh, self.kvh, self.hd, ctx)
+
+    def close(self):
+        self.m.close()
+
+
+@pytest.mark.parametrize("fmt", [tk.KV_F16, tk.KV_I8])
+def test_prefill_then_forward_matches_oracle(gpu, fmt):
+    """prefill_run of 100 tokens (block-prefill kernel), then forward of one
+    token (decode kernel), two layers, fragmented pool."""
+    say(f"driver prefill+forward fmt={fmt}")
+    md = Model(2, 14, 2, 64, fmt, sequences=2, pages=40, context=512, seed=1, fragment=5)
+    q, k, v = md.rows(100)
+    md.m.begin_prefill(0, 0, 100)
+    md.keep(0, 0, k, v)
+    outs = md.run_layers(q, k, v)
+    for l in range(2):
+        assert_attention_close(outs[l], md.oracle(l, 0, q[l], 0), f"prefill layer {l}")
+    assert md.m.length(0) == 100 and len(md.m.pages(0)) == 7
+    q, k, v = md.rows(1)
+    md.m.begin_forward(0, 100)
+    md.keep(0, 100, k, v)
+    outs = md.run_layers(q, k, v)
+    for l in range(2):
+        assert_attention_close(outs[l], md.oracle(l, 0, q[l], 100), f"forward layer {l}")
+    assert md.m.length(0) == 101 and len(md.m.pages(0)) == 7
+    md.close()
+
+
+def test_forward_batch_and_verify_match_oracle(gpu):
+    """forward_batch over two sequences (two rows for one, one for the
+    other), then verify_draft of 4 tokens (7B-like group of 7)."""
+    md = Model(1, 28, 4, 128, tk.KV_I8, sequences=3, pages=200, seed=2, fragment=9)
+    fills = {0: 300, 1: 47}
+    for s, n in fills.items():
+        _, k, v = md.rows(n)
+        md.m.begin_prefill(s, 0, n)
+        md.keep(s, 0, k, v)
+        md.run_layers(None, k, v, attend=False)
+    q, k, v = md.rows(3)
+    md.m.begin_forward_batch([300, 301, 47], [0, 0, 1])
+    md.keep(0, 300, [k[0][:2]], [v[0][:2]])
+    md.keep(1, 47, [k[0][2:]], [v[0][2:]])
+    out = md.run_layers(q, k, v)[0]
+    want = np.concatenate([md.oracle(0, 0, q[0][:2], 300), md.oracle(0, 1, q[0][2:], 47)])
+    assert_attention_close(out, want, "forward_batch")
+    assert md.m.length(0) == 302 and md.m.length(1) == 48
+    q, k, v = md.rows(4)
+    md.m.begin_verify(1, 48, 4)
+    md.keep(1, 48, k, v)
+    out = md.run_layers(q, k, v)[0]
+    assert_attention_close(out, md.oracle(0, 1, q[0], 48), "verify_draft")
+    # a verified draft can be rolled back: verifying again from 49 rewrites
+    # positions 49..52 (the store-then-attend order of verify_draft)
+    q, k, v = md.rows(4)
+    md.m.begin_verify(1, 49, 4)
+    md.keep(1, 49, k, v)
+    out = md.run_layers(q, k, v)[0]
+    assert_attention_close(out, md.oracle(0, 1, q[0], 49), "verify_draft again")
+    md.close()
+
+
+def test_reset_releases_pages_in_logical_order(gpu):
+    """reset_cache returns a sequence's pages in logical order, so the free
+    list hands them out again LIFO (last page first), exactly as the
+    reference BlockTable does (block_table.hpp:59-71)."""
+    md = Model(1, 14, 2, 64, tk.KV_F16, sequences=2, pages=16, seed=3)
+    orc = O.OracleBlockTable(16)
+    _, k, v = md.rows(40)
+    md.m.begin_prefill(0, 0, 40)
+    md.run_layers(None, k, v, attend=False)
+    want0 = [orc.allocate() for _ in range(3)]
+    assert md.m.pages(0) == want0
+    _, k, v = md.rows(20)
+    md.m.begin_prefill(1, 0, 20)
+    md.run_layers(None, k, v, attend=False)
+    want1 = [orc.allocate() for _ in range(2)]
+    assert md.m.pages(1) == want1
+    md.m.reset(0)
+    for p in want0:
+        orc.release(p)
+    assert md.m.length(0) == 0 and md.m.pages(0) == []
+    assert md.m.free_pages() == orc.free_count()
+    _, k, v = md.rows(30)
+    md.m.begin_prefill(1, 20, 30)
+    md.run_layers(None, k, v, attend=False)
+    want1 += [orc.allocate() for _ in range(2)]
+    assert md.m.pages(1) == want1
+    assert want1[2:] == [want0[2], want0[1]]
+    md.close()
+
+
+def test_driver_validation(gpu):
+    """Misuse is rejected with the reference's error class and leaves the
+    model unchanged."""
+    md = Model(2, 14, 2, 64, tk.KV_F16, sequences=2, pages=8, context=100, seed=4)
+    L = tk.lib()
+    h = md.m.h
+
+    def status(f):
+        with pytest.raises(tk.TgeError) as e:
+            f()
+        return e.value.status
+
+    assert status(lambda: md.m.begin_forward(0, 100)) == tk.ERR_RUNTIME     # beyond context
+    assert status(lambda: md.m.begin_forward(2, 0)) == tk.ERR_RUNTIME       # no such sequence
+    assert status(lambda: md.m.begin_forward(0, 5)) == tk.ERR_RUNTIME       # leaves a gap
+    assert status(lambda: md.m.begin_verify(0, 0, 7)) == tk.ERR_RUNTIME     # > 6 drafts
+    assert status(lambda: md.m.begin_forward_batch([0, 2], [0, 0])) == tk.ERR_RUNTIME
+    assert status(lambda: md.m.begin_prefill(0, 90, 20)) == tk.ERR_RUNTIME  # past context
+    assert L.tge_qwen2_kv_layer(h, 0, None, None, None, None, None) == tk.ERR_RUNTIME
+    # the pool has 8 pages = 128 positions: 2 x 70 does not fit
+    _, k, v = md.rows(70)
+    md.m.begin_prefill(0, 0, 70)
+    md.run_layers(None, k, v, attend=False)
+    assert status(lambda: md.m.begin_prefill(1, 0, 70)) == tk.ERR_RUNTIME   # table full
+    assert md.m.length(1) == 0 and md.m.length(0) == 70 and md.m.free_pages() == 3
+    md.m.begin_forward(0, 70)
+    assert L.tge_qwen2_kv_layer(h, 5, None, None, None, None, None) == tk.ERR_INVALID
+    md.close()
