@@ -226,6 +226,22 @@ __device__ __forceinline__ void wait_vmcnt() {
   __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | (7 << 4) | (15 << 8));
 }
 
+// wait_vmcnt<n * LOADS> for a wave-uniform n in [0, MAXN]: all but this
+// wave's n most recently issued pages have landed.
+template <int MAXN, int LOADS>
+__device__ __forceinline__ void wait_vmcnt_pages(int n) {
+  static_assert(MAXN <= 3, "up to three pages in flight");
+  if (MAXN >= 3 && n >= 3) {
+    wait_vmcnt<(MAXN >= 3 ? 3 : 0) * LOADS>();
+  } else if (MAXN >= 2 && n == 2) {
+    wait_vmcnt<(MAXN >= 2 ? 2 : 0) * LOADS>();
+  } else if (MAXN >= 1 && n == 1) {
+    wait_vmcnt<(MAXN >= 1 ? 1 : 0) * LOADS>();
+  } else {
+    wait_vmcnt<0>();
+  }
+}
+
 // K operand (16x16x32 A) of 32-dim block pp.
 template <int FMT, bool SF32, int D>
 __device__ __forceinline__ half8_t k_operand(const PageRegs<FMT, SF32, D>& r, int pp) {
@@ -897,6 +913,158 @@ void paged_decode_kernel(AttnParams p) {
   }
 }
 
+// ---------------------------------------------------------------------------
+// Block-prefill kernel: one workgroup per (session, KV head, query tile,
+// page split). The tile holds up to 128 rows, (query, head) pairs of the KV
+// head's query group in query-major order; wave w owns rows [32w, 32w+32).
+// The waves share the pages instead of splitting them: each iteration every
+// wave fetches one page of a four-page tile into a shared LDS ring, and after
+// one barrier all four waves run their own rows against all four pages. Rows
+// never meet across waves, so each wave writes its rows (or its split's
+// partial) directly.
+// ---------------------------------------------------------------------------
+template <int FMT, bool SF32, int D, int WPE>
+struct PrefillShared {
+  static constexpr int SLOT = Ring<FMT, SF32, D>::SLOT;
+  static constexpr int TILE = kWaves * SLOT;  // four pages
+  static constexpr int NB_FIT = (160 * 1024 / WPE - 64) / TILE;
+  static constexpr int NB = NB_FIT > 4 ? 4 : NB_FIT;
+  static_assert(NB >= 2, "the prefill ring needs two tiles");
+  alignas(16) char ring[NB * TILE];
+};
+
+template <int FMT, bool SF32, int D, bool QSPLIT, int WPE>
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(WPE, WPE)))
+void paged_prefill_kernel(AttnParams p) {
+  constexpr int NRG = 2;  // 32 rows per wave
+  using SH = PrefillShared<FMT, SF32, D, WPE>;
+  using U = Unit<FMT, SF32, D, NRG, QSPLIT>;
+  using Regs = typename U::Regs;
+  using RG = Ring<FMT, SF32, D>;
+  constexpr int NB = SH::NB;
+  constexpr int NP = D / 32;
+  constexpr int NT = D / 16;
+  __shared__ SH sh;
+
+  const WorkRec w = load_work((const sconst_work*)p.work + blockIdx.x);
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int col = lane & 15;
+  const int grp = lane >> 4;
+  const int q_stride = p.q_heads * D;
+  const int row0 = wave * 32;
+  const bool has_rows = row0 < w.rows;
+
+  LayerRsrc rs;
+  rs.k = make_rsrc(p.kpool, p.kv_array_bytes);
+  rs.v = make_rsrc(p.vpool, p.kv_array_bytes);
+
+  // This wave's rows: Q^T operands (as in attend_unit) and visible limits.
+  U u;
+#pragma unroll
+  for (int rg = 0; rg < NRG; ++rg) {
+    const int r = row0 + rg * 16 + col;
+    const bool valid = r < w.rows;
+    const int qi = w.row_begin + (valid ? r / w.rows_per_query : 0);
+    const int head = w.head_base + (valid ? r % w.rows_per_query : 0);
+    const float* qp = p.q + (size_t)(w.q_row + qi) * q_stride + (size_t)head * D + 4 * grp;
+#pragma unroll
+    for (int pp = 0; pp < NP; ++pp) {
+      float4 a = make_float4(0, 0, 0, 0), b = make_float4(0, 0, 0, 0);
+      if (valid) {
+        a = *reinterpret_cast<const float4*>(qp + 32 * pp);
+        b = *reinterpret_cast<const float4*>(qp + 32 * pp + 16);
+      }
+      const float c = p.scale_log2;
+      const float x[8] = {a.x * c, a.y * c, a.z * c, a.w * c, b.x * c, b.y * c, b.z * c, b.w * c};
+#pragma unroll
+      for (int j = 0; j < 8; ++j) {
+        const _Float16 hi = (_Float16)x[j];
+        u.qhi[rg][pp][j] = hi;
+        u.qlo[rg][pp][j] = QSPLIT ? (_Float16)(x[j] - (float)hi) : (_Float16)0.0f;
+      }
+    }
+    u.lim[rg] = valid ? w.ctx + w.row_begin + r / w.rows_per_query : -1;
+    u.base[rg] = 0.0f;
+    u.thr[rg] = -INFINITY;
+    u.l4[rg] = float4_t{0, 0, 0, 0};
+#pragma unroll
+    for (int t = 0; t < NT; ++t) u.o[rg][t] = float4_t{0, 0, 0, 0};
+  }
+  // Pages at or past `unmasked` hold a position some row of the wave may not see.
+  const int unmasked = (w.ctx + w.row_begin + row0 / w.rows_per_query + 1) / 16;
+
+  const int npages = w.page_end - w.page_begin;
+  const int ntiles = (npages + kWaves - 1) / kWaves;
+  const sconst_int* table = (const sconst_int*)(p.tables + w.table_off + w.page_begin);
+  // Tile k, page `wave` of it: fetched by this wave (nothing past the range).
+  auto fetch_tile = [&](int k) __attribute__((always_inline)) -> void {
+    const int j = k * kWaves + wave;
+    if (j < npages) {
+      fetch_page<FMT, SF32, D>(sh.ring + (k % NB) * SH::TILE + wave * RG::SLOT, rs, p,
+                               table[j] * p.kv_heads + w.kv_head, lane);
+    }
+  };
+#pragma unroll
+  for (int k = 0; k < NB - 1; ++k) {
+    if (k < ntiles) fetch_tile(k);
+  }
+  // Last tile holding a page of this wave.
+  const int t_last = wave < npages ? (npages - 1 - wave) / kWaves : -1;
+  for (int k = 0; k < ntiles; ++k) {
+    // this wave's page of tile k has landed (its pages of up to NB - 2
+    // younger tiles may still be in flight), then every wave's has, and
+    // every wave is done with tile k - 1, whose slot the fetch below refills
+    if (k <= t_last) {
+      const int younger = (k + NB - 2 < t_last ? k + NB - 2 : t_last) - k;
+      wait_vmcnt_pages<NB - 2, RG::LOADS>(younger);
+    }
+    lds_barrier();
+    if (k + NB - 1 < ntiles) fetch_tile(k + NB - 1);
+    if (has_rows) {
+      const char* tile = sh.ring + (k % NB) * SH::TILE;
+#pragma unroll
+      for (int j = 0; j < kWaves; ++j) {
+        const int pg = k * kWaves + j;
+        if (pg < npages) {
+          Regs r;
+          read_page<FMT, SF32, D>(r, tile + j * RG::SLOT, lane, grp);
+          const int pi = w.page_begin + pg;
+          u.consume(r, pi, grp, pi >= unmasked);
+        }
+      }
+    }
+  }
+  if (!has_rows) return;
+
+  // Write this wave's rows: normalised output, or the split's partial state.
+#pragma unroll
+  for (int rg = 0; rg < NRG; ++rg) {
+    const int r = row0 + rg * 16 + col;
+    if (r >= w.rows) continue;
+    const float sum = u.l4[rg][0];
+    if (w.part < 0) {
+      const int qi = w.row_begin + r / w.rows_per_query;
+      const int head = w.head_base + r % w.rows_per_query;
+      float* op = p.out + (size_t)(w.q_row + qi) * q_stride + (size_t)head * D + 4 * grp;
+#pragma unroll
+      for (int t = 0; t < NT; ++t) {
+        float4_t res = float4_t{0, 0, 0, 0};
+        if (sum > 0.0f) res = div4(u.o[rg][t], sum);
+        *reinterpret_cast<float4_t*>(op + 16 * t) = res;
+      }
+    } else {
+      float* po = p.part_o + ((size_t)w.part * p.rows_cap + r) * D + 4 * grp;
+#pragma unroll
+      for (int t = 0; t < NT; ++t) *reinterpret_cast<float4_t*>(po + 16 * t) = u.o[rg][t];
+      if (grp == 0) {
+        p.part_ml[((size_t)w.part * p.rows_cap + r) * 2] = u.thr[rg] == -INFINITY ? -INFINITY : u.base[rg];
+        p.part_ml[((size_t)w.part * p.rows_cap + r) * 2 + 1] = sum;
+      }
+    }
+  }
+}
+
 // Merge the partial states of the splits of one unit (merge_gqa_chunks:
 // splits with no visible position are skipped, none at all gives zeros).
 // A row's D/4 lanes (4 dims each) are replicated over S slots; slot j folds
@@ -988,74 +1156,7 @@ __global__ __launch_bounds__(256) void split_reduce_kernel(ReduceParams p) {
   *reinterpret_cast<float4_t*>(p.out + (size_t)(s.q_row + qi) * q_stride + (size_t)head * D + 4 * d4) = res;
 }
 
-template <int FMT, bool SF32, int D, bool QSPLIT>
-hipError_t launch_rg(int row_groups, int n_work, const AttnParams& p, hipStream_t stream) {
-  const dim3 grid((unsigned)n_work), block(256);
-  switch (row_groups) {
-#define TGE_RG(n)                                                                          \
-  case n:                                                                                  \
-    hipLaunchKernelGGL((paged_attention_kernel<FMT, SF32, D, n, QSPLIT, waves_per_eu<FMT, D, n, QSPLIT>()>), \
-                       grid, block, 0, stream, p);                                         \
-    break;
-    TGE_RG(1)
-    TGE_RG(2)
-    TGE_RG(3)
-    TGE_RG(4)
-#undef TGE_RG
-    default: return hipErrorInvalidValue;
-  }
-  return hipGetLastError();
-}
-
-template <int FMT, bool SF32, bool QSPLIT>
-hipError_t launch_d(int head_dim, int row_groups, int n_work, const AttnParams& p, hipStream_t stream) {
-  if (head_dim == 64) return launch_rg<FMT, SF32, 64, QSPLIT>(row_groups, n_work, p, stream);
-  if (head_dim == 128) return launch_rg<FMT, SF32, 128, QSPLIT>(row_groups, n_work, p, stream);
-  return hipErrorInvalidValue;
-}
-
 }  // namespace
-
-hipError_t launch_attention(int format, int scale_f32, int head_dim, int row_groups, bool qsplit,
-                            int n_work, const AttnParams& p, hipStream_t stream) {
-  if (n_work == 0) return hipSuccess;
-  if (format == kF16) {
-    return qsplit ? launch_d<kF16, false, true>(head_dim, row_groups, n_work, p, stream)
-                  : launch_d<kF16, false, false>(head_dim, row_groups, n_work, p, stream);
-  }
-  if (!qsplit) return hipErrorInvalidValue;
-  return scale_f32 ? launch_d<kI8, true, true>(head_dim, row_groups, n_work, p, stream)
-                   : launch_d<kI8, false, true>(head_dim, row_groups, n_work, p, stream);
-}
-
-template <int FMT, bool SF32, int D, bool QSPLIT>
-int blocks_rg(int row_groups) {
-  int n = 0;
-  hipError_t e = hipErrorInvalidValue;
-  switch (row_groups) {
-#define TGE_OCC(r)                                                                           \
-  case r:                                                                                    \
-    e = hipOccupancyMaxActiveBlocksPerMultiprocessor(                                        \
-        &n, paged_attention_kernel<FMT, SF32, D, r, QSPLIT, waves_per_eu<FMT, D, r, QSPLIT>()>, \
-        256, 0);                                                                             \
-    break;
-    TGE_OCC(1)
-    TGE_OCC(2)
-    TGE_OCC(3)
-    TGE_OCC(4)
-#undef TGE_OCC
-  }
-  return e == hipSuccess ? n : 0;
-}
-
-int attention_blocks_per_cu(int format, int scale_f32, int head_dim, int row_groups, bool qsplit) {
-  if (format == kF16) {
-    if (head_dim == 64) return qsplit ? blocks_rg<kF16, false, 64, true>(row_groups) : blocks_rg<kF16, false, 64, false>(row_groups);
-    return qsplit ? blocks_rg<kF16, false, 128, true>(row_groups) : blocks_rg<kF16, false, 128, false>(row_groups);
-  }
-  if (head_dim == 64) return scale_f32 ? blocks_rg<kI8, true, 64, true>(row_groups) : blocks_rg<kI8, false, 64, true>(row_groups);
-  return scale_f32 ? blocks_rg<kI8, true, 128, true>(row_groups) : blocks_rg<kI8, false, 128, true>(row_groups);
-}
 
 // Whether a variant's decode ring (two or more slots per wave) and merge
 // area fit its share of LDS; the others run the unit-at-a-time kernel.
@@ -1149,6 +1250,35 @@ int decode_blocks_per_cu(int format, int scale_f32, int head_dim, int row_groups
   return scale_f32 ? decode_blocks_d<kI8, true, 128>(row_groups) : decode_blocks_d<kI8, false, 128>(row_groups);
 }
 
+template <int FMT, bool SF32, int D, bool QSPLIT>
+hipError_t launch_prefill_d(int n_units, const AttnParams& p, hipStream_t stream) {
+  constexpr int wpe = waves_per_eu<FMT, D, 2, QSPLIT>();
+  hipLaunchKernelGGL((paged_prefill_kernel<FMT, SF32, D, QSPLIT, wpe>), dim3((unsigned)n_units),
+                     dim3(256), 0, stream, p);
+  return hipGetLastError();
+}
+
+hipError_t launch_prefill(int format, int scale_f32, int head_dim, bool qsplit, int n_units,
+                          const AttnParams& p, hipStream_t stream) {
+  if (n_units <= 0) return hipSuccess;
+  if (format == kF16) {
+    if (head_dim == 64)
+      return qsplit ? launch_prefill_d<kF16, false, 64, true>(n_units, p, stream)
+                    : launch_prefill_d<kF16, false, 64, false>(n_units, p, stream);
+    if (head_dim == 128)
+      return qsplit ? launch_prefill_d<kF16, false, 128, true>(n_units, p, stream)
+                    : launch_prefill_d<kF16, false, 128, false>(n_units, p, stream);
+  } else if (format == kI8 && qsplit) {
+    if (head_dim == 64)
+      return scale_f32 ? launch_prefill_d<kI8, true, 64, true>(n_units, p, stream)
+                       : launch_prefill_d<kI8, false, 64, true>(n_units, p, stream);
+    if (head_dim == 128)
+      return scale_f32 ? launch_prefill_d<kI8, true, 128, true>(n_units, p, stream)
+                       : launch_prefill_d<kI8, false, 128, true>(n_units, p, stream);
+  }
+  return hipErrorInvalidValue;
+}
+
 template <int D>
 hipError_t launch_reduce_d(int n_items, int max_parts, const ReduceParams& p, hipStream_t stream) {
   // Slots per row: about one per 4 splits, at most 8.
@@ -1172,6 +1302,5 @@ hipError_t launch_reduce(int head_dim, int n_items, int max_parts, const ReduceP
   if (head_dim == 128) return launch_reduce_d<128>(n_items, max_parts, p, stream);
   return hipErrorInvalidValue;
 }
-
 
 }  // namespace tge

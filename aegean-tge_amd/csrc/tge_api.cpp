@@ -525,7 +525,11 @@ void build_decode(tge_batch* b, Residency res) {
   pl.groups = (int)pl.wg_first.size() - 1;
 }
 
-// Prefill units: (session, query head, 32-query tile) x splits of 64 pages.
+// Prefill units: (session, KV head, query tile) x page splits. A tile takes
+// as many whole queries as fit 128 rows of (query, head) pairs of the KV
+// head's query group, so every K/V page a tile reads serves the whole group.
+// Long spans are split so the launch has work for every CU; items are
+// ordered longest first.
 void build_prefill(tge_batch* b) {
   AttnPlan& pl = b->prefill;
   pl.work.clear();
@@ -533,28 +537,40 @@ void build_prefill(tge_batch* b) {
   pl.wg_first.clear();
   pl.groups = 0;
   pl.parts = pl.max_splits = 0;
-  pl.row_groups = 2;
-  const int tile = 16 * pl.row_groups;
-  const int pps = 64;
+  pl.row_groups = tge::kPrefillRows / 16;
+  const int tq = std::max(1, tge::kPrefillRows / b->group);
+  // Page-split size: enough items for about two rounds of two workgroups
+  // on each of 256 CUs, at least 32 pages (eight tiles of four).
+  long pages_total = 0;
+  for (const auto& sr : b->sessions) {
+    for (int a = 0; a < sr.n_new; a += tq)
+      pages_total += (long)((sr.ctx + std::min(sr.n_new, a + tq) + 15) / 16) * b->kv_heads;
+  }
+  const long target_units = 2L * 256 * 2;
+  const int pps = (int)std::max<long>(32, ((pages_total + target_units - 1) / target_units + 3) / 4 * 4);
   for (int s = 0; s < (int)b->sessions.size(); ++s) {
     const tge::SessionRec& sr = b->sessions[s];
-    for (int hq = 0; hq < b->q_heads; ++hq) {
-      for (int a = 0; a < sr.n_new; a += tile) {
+    for (int h = 0; h < b->kv_heads; ++h) {
+      for (int a = 0; a < sr.n_new; a += tq) {
         tge::WorkRec w{};
         w.session = s;
-        w.kv_head = hq / b->group;
+        w.kv_head = h;
         w.ctx = sr.ctx;
         w.q_row = sr.q_row;
         w.table_off = sr.table_off;
         w.row_begin = a;
-        w.rows = std::min(tile, sr.n_new - a);
-        w.rows_per_query = 1;
-        w.head_base = hq;
-        const int pages = (sr.ctx + a + w.rows + 15) / 16;
+        w.rows = std::min(tq, sr.n_new - a) * b->group;
+        w.rows_per_query = b->group;
+        w.head_base = h * b->group;
+        const int pages = (sr.ctx + a + std::min(tq, sr.n_new - a) + 15) / 16;
         add_units(pl.work, pl.reduce, pl.parts, pl.max_splits, w, pages, pps);
       }
     }
   }
+  // Longest items first (partial slots are fixed per item, so order is free).
+  std::stable_sort(pl.work.begin(), pl.work.end(), [](const tge::WorkRec& x, const tge::WorkRec& y) {
+    return x.page_end - x.page_begin > y.page_end - y.page_begin;
+  });
 }
 
 }  // namespace
@@ -749,8 +765,8 @@ int run_attention(const tge_batch* b, const tge_kv_pool* p, int layer, const flo
     TGE_HIP(tge::launch_decode(p->desc.format, p->desc.scale_format == TGE_SCALE_F32, b->head_dim,
                                pl.row_groups, pl.groups, a, st));
   } else {
-    TGE_HIP(tge::launch_attention(p->desc.format, p->desc.scale_format == TGE_SCALE_F32,
-                                  b->head_dim, pl.row_groups, qsplit, pl.groups, a, st));
+    TGE_HIP(tge::launch_prefill(p->desc.format, p->desc.scale_format == TGE_SCALE_F32,
+                                b->head_dim, qsplit, (int)pl.work.size(), a, st));
   }
   if (ev) TGE_HIP(hipEventRecord((*ev)[1], st));
   if (!pl.reduce.empty()) {

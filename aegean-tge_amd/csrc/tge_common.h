@@ -9,7 +9,8 @@ namespace tge {
 
 constexpr int kPageTokens = 16;  // block_table.hpp:19 kBlockTokens
 constexpr int kWaves = 4;        // waves per decode workgroup
-constexpr int kMaxRows = 64;     // query rows (n_new * group) per decode unit
+constexpr int kMaxRows = 64;
+constexpr int kPrefillRows = 128;  // rows of one block-prefill work item (4 waves x 32)     // query rows (n_new * group) per decode unit
 
 enum Format { kF16 = 1, kI8 = 2 };
 

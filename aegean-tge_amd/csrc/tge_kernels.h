@@ -71,21 +71,16 @@ struct ReduceParams {
 
 hipError_t launch_kv_append(int format, const AppendParams& p, hipStream_t stream);
 hipError_t launch_kv_gather(int format, const GatherParams& p, hipStream_t stream);
-// row_groups: 16-row groups per unit (1..4). qsplit: Q as f16 hi + lo.
-// n_groups workgroups; with p.wg_first set each runs a range of the items.
-hipError_t launch_attention(int format, int scale_f32, int head_dim, int row_groups,
-                            bool qsplit, int n_groups, const AttnParams& p,
-                            hipStream_t stream);
 // Decode attention over a balanced plan (p.wg_first required): n_groups
 // persistent workgroups of four waves.
 hipError_t launch_decode(int format, int scale_f32, int head_dim, int row_groups, int n_groups,
                          const AttnParams& p, hipStream_t stream);
+// Block prefill: one workgroup per work item (tiles of up to 128 rows).
+hipError_t launch_prefill(int format, int scale_f32, int head_dim, bool qsplit, int n_units,
+                          const AttnParams& p, hipStream_t stream);
 // Resident decode workgroups per CU.
 int decode_blocks_per_cu(int format, int scale_f32, int head_dim, int row_groups);
 hipError_t launch_reduce(int head_dim, int n_items, int max_parts, const ReduceParams& p,
                          hipStream_t stream);
-// Resident 256-thread workgroups per CU of one attention variant (0 if the
-// query fails).
-int attention_blocks_per_cu(int format, int scale_f32, int head_dim, int row_groups, bool qsplit);
 
 }  // namespace tge

@@ -239,6 +239,9 @@ def run_prefill(tk, synth, cfg, reps=3):
     hip = tk.hip()
     ch = cfg.prefill_chunk
     per_chunk = np.zeros(n // ch)
+    kern_us = np.zeros(n // ch)   # block-prefill kernel alone, per layer
+    merge_us = np.zeros(n // ch)
+    lib = tk.lib()
     for r in range(reps + 1):
         model.reset(0)
         for c in range(n // ch):
@@ -251,14 +254,34 @@ def run_prefill(tk, synth, cfg, reps=3):
             hip.sync()
             if r:
                 per_chunk[c] += time.perf_counter() - t0
+                # the kernels of one layer-chunk, timed on their own (back to back)
+                batch, pool = model.batch_handle(), model.pool_handle()
+                tk.check(lib.tge_batch_set_profiling(batch, 1))
+                for layer in range(L):
+                    tk.check(lib.tge_prefill_attention(batch, pool, layer,
+                                                       q.ptr + c * ch * sh.q_dim * 4,
+                                                       out.ptr + c * ch * sh.q_dim * 4, None))
+                n_calls, a_us, m_us = C.c_int(), C.c_float(), C.c_float()
+                tk.check(lib.tge_batch_kernel_times(batch, C.byref(n_calls), C.byref(a_us),
+                                                    C.byref(m_us)))
+                tk.check(lib.tge_batch_set_profiling(batch, 0))
+                kern_us[c] += a_us.value / n_calls.value
+                merge_us[c] += m_us.value / n_calls.value
     per_chunk /= reps
+    kern_us /= reps
+    merge_us /= reps
     flops = [synth.prefill_flops(sh, c * ch, ch) * L for c in range(n // ch)]
     total_s = float(per_chunk.sum())
     tflops = sum(flops) / total_s / 1e12
+    kern_tflops = sum(flops) / (float(kern_us.sum()) * L * 1e-6) / 1e12
     res = {
         "us_per_layer_chunk": [1e6 * t / L for t in per_chunk],
         "tflops": tflops,
         "mfma_util": tflops / MFMA_F16_PEAK_TFLOPS,
+        "attn_kernel_us_per_chunk": [float(x) for x in kern_us],
+        "merge_kernel_us_per_chunk": [float(x) for x in merge_us],
+        "attn_kernel_tflops": kern_tflops,
+        "attn_kernel_mfma_util": kern_tflops / MFMA_F16_PEAK_TFLOPS,
         "prompt_ms": 1e3 * total_s,
         "tokens_per_s": n / total_s,
     }
