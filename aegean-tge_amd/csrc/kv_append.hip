@@ -40,8 +40,7 @@ __global__ __launch_bounds__(256) void kv_append_kernel(AppendParams p) {
     x[4 * i + 2] = f.z;
     x[4 * i + 3] = f.w;
   }
-  const size_t block = (size_t)rr.page * p.kv_heads + h;
-  const size_t elems = (size_t)16 * p.head_dim;
+  char* const blk = static_cast<char*>(p.pool) + ((size_t)rr.page * p.kv_heads + h) * p.geom.block_bytes;
   const int t = rr.slot;
 
   if (FMT == kF16) {
@@ -49,7 +48,7 @@ __global__ __launch_bounds__(256) void kv_append_kernel(AppendParams p) {
 #pragma unroll
     for (int i = 0; i < 32; ++i) hx[i] = float_to_half_ref(x[i]);
     if (which == 0) {
-      uint16_t* dst = static_cast<uint16_t*>(p.kpool) + block * elems;
+      uint16_t* dst = reinterpret_cast<uint16_t*>(blk);
 #pragma unroll
       for (int g = 0; g < 4; ++g) {
         uint4 w;
@@ -60,7 +59,7 @@ __global__ __launch_bounds__(256) void kv_append_kernel(AppendParams p) {
         *reinterpret_cast<uint4*>(dst + k_index_np(t, 32 * b + 4 * g, nb)) = w;
       }
     } else {
-      uint16_t* dst = static_cast<uint16_t*>(p.vpool) + block * elems;
+      uint16_t* dst = reinterpret_cast<uint16_t*>(blk + p.geom.v_off());
 #pragma unroll
       for (int d = 0; d < 32; ++d) dst[v_index_np(t, 32 * b + d, nb)] = hx[d];
     }
@@ -68,7 +67,7 @@ __global__ __launch_bounds__(256) void kv_append_kernel(AppendParams p) {
     int8_t c[32];
     const float scale = quantize_block_ref(x, c);
     if (which == 0) {
-      int8_t* dst = static_cast<int8_t*>(p.kpool) + block * elems;
+      int8_t* dst = reinterpret_cast<int8_t*>(blk);
 #pragma unroll
       for (int g = 0; g < 4; ++g) {
         uint2 w;
@@ -80,16 +79,15 @@ __global__ __launch_bounds__(256) void kv_append_kernel(AppendParams p) {
         *reinterpret_cast<uint2*>(dst + k_index_np(t, 32 * b + 4 * g, nb)) = w;
       }
     } else {
-      int8_t* dst = static_cast<int8_t*>(p.vpool) + block * elems;
+      int8_t* dst = reinterpret_cast<int8_t*>(blk + p.geom.v_off());
 #pragma unroll
       for (int d = 0; d < 32; ++d) dst[v_index_np(t, 32 * b + d, nb)] = c[d];
     }
-    const size_t sblock = block * (size_t)(16 * nb);
-    void* sp = which ? p.vscale : p.kscale;
+    char* sp = blk + (which ? p.geom.vs_off() : p.geom.ks_off());
     if (p.scale_f32) {
-      static_cast<float*>(sp)[sblock + scale_index_np(t, b, nb)] = scale;
+      reinterpret_cast<float*>(sp)[scale_index_np(t, b, nb)] = scale;
     } else {
-      static_cast<uint16_t*>(sp)[sblock + scale_index_np(t, b, nb)] = float_to_half_ref(scale);
+      reinterpret_cast<uint16_t*>(sp)[scale_index_np(t, b, nb)] = float_to_half_ref(scale);
     }
   }
 }
@@ -106,19 +104,20 @@ __global__ __launch_bounds__(256) void kv_gather_kernel(GatherParams p) {
   const int h = c / p.head_dim, d = c % p.head_dim;
   const int page = p.table[pos >> 4], t = pos & 15;
   const int np = p.head_dim >> 5;
-  const size_t block = ((size_t)page * p.kv_heads + h) * (size_t)(16 * p.head_dim);
-  static_cast<T*>(p.k_rows)[idx] = static_cast<const T*>(p.kpool)[block + k_index_np(t, d, np)];
-  static_cast<T*>(p.v_rows)[idx] = static_cast<const T*>(p.vpool)[block + v_index_np(t, d, np)];
+  const char* blk = static_cast<const char*>(p.pool) + ((size_t)page * p.kv_heads + h) * p.geom.block_bytes;
+  static_cast<T*>(p.k_rows)[idx] = reinterpret_cast<const T*>(blk)[k_index_np(t, d, np)];
+  static_cast<T*>(p.v_rows)[idx] = reinterpret_cast<const T*>(blk + p.geom.v_off())[v_index_np(t, d, np)];
   if (p.k_scales && (d & 31) == 0) {
-    const size_t sb = ((size_t)page * p.kv_heads + h) * (size_t)(16 * (p.head_dim >> 5));
     const size_t o = (size_t)pos * (kv_dim >> 5) + (c >> 5);
     const int si = scale_index_np(t, d >> 5, np);
+    const char* ks = blk + p.geom.ks_off();
+    const char* vs = blk + p.geom.vs_off();
     if (p.scale_bytes == 4) {
-      static_cast<float*>(p.k_scales)[o] = static_cast<const float*>(p.kscale)[sb + si];
-      static_cast<float*>(p.v_scales)[o] = static_cast<const float*>(p.vscale)[sb + si];
+      static_cast<float*>(p.k_scales)[o] = reinterpret_cast<const float*>(ks)[si];
+      static_cast<float*>(p.v_scales)[o] = reinterpret_cast<const float*>(vs)[si];
     } else {
-      static_cast<uint16_t*>(p.k_scales)[o] = static_cast<const uint16_t*>(p.kscale)[sb + si];
-      static_cast<uint16_t*>(p.v_scales)[o] = static_cast<const uint16_t*>(p.vscale)[sb + si];
+      static_cast<uint16_t*>(p.k_scales)[o] = reinterpret_cast<const uint16_t*>(ks)[si];
+      static_cast<uint16_t*>(p.v_scales)[o] = reinterpret_cast<const uint16_t*>(vs)[si];
     }
   }
 }

@@ -1,6 +1,6 @@
 // Paged GQA attention on CDNA4 matrix cores: decode (one or a few new tokens
 // per session, split-K over long contexts) and chunked prefill (a query tile
-// against every prior page) share one workgroup kernel.
+// against every prior page).
 //
 // Reference semantics (AegeanWorks/Aegean-TGE):
 //   per-head oracle      attention_scalar.cpp:48-115
@@ -11,34 +11,31 @@
 // out = softmax(q.K^T / sqrt(D)) V with fp32 accumulation; query i of a
 // session sees positions 0 .. ctx+i.
 //
-// Work unit (one 256-thread workgroup = 4 waves): one session, one KV head,
-// up to 16*NRG query rows, a range of logical pages. Rows are (query, head)
-// pairs: decode packs the whole GQA group of every new token into the rows
-// (each K/V page is fetched once for the group), prefill packs 16*NRG
-// consecutive queries of one head. Wave w takes pages w, w+4, ... of the
-// range. Each lane owns one contiguous chunk of every page block (see the
-// layout in tge_common.h) and fetches it with 16-byte loads; the next page
-// is fetched while the current one is consumed, and page ids come in
-// batches of 64 (one per lane, then readlane). The Q^T operands (f16 hi +
-// lo) sit in LDS, so the accumulators, the two page register sets and the
-// softmax state fit the architectural VGPRs at two waves per SIMD.
+// Work unit: one session, one KV head, up to 16*NRG query rows, a range of
+// logical pages. Rows are (query, head) pairs: decode packs the whole GQA
+// group of every new token into the rows (each K/V page block is fetched
+// once for the group), prefill packs the query group of consecutive
+// queries. A page block (16 tokens of one KV head: K, V and int8 scales, one
+// contiguous run of HBM) is fetched straight into LDS by 16-byte
+// buffer_load ... lds instructions, one contiguous chunk per lane (layout in
+// tge_common.h), and read back into the lane's MFMA operand registers.
 //
 // Per page, per 16-row group, per wave (lane = group g 0..3, column c 0..15):
 //   S^T[token][row] = K (16 x D) . Q^T: one v_mfma_f32_16x16x32_f16 per 32-dim
-//     block (two with Q split into f16 hi + lo for fp32-grade scores);
+//     block (prefill of int8 pools: two, with Q split into f16 hi + lo);
 //     int8 codes are exact in f16 and the block's per-token scale multiplies
 //     the block's fp32 partial score. Lane (g, c) then holds row c,
 //     tokens 4g..4g+3.
-//   online softmax per row in the log2 domain; the reference maximum only
-//     moves when a score exceeds it by more than 2^8, so the accumulators
-//     are rescaled rarely (weights stay <= 256, exact enough in f16).
+//   online softmax per row in the log2 domain; the row base only moves when
+//     a score exceeds it by more than 2^8, so the accumulators are rescaled
+//     rarely (weights stay <= 256, exact enough in f16).
 //   O^T[dim][row] += V^T (D x 16) . P^T: v_mfma_f32_16x16x16_f16 per 16-dim
 //     tile; lane (g, c) holds row c, dims 16j+4g..+3, the same row as its
 //     softmax state. int8 V is dequantised in f16 (exact code times the f16
 //     scale, one rounding).
-// The 4 waves merge through LDS in a fixed order (deterministic output);
-// units of a split context write partial (max, sum, acc) for the reduction
-// kernel.
+// Waves that shared a unit merge through LDS in a fixed order (the output
+// is bit-reproducible); units of a split context write partial
+// (max, sum, acc) for the reduction kernel.
 #include <math.h>
 
 #include "tge_common.h"
@@ -107,21 +104,15 @@ struct PageRegs {
   uint32_t vs[SW > 0 ? SW : 1];
 };
 
-// Buffer resources of one layer's K, V and scale arrays. Loads address a
-// page block with a wave-uniform byte offset (SGPR) plus the lane's fixed
-// chunk offset (VGPR); offsets past the end of an array read zeros instead
-// of faulting.
-struct LayerRsrc {
-  __amdgpu_buffer_rsrc_t k, v;
-};
-
+// Buffer resource of one layer's block array. Loads address a page block with
+// a wave-uniform byte offset (SGPR) plus the lane's fixed chunk offset
+// (VGPR); offsets past the end of the array read zeros instead of faulting.
 __device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void* base, uint32_t bytes) {
   return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), (short)0, (int)bytes,
                                            0x00020000);
 }
 
 typedef __attribute__((address_space(3))) void lds_void_t;
-typedef const __attribute__((address_space(1))) void global_void_t;
 typedef const __attribute__((address_space(4))) int sconst_int;  // scalar (constant) loads
 
 // Per-wave LDS ring of page slots filled by direct-to-LDS loads. A slot
@@ -139,54 +130,44 @@ struct Ring {
   static constexpr int LOADS = 2 * PIECES + SC_LOADS;        // loads per page
 };
 
-// Waves per SIMD each variant is compiled for: the register budget that keeps
-// every live value in the 256 architectural VGPRs (no AGPR round trips on
-// the accumulators) while leaving room for a second wave to hide latency.
+// Waves per SIMD the block-prefill kernel is compiled for: the register
+// budget that keeps every live value in the 256 architectural VGPRs while
+// leaving room for a second wave to hide latency.
 template <int FMT, int D, int NRG, bool QSPLIT>
 constexpr int waves_per_eu() {
   return D == 64 ? (NRG <= 2 ? 3 : 2) : (NRG <= 2 ? 2 : 1);
 }
 
-// Ring slots per wave: as many as the workgroups resident on a CU (one per
-// wave per SIMD) leave room for in the 160 KiB of LDS, between 2 and 4.
-// NB slots keep NB-1 pages in flight while the wave consumes one.
-template <int FMT, bool SF32, int D, int NRG, bool QSPLIT>
-constexpr int ring_slots() {
-  constexpr int budget = 160 * 1024 / waves_per_eu<FMT, D, NRG, QSPLIT>();
-  constexpr int n = budget / (kWaves * Ring<FMT, SF32, D>::SLOT);
-  return n < 2 ? 2 : (n > 4 ? 4 : n);
-}
-
-// Issue the direct-to-LDS loads of page block `blk` into `slot`.
+// Issue the direct-to-LDS loads of the page block at byte offset `boff` of
+// the layer's array into `slot`: the block's K part, V part and (int8) the
+// K and V scale parts, which follow each other in memory. The instruction
+// offset field stays 0 (it would move the LDS address too); every offset
+// goes into the lane's VGPR.
 template <int FMT, bool SF32, int D>
-__device__ __forceinline__ void fetch_page(char* slot, const LayerRsrc& rs, const AttnParams& p,
-                                           int blk, int lane) {
+__device__ __forceinline__ void fetch_page(char* slot, __amdgpu_buffer_rsrc_t rs, uint32_t boff,
+                                           int lane) {
 #if defined(__HIP_DEVICE_COMPILE__)  // the LDS-load builtins exist for the device pass only
   using RG = Ring<FMT, SF32, D>;
-  const int kv_block = RG::KV_BYTES;  // bytes of one K (or V) page block
 #pragma unroll
   for (int i = 0; i < RG::PIECES; ++i) {
-    __builtin_amdgcn_raw_ptr_buffer_load_lds(rs.k, (lds_void_t*)(slot + i * 1024), 16,
-                                             lane * RG::PIECES * 16 + i * 16, blk * kv_block, 0, 0);
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(rs, (lds_void_t*)(slot + i * 1024), 16,
+                                             lane * RG::PIECES * 16 + i * 16, boff, 0, 0);
   }
 #pragma unroll
   for (int i = 0; i < RG::PIECES; ++i) {
-    __builtin_amdgcn_raw_ptr_buffer_load_lds(rs.v, (lds_void_t*)(slot + RG::KV_BYTES + i * 1024), 16,
-                                             lane * RG::PIECES * 16 + i * 16, blk * kv_block, 0, 0);
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(rs, (lds_void_t*)(slot + RG::KV_BYTES + i * 1024), 16,
+                                             RG::KV_BYTES + lane * RG::PIECES * 16 + i * 16, boff,
+                                             0, 0);
   }
   if constexpr (FMT == kI8) {
-    // dword d of the slot's scale area (K scales then V scales)
-    char* sdst = slot + 2 * RG::KV_BYTES;
+    // dword d of [K scales | V scales]; lanes past the end re-read dword 0
+    // into the slot's padding (never the next block).
 #pragma unroll
     for (int i = 0; i < RG::SC_LOADS; ++i) {
-      // dword d of [K scales | V scales]; lanes past the end re-read the
-      // first K scale dword into the slot's padding.
       const int d = i * 64 + lane;
-      const int per = RG::SC_BYTES / 4;
-      const char* kb = static_cast<const char*>(p.kscale) + (size_t)blk * RG::SC_BYTES;
-      const char* vb = static_cast<const char*>(p.vscale) + (size_t)blk * RG::SC_BYTES;
-      const char* src = d < per ? kb + 4 * d : (d < 2 * per ? vb + 4 * (d - per) : kb);
-      __builtin_amdgcn_global_load_lds((global_void_t*)src, (lds_void_t*)(sdst + i * 256), 4, 0, 0);
+      const int dd = d < RG::SC_BYTES / 2 ? d : 0;
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(rs, (lds_void_t*)(slot + 2 * RG::KV_BYTES + i * 256),
+                                               4, 2 * RG::KV_BYTES + 4 * dd, boff, 0, 0);
     }
   }
 #endif
@@ -290,9 +271,19 @@ struct Unit {
     return part ? qlo[rg][pp] : qhi[rg][pp];
   }
 
+  // One page with the Q^T operands held in this unit's registers.
+  __device__ __forceinline__ void consume(const Regs& r, int pi, int grp, bool masked) {
+    consume_with(r, pi, grp, masked,
+                 [&](int rg, int pp, int part) __attribute__((always_inline)) { return qop(rg, pp, part); });
+  }
+
   // One page: scores relative to base, online softmax, value accumulation.
   // `masked` pages hold positions beyond the unit's smallest visible limit.
-  __device__ __forceinline__ void consume(const Regs& r, int pi, int grp, bool masked) {
+  // qf(rg, pp, part) yields the Q^T operand of row group rg, 32-dim block pp
+  // (part 1: the f16 low part, used when QSPLIT).
+  template <class QF>
+  __device__ __forceinline__ void consume_with(const Regs& r, int pi, int grp, bool masked,
+                                               const QF& qf) {
     float4_t sacc[NRG];
 #pragma unroll
     for (int rg = 0; rg < NRG; ++rg) sacc[rg] = float4_t{0, 0, 0, 0};
@@ -302,15 +293,15 @@ struct Unit {
       if (FMT == kF16) {
 #pragma unroll
         for (int rg = 0; rg < NRG; ++rg) {
-          sacc[rg] = MFMA16x16x32(ka, qop(rg, pp, 0), sacc[rg]);
-          if (QSPLIT) sacc[rg] = MFMA16x16x32(ka, qop(rg, pp, 1), sacc[rg]);
+          sacc[rg] = MFMA16x16x32(ka, qf(rg, pp, 0), sacc[rg]);
+          if (QSPLIT) sacc[rg] = MFMA16x16x32(ka, qf(rg, pp, 1), sacc[rg]);
         }
       } else {
         const float4_t ks = scales4<SF32>(r.ks, pp);
 #pragma unroll
         for (int rg = 0; rg < NRG; ++rg) {
-          float4_t b = MFMA16x16x32(ka, qop(rg, pp, 0), (float4_t{0, 0, 0, 0}));
-          if (QSPLIT) b = MFMA16x16x32(ka, qop(rg, pp, 1), b);
+          float4_t b = MFMA16x16x32(ka, qf(rg, pp, 0), (float4_t{0, 0, 0, 0}));
+          if (QSPLIT) b = MFMA16x16x32(ka, qf(rg, pp, 1), b);
 #pragma unroll
           for (int e = 0; e < 4; ++e) sacc[rg][e] = fmaf(b[e], ks[e], sacc[rg][e]);
         }
@@ -380,248 +371,87 @@ struct Unit {
   }
 };
 
-// Workgroup LDS: the four waves' page rings; after the page loop the same
-// bytes hold the merge buffers.
-template <int FMT, bool SF32, int D, int NRG, bool QSPLIT>
-struct Shared {
+// ---------------------------------------------------------------------------
+// Decode kernel: one persistent workgroup of W waves per CU, each covering a
+// contiguous share of the plan's page sequence (its work items in order).
+//
+// The HBM rate a CU reaches grows with the number of waves issuing loads far
+// more than with the pages each wave has in flight, so the kernel runs as
+// many waves as the registers allow: the Q^T operands of the share's units
+// sit in LDS (f16, read per page), not in registers, which fits three waves
+// per SIMD (W = 12) for up to 32 rows per unit.
+//
+// Within a unit the waves take pages round-robin (wave w: pages w, w+W,
+// ...). Each wave streams its pages through a private LDS ring of NB slots
+// (NB-1 page blocks in flight while it consumes one) and crosses unit
+// boundaries without draining: the next unit's first pages are already in
+// flight while the current unit is merged. A unit ends for a wave when its
+// next page belongs to a later unit (or the share is exhausted); the W waves
+// then merge their states for that unit in wave order, so every wave passes
+// the same barriers. The page split is fixed by the plan, so results are
+// bit-reproducible.
+// ---------------------------------------------------------------------------
+constexpr int kLdsBytes = 160 * 1024;  // LDS of one CU (gfx950)
+
+#ifndef TGE_DECODE_WAVES
+#define TGE_DECODE_WAVES 4
+#endif
+#ifndef TGE_DECODE_WPE
+#define TGE_DECODE_WPE 2
+#endif
+#ifndef TGE_DECODE_MAX_SLOTS
+#define TGE_DECODE_MAX_SLOTS 4
+#endif
+
+// Launch shape of a decode variant: W waves per workgroup at WPE waves per
+// SIMD (one workgroup per CU), NB ring slots per wave, and the Q^T operands
+// of up to MAXU units resident in LDS.
+template <int FMT, bool SF32, int D, int NRG>
+struct DecodeCfg {
+  static constexpr int SLOT = Ring<FMT, SF32, D>::SLOT;
   static constexpr int ROWS = 16 * NRG;
-  static constexpr int OPAD = D + 4;
-  static constexpr int MERGE_BYTES = (2 * kWaves * ROWS + ROWS * OPAD) * 4;
-  static constexpr int RING_BYTES =
-      kWaves * ring_slots<FMT, SF32, D, NRG, QSPLIT>() * Ring<FMT, SF32, D>::SLOT;
-  static constexpr int BYTES = RING_BYTES > MERGE_BYTES ? RING_BYTES : MERGE_BYTES;
-  alignas(16) char raw[BYTES];
+  static constexpr int QBYTES = NRG * (D / 32) * 64 * 16;  // one unit's Q^T operands (f16)
+  static constexpr int merge_bytes(int w) { return 4 * (2 * w * ROWS + 2 * ROWS + w); }
+  // Ring slots per wave that fit a workgroup of w waves at wpe waves per
+  // SIMD, next to its merge area and one unit's Q^T operands.
+  static constexpr int nb_fit(int w, int wpe) {
+    return (kLdsBytes / (4 * wpe / w > 1 ? 4 * wpe / w : 1) - 256 - merge_bytes(w) - QBYTES) / (w * SLOT);
+  }
+  // More than 32 rows need a whole SIMD's registers per wave; otherwise the
+  // configured shape, or eight waves at two per SIMD when its rings do not
+  // fit (f16 pages at head_dim 128).
+  static constexpr bool kBig = NRG > 2;
+  static constexpr bool kFits = nb_fit(TGE_DECODE_WAVES, TGE_DECODE_WPE) >= 2;
+  static constexpr int W = kBig ? 4 : (kFits ? TGE_DECODE_WAVES : 8);
+  static constexpr int WPE = kBig ? 1 : (kFits ? TGE_DECODE_WPE : 2);
+  static constexpr int PER_CU = 4 * WPE / W > 1 ? 4 * WPE / W : 1;  // workgroups per CU
+  static constexpr int LDS = kLdsBytes / PER_CU - 256;             // one workgroup's share
+  static constexpr int NB = nb_fit(W, WPE) > TGE_DECODE_MAX_SLOTS ? TGE_DECODE_MAX_SLOTS : nb_fit(W, WPE);
+  static constexpr int LEFT = LDS - merge_bytes(W) - W * NB * SLOT;
+  static constexpr int MAXU = LEFT / QBYTES > 4 ? 4 : LEFT / QBYTES;
+  static_assert(NB >= 2 && MAXU >= 1, "decode LDS plan");
+  // a merge pass stages 8 rows of D floats (row stride D+4) in one ring slot
+  static_assert(8 * (D + 4) * 4 <= SLOT, "merge staging fits a slot");
 };
 
-// One work item (unit) by the whole workgroup.
-template <int FMT, bool SF32, int D, int NRG, bool QSPLIT>
-__device__ __forceinline__ void attend_unit(const AttnParams& p, const WorkRec& w,
-                                            Shared<FMT, SF32, D, NRG, QSPLIT>& sh) {
-  using U = Unit<FMT, SF32, D, NRG, QSPLIT>;
-  using Regs = typename U::Regs;
-  using RG = Ring<FMT, SF32, D>;
-  constexpr int NP = D / 32;
-  constexpr int NT = D / 16;
-  constexpr int ROWS = 16 * NRG;
-  constexpr int OPAD = D + 4;
-  constexpr int NB = ring_slots<FMT, SF32, D, NRG, QSPLIT>();
-
-  const int lane = threadIdx.x & 63;
-  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-  const int col = lane & 15;
-  const int grp = lane >> 4;
-
-  const SessionRec s = p.sessions[w.session];
-  const int q_stride = p.q_heads * D;
-  const int geff = w.rows_per_query;
-
-  U u;
-  // Q^T operands: lane (g, c) of row group rg holds row c, dims
-  // {32pp+4g+e, 32pp+16+4g+e} (the K operand's dim order), pre-multiplied by
-  // log2(e)/sqrt(D) and split into f16 hi + lo.
-#pragma unroll
-  for (int rg = 0; rg < NRG; ++rg) {
-    const int r = rg * 16 + col;
-    const bool valid = r < w.rows;
-    const int qi = w.row_begin + (valid ? r / geff : 0);
-    const int head = w.head_base + (valid ? r % geff : 0);
-    const float* qp = p.q + (size_t)(s.q_row + qi) * q_stride + (size_t)head * D + 4 * grp;
-#pragma unroll
-    for (int pp = 0; pp < NP; ++pp) {
-      float4 a = make_float4(0, 0, 0, 0), b = make_float4(0, 0, 0, 0);
-      if (valid) {
-        a = *reinterpret_cast<const float4*>(qp + 32 * pp);
-        b = *reinterpret_cast<const float4*>(qp + 32 * pp + 16);
-      }
-      const float c = p.scale_log2;
-      const float x[8] = {a.x * c, a.y * c, a.z * c, a.w * c, b.x * c, b.y * c, b.z * c, b.w * c};
-#pragma unroll
-      for (int j = 0; j < 8; ++j) {
-        const _Float16 hi = (_Float16)x[j];
-        u.qhi[rg][pp][j] = hi;
-        u.qlo[rg][pp][j] = QSPLIT ? (_Float16)(x[j] - (float)hi) : (_Float16)0.0f;
-      }
-    }
-    u.lim[rg] = valid ? s.ctx + w.row_begin + r / geff : -1;
-    u.base[rg] = 0.0f;
-    u.thr[rg] = -INFINITY;
-    u.l4[rg] = float4_t{0, 0, 0, 0};
-#pragma unroll
-    for (int t = 0; t < NT; ++t) u.o[rg][t] = float4_t{0, 0, 0, 0};
-  }
-
-  LayerRsrc rs;
-  rs.k = make_rsrc(p.kpool, p.kv_array_bytes);
-  rs.v = make_rsrc(p.vpool, p.kv_array_bytes);
-
-  // This wave's pages j = 0 .. mine-1 are pages page_begin + wave + 4j; the
-  // first `clean` of them hold no position any row of the unit may not see.
-  const int* table = p.tables + s.table_off;
-  const int first_limit = s.ctx + w.row_begin;  // smallest visible limit of the unit
-  const int mine = w.page_begin + wave < w.page_end
-                       ? (w.page_end - w.page_begin - wave + kWaves - 1) / kWaves
-                       : 0;
-  const int unmasked_pages = (first_limit + 1) / 16;  // pi*16+15 <= first_limit
-  int clean = 0;
-  if (unmasked_pages > w.page_begin + wave) {
-    clean = (unmasked_pages - w.page_begin - wave + kWaves - 1) / kWaves;
-    clean = clean < mine ? clean : mine;
-  }
-  char* ring = sh.raw + wave * NB * RG::SLOT;
-  if (mine > 0) {
-    // Page ids come through the scalar cache (read-only constant loads), one
-    // page ahead of their use, so no vector-memory wait is tied to them.
-    const sconst_int* ids = (const sconst_int*)(table + w.page_begin + wave);
-    auto block_of = [&](int id) -> int { return id * p.kv_heads + w.kv_head; };
-#pragma unroll
-    for (int b = 0; b < NB - 1; ++b) {
-      if (b < mine) fetch_page<FMT, SF32, D>(ring + b * RG::SLOT, rs, p, block_of(ids[kWaves * b]), lane);
-    }
-    int id_next = NB - 1 < mine ? ids[kWaves * (NB - 1)] : 0;
-    int slot = 0;
-    for (int j = 0; j < mine; ++j) {
-      const int jn = j + NB - 1;
-      if (jn < mine) {
-        const int id = id_next;
-        id_next = jn + 1 < mine ? ids[kWaves * (jn + 1)] : 0;
-        int sn = slot + NB - 1;
-        sn = sn >= NB ? sn - NB : sn;
-        fetch_page<FMT, SF32, D>(ring + sn * RG::SLOT, rs, p, block_of(id), lane);
-        wait_vmcnt<(NB - 1) * RG::LOADS>();  // page j has landed
-      } else {
-        wait_vmcnt<0>();
-      }
-      Regs r;
-      read_page<FMT, SF32, D>(r, ring + slot * RG::SLOT, lane, grp);
-      u.consume(r, w.page_begin + wave + kWaves * j, grp, j >= clean);
-      slot = slot + 1 == NB ? 0 : slot + 1;
-    }
-  }
-
-  float* lds_base = reinterpret_cast<float*>(sh.raw);
-  float (*lds_m)[ROWS] = reinterpret_cast<float (*)[ROWS]>(lds_base);
-  float (*lds_l)[ROWS] = reinterpret_cast<float (*)[ROWS]>(lds_base + kWaves * ROWS);
-  float* lds_o = lds_base + 2 * kWaves * ROWS;
-  __syncthreads();  // every wave is done with its ring before it is reused
-
-  // ---- merge the four waves (fixed order) and write --------------------
-  // Each wave's state for a row is (base, l, o): o and l are sums of
-  // exp2(s - base). Rows that saw no visible position have thr = -inf.
-#pragma unroll
-  for (int rg = 0; rg < NRG; ++rg) {
-    if (grp == 0) {
-      lds_m[wave][rg * 16 + col] = u.thr[rg] == -INFINITY ? -INFINITY : u.base[rg];
-      lds_l[wave][rg * 16 + col] = u.l4[rg][0];
-    }
-  }
-  __syncthreads();
-#pragma unroll
-  for (int rg = 0; rg < NRG; ++rg) {
-    const int r = rg * 16 + col;
-    float mm = lds_m[0][r];
-#pragma unroll
-    for (int k = 1; k < kWaves; ++k) mm = fmaxf(mm, lds_m[k][r]);
-    const float mine_m = lds_m[wave][r];
-    const float f = (mine_m == -INFINITY) ? 0.0f : pow2i(mine_m - mm);
-#pragma unroll
-    for (int t = 0; t < NT; ++t) u.o[rg][t] *= f;
-  }
-  for (int k = 0; k < kWaves; ++k) {
-    if (wave == k) {
-#pragma unroll
-      for (int rg = 0; rg < NRG; ++rg) {
-#pragma unroll
-        for (int t = 0; t < NT; ++t) {
-          float4_t* dst = reinterpret_cast<float4_t*>(&lds_o[(rg * 16 + col) * OPAD + 16 * t + 4 * grp]);
-          if (k == 0) {
-            *dst = u.o[rg][t];
-          } else {
-            *dst += u.o[rg][t];
-          }
-        }
-      }
-    }
-    __syncthreads();
-  }
-
-  for (int idx = threadIdx.x; idx < w.rows * (D / 4); idx += 256) {
-    const int r = idx / (D / 4);
-    const int d4 = idx % (D / 4);
-    float mm = lds_m[0][r];
-#pragma unroll
-    for (int k = 1; k < kWaves; ++k) mm = fmaxf(mm, lds_m[k][r]);
-    float sum = 0.0f;
-#pragma unroll
-    for (int k = 0; k < kWaves; ++k) {
-      const float mk = lds_m[k][r];
-      if (mk != -INFINITY) sum += lds_l[k][r] * pow2i(mk - mm);
-    }
-    const float4_t acc = *reinterpret_cast<const float4_t*>(&lds_o[r * OPAD + 4 * d4]);
-    if (w.part < 0) {
-      const int qi = w.row_begin + r / geff;
-      const int head = w.head_base + r % geff;
-      float4_t res = float4_t{0, 0, 0, 0};
-      if (sum > 0.0f) res = div4(acc, sum);
-      *reinterpret_cast<float4_t*>(p.out + (size_t)(s.q_row + qi) * q_stride + (size_t)head * D + 4 * d4) = res;
-    } else {
-      *reinterpret_cast<float4_t*>(p.part_o + ((size_t)w.part * p.rows_cap + r) * D + 4 * d4) = acc;
-      if (d4 == 0) {
-        p.part_ml[((size_t)w.part * p.rows_cap + r) * 2] = mm;
-        p.part_ml[((size_t)w.part * p.rows_cap + r) * 2 + 1] = sum;
-      }
-    }
-  }
-}
-
-// The workgroup runs its work items in turn: items [first[g], first[g+1])
-// for workgroup g under a balanced schedule (every workgroup of the launch
-// gets the same number of pages), or item g alone when `first` is null.
-template <int FMT, bool SF32, int D, int NRG, bool QSPLIT, int WPE>
-__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(WPE, WPE)))
-void paged_attention_kernel(AttnParams p) {
-  __shared__ Shared<FMT, SF32, D, NRG, QSPLIT> sh;
-  int it = blockIdx.x, end = blockIdx.x + 1;
-  if (p.wg_first) {
-    it = p.wg_first[blockIdx.x];
-    end = p.wg_first[blockIdx.x + 1];
-  }
-  for (; it < end; ++it) {
-    const WorkRec w = p.work[it];
-    attend_unit<FMT, SF32, D, NRG, QSPLIT>(p, w, sh);
-    __syncthreads();  // LDS is reused by the next item
-  }
-}
-
-// ---------------------------------------------------------------------------
-// Decode kernel: persistent workgroups of four waves (as many per CU as the
-// registers allow), each covering a contiguous share of the plan's page
-// sequence (its work items in order).
-//
-// Within a unit the waves take pages round-robin (wave w: pages w, w+4,
-// ...). Each wave streams its pages through a private LDS ring and crosses
-// unit boundaries without draining: the next unit's first pages are already
-// in flight while the current unit is merged. A unit ends for a wave when
-// its next page belongs to a later unit (or the share is exhausted); the
-// four waves then merge their states for that unit in wave order, so every
-// wave passes the same barriers. The page split is fixed by the plan, so
-// results are bit-reproducible.
-// ---------------------------------------------------------------------------
-template <int FMT, bool SF32, int D, int NRG, int WPE>
+template <int FMT, bool SF32, int D, int NRG>
 struct DecodeShared {
+  using C = DecodeCfg<FMT, SF32, D, NRG>;
   static constexpr int ROWS = 16 * NRG;
-  static constexpr int OPAD = D + 4;
-  static constexpr int MERGE_FLOATS = 2 * kWaves * ROWS + ROWS * OPAD;
-  static constexpr int SLOT = Ring<FMT, SF32, D>::SLOT;
-  // LDS of one of the WPE workgroups that share a CU.
-  static constexpr int BUDGET = 160 * 1024 / WPE - 4 * MERGE_FLOATS - 64;
-  static constexpr int NB_FIT = BUDGET / (kWaves * SLOT);
-  static constexpr int NB = NB_FIT > 4 ? 4 : NB_FIT;
-  static_assert(NB >= 2, "the decode ring needs two slots per wave");
-  alignas(16) char ring[kWaves * NB * SLOT];
+  static constexpr int MERGE_FLOATS = 2 * C::W * ROWS + 2 * ROWS + C::W;
+  alignas(16) char ring[C::W * C::NB * C::SLOT];
+  alignas(16) half8_t q[C::MAXU * NRG * (D / 32) * 64];  // [unit][rg][pp][lane]
   alignas(16) float merge[MERGE_FLOATS];
 };
 
 typedef const __attribute__((address_space(4))) WorkRec sconst_work;
+
+// Wait for this wave's outstanding LDS and scalar-memory operations; a
+// compiler barrier for memory accesses.
+__device__ __forceinline__ void lgkm_wait_all() {
+  __builtin_amdgcn_s_waitcnt((15) | (7 << 4) | (0 << 8) | (3 << 14));  // lgkmcnt(0) only
+  __atomic_signal_fence(__ATOMIC_SEQ_CST);
+}
 
 // Workgroup barrier ordering LDS only: this wave's LDS accesses complete,
 // then all waves meet. Direct-to-LDS page loads stay in flight across it
@@ -651,35 +481,41 @@ __device__ __forceinline__ WorkRec load_work(const sconst_work* w) {
 }
 
 // Share indices of the pages in a wave's ring, oldest first (a FIFO of at
-// most four wave-uniform values kept in scalar registers).
+// most N wave-uniform values; the constant-index loops keep it in scalar
+// registers).
+template <int N>
 struct PageFifo {
-  int t0 = 0, t1 = 0, t2 = 0, t3 = 0;
+  int t[N];
+  __device__ __forceinline__ PageFifo() {
+#pragma unroll
+    for (int i = 0; i < N; ++i) t[i] = 0;
+  }
   __device__ __forceinline__ void push(int n, int g) {  // n = entries before the push
-    t0 = n == 0 ? g : t0;
-    t1 = n == 1 ? g : t1;
-    t2 = n == 2 ? g : t2;
-    t3 = n == 3 ? g : t3;
+#pragma unroll
+    for (int i = 0; i < N; ++i) t[i] = n == i ? g : t[i];
   }
   __device__ __forceinline__ void pop() {
-    t0 = t1;
-    t1 = t2;
-    t2 = t3;
+#pragma unroll
+    for (int i = 0; i + 1 < N; ++i) t[i] = t[i + 1];
   }
+  __device__ __forceinline__ int front() const { return t[0]; }
 };
 
-template <int FMT, bool SF32, int D, int NRG, bool QSPLIT, int WPE>
-__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(WPE, WPE)))
+template <int FMT, bool SF32, int D, int NRG, int W, int WPE>
+__global__ __launch_bounds__(64 * W) __attribute__((amdgpu_waves_per_eu(WPE, WPE)))
 void paged_decode_kernel(AttnParams p) {
-  constexpr int W = kWaves;
-  using SH = DecodeShared<FMT, SF32, D, NRG, WPE>;
-  using U = Unit<FMT, SF32, D, NRG, QSPLIT>;
+  using CFG = DecodeCfg<FMT, SF32, D, NRG>;
+  using SH = DecodeShared<FMT, SF32, D, NRG>;
+  using U = Unit<FMT, SF32, D, NRG, false>;
   using Regs = typename U::Regs;
   using RG = Ring<FMT, SF32, D>;
-  constexpr int NB = SH::NB;
+  static_assert(CFG::W == W && CFG::WPE == WPE, "launch shape");
+  constexpr int NB = CFG::NB;
+  constexpr int MAXU = CFG::MAXU;
   constexpr int NP = D / 32;
   constexpr int NT = D / 16;
   constexpr int ROWS = 16 * NRG;
-  constexpr int OPAD = D + 4;
+  constexpr int QUNIT = NRG * NP * 64;  // half8 entries of one unit's Q^T
   __shared__ SH sh;
 
   const int first = p.wg_first[blockIdx.x];
@@ -693,26 +529,58 @@ void paged_decode_kernel(AttnParams p) {
   const sconst_work* work = (const sconst_work*)p.work;
   const int q_stride = p.q_heads * D;
 
-  LayerRsrc rs;
-  rs.k = make_rsrc(p.kpool, p.kv_array_bytes);
-  rs.v = make_rsrc(p.vpool, p.kv_array_bytes);
+  const __amdgpu_buffer_rsrc_t rs = make_rsrc(p.pool, p.array_bytes);
   char* ring = sh.ring + wave * NB * RG::SLOT;
+
+  // ---- Q^T operands of units [qfirst, qfirst + MAXU) in LDS ----------------
+  // Entry (u, rg, pp, l): lane l = 16g + c of row group rg holds row c, dims
+  // {32pp+4g+e, 32pp+16+4g+e}, pre-multiplied by log2(e)/sqrt(D), in f16.
+  // Each block of 64 entries is one wave's, so the unit is wave-uniform.
+  int qfirst = first;
+  auto fill_q = [&](int from) __attribute__((always_inline)) -> void {
+    for (int idx = threadIdx.x; idx < MAXU * QUNIT; idx += 64 * W) {
+      const int l = idx & 63;
+      const int blk = __builtin_amdgcn_readfirstlane(idx >> 6);
+      const int pp = blk % NP;
+      const int rg = (blk / NP) % NRG;
+      const int it = from + blk / (NP * NRG);
+      half8_t h = {};
+      if (it < last) {
+        const WorkRec w = load_work(work + it);
+        const int r = rg * 16 + (l & 15);
+        if (r < w.rows) {
+          const int qi = w.row_begin + r / w.rows_per_query;
+          const int head = w.head_base + r % w.rows_per_query;
+          const float* qp = p.q + (size_t)(w.q_row + qi) * q_stride + (size_t)head * D + 32 * pp + 4 * (l >> 4);
+          const float4 a = *reinterpret_cast<const float4*>(qp);
+          const float4 b = *reinterpret_cast<const float4*>(qp + 16);
+          const float c = p.scale_log2;
+          h = half8_t{(_Float16)(a.x * c), (_Float16)(a.y * c), (_Float16)(a.z * c), (_Float16)(a.w * c),
+                      (_Float16)(b.x * c), (_Float16)(b.y * c), (_Float16)(b.z * c), (_Float16)(b.w * c)};
+        }
+      }
+      sh.q[idx] = h;
+    }
+  };
 
   // ---- issue side: this wave's next page, its block, its fetch -------------
   // Cursor over the share's units: unit `ik` covers share pages
-  // [ibase, ibase + its page count); `jn` is this wave's next page in it.
+  // [ibase, ibase + its page count); `jn` is this wave's next page in it
+  // (wave w takes the unit's pages w, w+W, ...: a fixed split, so results
+  // are bit-reproducible and independent of where the pages sit).
   int ik = first, ibase = 0, jn = wave;
   WorkRec iw = load_work(work + first);
   WorkRec iw_next = load_work(work + (first + 1 < last ? first + 1 : first));
-  int pend_g = -1, pend_block = 0;  // next page to fetch (share index, block)
+  // Next page to fetch: share index (-1: none), page id and KV head. The id
+  // is used only at the next fetch, so its scalar load is waited for there.
+  int pend_g = -1, pend_id = 0, pend_head = 0;
   auto request = [&]() __attribute__((always_inline)) -> void {
     bool ok = true;
     while (ok && jn >= iw.page_end - iw.page_begin) {
       if (ik + 1 >= last) {
         ok = false;  // past the share: the cursor stays on its last unit
       } else {
-        const int np = iw.page_end - iw.page_begin;
-        ibase += np;
+        ibase += iw.page_end - iw.page_begin;
         ++ik;
         jn = wave;
         iw = iw_next;
@@ -723,16 +591,18 @@ void paged_decode_kernel(AttnParams p) {
     const sconst_int* t = (const sconst_int*)(p.tables + iw.table_off + iw.page_begin);
     const int id = t[ok ? jn : 0];
     pend_g = ok ? ibase + jn : -1;
-    pend_block = id * p.kv_heads + iw.kv_head;
+    pend_id = id;
+    pend_head = iw.kv_head;
     jn += W;
   };
-  // Fetch the pending page into `slot` and take the next; returns the
-  // fetched page's share index, or -1 when the share is exhausted.
+  // Fetch the pending page into `slot`; returns the fetched page's share
+  // index, or -1 when the share is exhausted. The caller then takes the
+  // next page with request().
   auto issue = [&](int slot) __attribute__((always_inline)) -> int {
     const int g = pend_g;
     if (g >= 0) {
-      fetch_page<FMT, SF32, D>(ring + slot * RG::SLOT, rs, p, pend_block, lane);
-      request();
+      const uint32_t off = (uint32_t)(pend_id * p.kv_heads + pend_head) * p.block_bytes;
+      fetch_page<FMT, SF32, D>(ring + slot * RG::SLOT, rs, off, lane);
     }
     return g;
   };
@@ -755,40 +625,24 @@ void paged_decode_kernel(AttnParams p) {
     }
     unmasked = (cw.ctx + cw.row_begin + 1) / 16;  // pages with no masked position
   };
-  // Q^T operands of the unit (see attend_unit), loaded before its first page.
-  auto load_q = [&]() __attribute__((always_inline)) -> void {
-#pragma unroll
-    for (int rg = 0; rg < NRG; ++rg) {
-      const int r = rg * 16 + col;
-      const bool valid = r < cw.rows;
-      const int qi = cw.row_begin + (valid ? r / cw.rows_per_query : 0);
-      const int head = cw.head_base + (valid ? r % cw.rows_per_query : 0);
-      const float* qp = p.q + (size_t)(cw.q_row + qi) * q_stride + (size_t)head * D + 4 * grp;
-#pragma unroll
-      for (int pp = 0; pp < NP; ++pp) {
-        float4 a = make_float4(0, 0, 0, 0), b = make_float4(0, 0, 0, 0);
-        if (valid) {
-          a = *reinterpret_cast<const float4*>(qp + 32 * pp);
-          b = *reinterpret_cast<const float4*>(qp + 32 * pp + 16);
-        }
-        const float c = p.scale_log2;
-        const float x[8] = {a.x * c, a.y * c, a.z * c, a.w * c, b.x * c, b.y * c, b.z * c, b.w * c};
-#pragma unroll
-        for (int j = 0; j < 8; ++j) {
-          const _Float16 hi = (_Float16)x[j];
-          u.qhi[rg][pp][j] = hi;
-          u.qlo[rg][pp][j] = QSPLIT ? (_Float16)(x[j] - (float)hi) : (_Float16)0.0f;
-        }
-      }
-    }
-  };
-  // Merge the W waves' states of unit `cw` in wave order and write the
-  // output rows (or the unit's partial). Every wave calls this once per unit.
+  // Merge the W waves' states of unit `cw` and write the output rows (or the
+  // unit's partial). Every wave calls this once per unit, at a point where
+  // its ring has a free slot (slot `fs`: the ring holds `count` < NB pages).
+  //   1. each wave publishes its rows' (base, sum) and its free slot; wave 0
+  //      derives each row's common base and total sum; each wave rescales
+  //      its accumulators to the common base;
+  //   2. in passes of 8 rows, each wave stages its accumulators for those
+  //      rows in its free slot, then the workgroup's threads add the W
+  //      copies in wave order (a fixed order: results do not depend on
+  //      timing) and write the rows out.
+  constexpr int PASS_ROWS = 8;
   float* mbase = sh.merge;
   float (*lds_m)[ROWS] = reinterpret_cast<float (*)[ROWS]>(mbase);
   float (*lds_l)[ROWS] = reinterpret_cast<float (*)[ROWS]>(mbase + W * ROWS);
-  float* lds_o = mbase + 2 * W * ROWS;
-  auto finalize = [&]() __attribute__((always_inline)) -> void {
+  float* lds_mm = mbase + 2 * W * ROWS;  // [ROWS] common base
+  float* lds_sum = lds_mm + ROWS;         // [ROWS] total sum
+  int* lds_fs = reinterpret_cast<int*>(lds_sum + ROWS);  // [W] free ring slot of each wave
+  auto finalize = [&](int fs) __attribute__((always_inline)) -> void {
 #pragma unroll
     for (int rg = 0; rg < NRG; ++rg) {
       if (grp == 0) {
@@ -796,6 +650,7 @@ void paged_decode_kernel(AttnParams p) {
         lds_l[wave][rg * 16 + col] = u.l4[rg][0];
       }
     }
+    if (lane == 0) lds_fs[wave] = fs;
     lds_barrier();
 #pragma unroll
     for (int rg = 0; rg < NRG; ++rg) {
@@ -807,78 +662,105 @@ void paged_decode_kernel(AttnParams p) {
       const float f = (mine_m == -INFINITY) ? 0.0f : pow2i(mine_m - mm);
 #pragma unroll
       for (int t = 0; t < NT; ++t) u.o[rg][t] *= f;
+      if (wave == 0 && grp == 0) {
+        float sum = 0.0f;
+#pragma unroll
+        for (int k = 0; k < W; ++k) {
+          const float mk = lds_m[k][r];
+          if (mk != -INFINITY) sum += lds_l[k][r] * pow2i(mk - mm);
+        }
+        lds_mm[r] = mm;
+        lds_sum[r] = sum;
+      }
     }
-    for (int k = 0; k < W; ++k) {
-      if (wave == k) {
+    constexpr int SPAD = D + 4;  // staged row stride (floats): rows fall on different banks
+    float* stage = reinterpret_cast<float*>(ring + fs * RG::SLOT);  // [8 rows][SPAD]
 #pragma unroll
-        for (int rg = 0; rg < NRG; ++rg) {
+    for (int ps = 0; ps < NRG * 16 / PASS_ROWS; ++ps) {
+      const int rg = ps / (16 / PASS_ROWS);
+      const int r0 = ps * PASS_ROWS;  // first row of the pass
+      if (col - (r0 - rg * 16) >= 0 && col - (r0 - rg * 16) < PASS_ROWS) {
+        float* dst = stage + (col - (r0 - rg * 16)) * SPAD + 4 * grp;
 #pragma unroll
-          for (int t = 0; t < NT; ++t) {
-            float4_t* dst = reinterpret_cast<float4_t*>(&lds_o[(rg * 16 + col) * OPAD + 16 * t + 4 * grp]);
-            if (k == 0) {
-              *dst = u.o[rg][t];
-            } else {
-              *dst += u.o[rg][t];
+        for (int t = 0; t < NT; ++t) *reinterpret_cast<float4_t*>(dst + 16 * t) = u.o[rg][t];
+      }
+      lds_barrier();
+      for (int idx = threadIdx.x; idx < PASS_ROWS * (D / 4); idx += 64 * W) {
+        const int r = r0 + idx / (D / 4);
+        const int d4 = idx % (D / 4);
+        float4_t acc = float4_t{0, 0, 0, 0};
+#pragma unroll
+        for (int k = 0; k < W; ++k) {
+          const float* src = reinterpret_cast<const float*>(sh.ring + (k * NB + lds_fs[k]) * RG::SLOT);
+          acc += *reinterpret_cast<const float4_t*>(src + (r - r0) * SPAD + 4 * d4);
+        }
+        if (r < cw.rows) {
+          const float sum = lds_sum[r];
+          if (cw.part < 0) {
+            const int qi = cw.row_begin + r / cw.rows_per_query;
+            const int head = cw.head_base + r % cw.rows_per_query;
+            float4_t res = float4_t{0, 0, 0, 0};
+            if (sum > 0.0f) res = div4(acc, sum);
+            *reinterpret_cast<float4_t*>(p.out + (size_t)(cw.q_row + qi) * q_stride + (size_t)head * D + 4 * d4) = res;
+          } else {
+            *reinterpret_cast<float4_t*>(p.part_o + ((size_t)cw.part * p.rows_cap + r) * D + 4 * d4) = acc;
+            if (d4 == 0) {
+              p.part_ml[((size_t)cw.part * p.rows_cap + r) * 2] = lds_mm[r];
+              p.part_ml[((size_t)cw.part * p.rows_cap + r) * 2 + 1] = sum;
             }
           }
         }
       }
-      lds_barrier();
+      lds_barrier();  // the slots (and, after the last pass, the merge area) are free again
     }
-    for (int idx = threadIdx.x; idx < cw.rows * (D / 4); idx += 64 * W) {
-      const int r = idx / (D / 4);
-      const int d4 = idx % (D / 4);
-      float mm = lds_m[0][r];
-#pragma unroll
-      for (int k = 1; k < W; ++k) mm = fmaxf(mm, lds_m[k][r]);
-      float sum = 0.0f;
-#pragma unroll
-      for (int k = 0; k < W; ++k) {
-        const float mk = lds_m[k][r];
-        if (mk != -INFINITY) sum += lds_l[k][r] * pow2i(mk - mm);
-      }
-      const float4_t acc = *reinterpret_cast<const float4_t*>(&lds_o[r * OPAD + 4 * d4]);
-      if (cw.part < 0) {
-        const int qi = cw.row_begin + r / cw.rows_per_query;
-        const int head = cw.head_base + r % cw.rows_per_query;
-        float4_t res = float4_t{0, 0, 0, 0};
-        if (sum > 0.0f) res = div4(acc, sum);
-        *reinterpret_cast<float4_t*>(p.out + (size_t)(cw.q_row + qi) * q_stride + (size_t)head * D + 4 * d4) = res;
-      } else {
-        *reinterpret_cast<float4_t*>(p.part_o + ((size_t)cw.part * p.rows_cap + r) * D + 4 * d4) = acc;
-        if (d4 == 0) {
-          p.part_ml[((size_t)cw.part * p.rows_cap + r) * 2] = mm;
-          p.part_ml[((size_t)cw.part * p.rows_cap + r) * 2 + 1] = sum;
-        }
-      }
-    }
-    lds_barrier();  // the merge area is free for the next unit
   };
+  // Every wave passes the same unit boundaries in the same order (in the
+  // page loop or in the closing loop below), so the barriers of finalize and
+  // of a table reload pair up.
   auto next_unit = [&]() __attribute__((always_inline)) -> void {
     cbase += cw.page_end - cw.page_begin;
     ++ck;
     cw = load_work(work + (ck < last ? ck : last - 1));
     reset_unit();
+    if (ck < last && ck >= qfirst + MAXU) {
+      // (rare: more than MAXU units in one share) every wave has merged the
+      // previous unit, so the table is free; the reload waits for this
+      // wave's loads in flight.
+      qfirst = ck;
+      fill_q(qfirst);
+      __syncthreads();
+    }
   };
-  // Q^T of the unit is loaded when the wave starts it, so the previous
-  // unit's Q is dead while that unit is merged.
 
   // ---- the page loop -----------------------------------------------------------
+  fill_q(qfirst);
   reset_unit();
-  load_q();
+  __syncthreads();  // the Q table is written
   request();
-  PageFifo fifo;
+  PageFifo<NB> fifo;
   int head = 0, count = 0;
 #pragma unroll
   for (int b = 0; b < NB - 1; ++b) {
     if (count == b) {
       const int g = issue(b);
       if (g >= 0) {
+        request();
         fifo.push(count, g);
         ++count;
       }
     }
   }
+  // Close every unit that ends before this wave's next page (all of them
+  // once the share is exhausted). Called with a free ring slot.
+  auto close_units = [&]() __attribute__((always_inline)) -> void {
+    while (ck < last && (count == 0 || fifo.front() >= cbase + (cw.page_end - cw.page_begin))) {
+      int fs = head + count;
+      fs = fs >= NB ? fs - NB : fs;
+      finalize(fs);
+      next_unit();
+    }
+  };
+  close_units();
   while (count > 0) {
     int nslot = head + count;
     nslot = nslot >= NB ? nslot - NB : nslot;
@@ -890,26 +772,22 @@ void paged_decode_kernel(AttnParams p) {
     } else {
       wait_vmcnt<0>();
     }
-    const int g = fifo.t0;
-    if (g >= cbase + (cw.page_end - cw.page_begin)) {
-      do {
-        finalize();
-        next_unit();
-      } while (g >= cbase + (cw.page_end - cw.page_begin));
-      load_q();
-    }
+    const int g = fifo.front();
     Regs r;
     read_page<FMT, SF32, D>(r, ring + head * RG::SLOT, lane, grp);
+    // The next page id is read through the scalar cache only now, after the
+    // page's LDS reads have completed (they share the lgkm counter), so its
+    // latency hides behind this page's math instead of stalling the wave.
+    lgkm_wait_all();
+    if (gn >= 0) request();
     const int pi = cw.page_begin + (g - cbase);
-    u.consume(r, pi, grp, pi >= unmasked);
+    const half8_t* qt = sh.q + (ck - qfirst) * QUNIT + lane;
+    u.consume_with(r, pi, grp, pi >= unmasked,
+                   [&](int rg, int pp, int) __attribute__((always_inline)) { return qt[(rg * NP + pp) * 64]; });
     head = head + 1 == NB ? 0 : head + 1;
     --count;
     fifo.pop();
-  }
-  // The share is exhausted: close this wave's remaining units.
-  while (ck < last) {
-    finalize();
-    next_unit();
+    close_units();  // the slot just read is free
   }
 }
 
@@ -955,9 +833,7 @@ void paged_prefill_kernel(AttnParams p) {
   const int row0 = wave * 32;
   const bool has_rows = row0 < w.rows;
 
-  LayerRsrc rs;
-  rs.k = make_rsrc(p.kpool, p.kv_array_bytes);
-  rs.v = make_rsrc(p.vpool, p.kv_array_bytes);
+  const __amdgpu_buffer_rsrc_t rs = make_rsrc(p.pool, p.array_bytes);
 
   // This wave's rows: Q^T operands (as in attend_unit) and visible limits.
   U u;
@@ -1001,8 +877,8 @@ void paged_prefill_kernel(AttnParams p) {
   auto fetch_tile = [&](int k) __attribute__((always_inline)) -> void {
     const int j = k * kWaves + wave;
     if (j < npages) {
-      fetch_page<FMT, SF32, D>(sh.ring + (k % NB) * SH::TILE + wave * RG::SLOT, rs, p,
-                               table[j] * p.kv_heads + w.kv_head, lane);
+      fetch_page<FMT, SF32, D>(sh.ring + (k % NB) * SH::TILE + wave * RG::SLOT, rs,
+                               (uint32_t)(table[j] * p.kv_heads + w.kv_head) * p.block_bytes, lane);
     }
   };
 #pragma unroll
@@ -1158,30 +1034,15 @@ __global__ __launch_bounds__(256) void split_reduce_kernel(ReduceParams p) {
 
 }  // namespace
 
-// Whether a variant's decode ring (two or more slots per wave) and merge
-// area fit its share of LDS; the others run the unit-at-a-time kernel.
-template <int FMT, bool SF32, int D, int NRG>
-constexpr bool decode_fits() {
-  constexpr int wpe = waves_per_eu<FMT, D, NRG, true>();
-  constexpr int rows = 16 * NRG;
-  constexpr int merge = 4 * (2 * kWaves * rows + rows * (D + 4));
-  return (160 * 1024 / wpe - merge - 64) / (kWaves * Ring<FMT, SF32, D>::SLOT) >= 2;
-}
-
 template <int FMT, bool SF32, int D>
 hipError_t launch_decode_d(int row_groups, int n_groups, const AttnParams& p, hipStream_t stream) {
   switch (row_groups) {
-#define TGE_DEC(n)                                                                                 \
-  case n: {                                                                                        \
-    constexpr int wpe = waves_per_eu<FMT, D, n, true>();                                           \
-    if constexpr (decode_fits<FMT, SF32, D, n>()) {                                                \
-      hipLaunchKernelGGL((paged_decode_kernel<FMT, SF32, D, n, true, wpe>),                        \
-                         dim3((unsigned)n_groups), dim3(256), 0, stream, p);                       \
-    } else {                                                                                       \
-      hipLaunchKernelGGL((paged_attention_kernel<FMT, SF32, D, n, true, wpe>),                     \
-                         dim3((unsigned)n_groups), dim3(256), 0, stream, p);                       \
-    }                                                                                              \
-    break;                                                                                         \
+#define TGE_DEC(n)                                                                          \
+  case n: {                                                                                 \
+    using C = DecodeCfg<FMT, SF32, D, n>;                                                   \
+    hipLaunchKernelGGL((paged_decode_kernel<FMT, SF32, D, n, C::W, C::WPE>),           \
+                       dim3((unsigned)n_groups), dim3(64 * C::W), 0, stream, p);            \
+    break;                                                                                  \
   }
     TGE_DEC(1)
     TGE_DEC(2)
@@ -1199,17 +1060,12 @@ int decode_blocks_d(int row_groups) {
   int n = 0;
   hipError_t e = hipErrorInvalidValue;
   switch (row_groups) {
-#define TGE_DOCC(r)                                                                          \
-  case r: {                                                                                  \
-    constexpr int wpe = waves_per_eu<FMT, D, r, true>();                                     \
-    if constexpr (decode_fits<FMT, SF32, D, r>()) {                                          \
-      e = hipOccupancyMaxActiveBlocksPerMultiprocessor(                                      \
-          &n, paged_decode_kernel<FMT, SF32, D, r, true, wpe>, 256, 0);                      \
-    } else {                                                                                 \
-      e = hipOccupancyMaxActiveBlocksPerMultiprocessor(                                      \
-          &n, paged_attention_kernel<FMT, SF32, D, r, true, wpe>, 256, 0);                   \
-    }                                                                                        \
-    break;                                                                                   \
+#define TGE_DOCC(r)                                                                        \
+  case r: {                                                                                \
+    using C = DecodeCfg<FMT, SF32, D, r>;                                                  \
+    e = hipOccupancyMaxActiveBlocksPerMultiprocessor(                                      \
+        &n, paged_decode_kernel<FMT, SF32, D, r, C::W, C::WPE>, 64 * C::W, 0);             \
+    break;                                                                                 \
   }
     TGE_DOCC(1)
     TGE_DOCC(2)

@@ -73,13 +73,9 @@ size_t align256(size_t x) { return (x + 255) & ~size_t(255); }
 
 struct tge_kv_pool {
   tge_kv_pool_desc desc{};
-  void* k = nullptr;
-  void* v = nullptr;
-  void* ks = nullptr;
-  void* vs = nullptr;
-  size_t kv_block_bytes = 0;    // one page block of K (or V)
-  size_t scale_block_bytes = 0;
-  size_t layer_blocks = 0;      // pages * kv_heads
+  void* blocks = nullptr;   // layers x (pages * kv_heads) page blocks
+  tge::BlockGeom geom{};
+  size_t layer_blocks = 0;  // pages * kv_heads
   size_t bytes = 0;
 };
 
@@ -206,44 +202,31 @@ int tge_kv_pool_create(const tge_kv_pool_desc* desc, tge_kv_pool** out) {
 
   auto* p = new tge_kv_pool;
   p->desc = d;
-  const size_t elem = d.format == TGE_KV_F16 ? 2 : 1;
-  p->kv_block_bytes = (size_t)16 * d.head_dim * elem;
-  p->scale_block_bytes =
-      d.format == TGE_KV_I8 ? (size_t)16 * (d.head_dim / 32) * (d.scale_format == TGE_SCALE_F32 ? 4 : 2)
-                            : 0;
+  p->geom = tge::block_geom(d.format, d.head_dim, d.format == TGE_KV_I8 && d.scale_format == TGE_SCALE_F32);
   p->layer_blocks = (size_t)d.pages * d.kv_heads;
-  // Attention kernels address one layer's K, V and scale arrays with 32-bit
-  // buffer offsets.
-  if (p->kv_block_bytes * p->layer_blocks >= (size_t(1) << 31)) {
+  // Attention kernels address one layer's block array with 32-bit buffer
+  // offsets.
+  const size_t layer_bytes = (size_t)p->geom.block_bytes * p->layer_blocks;
+  if (layer_bytes >= (size_t(1) << 31)) {
     delete p;
-    return fail(TGE_ERR_CAPACITY, "kv_pool_create: one layer's K array must stay below 2 GiB");
+    return fail(TGE_ERR_CAPACITY, "kv_pool_create: one layer's page blocks must stay below 2 GiB");
   }
-  const size_t kv_total = p->kv_block_bytes * p->layer_blocks * d.layers;
-  const size_t sc_total = p->scale_block_bytes * p->layer_blocks * d.layers;
-  hipError_t e = hipMalloc(&p->k, kv_total);
-  if (e == hipSuccess) e = hipMalloc(&p->v, kv_total);
-  if (e == hipSuccess && sc_total) e = hipMalloc(&p->ks, sc_total);
-  if (e == hipSuccess && sc_total) e = hipMalloc(&p->vs, sc_total);
-  if (e == hipSuccess) e = hipMemset(p->k, 0, kv_total);
-  if (e == hipSuccess) e = hipMemset(p->v, 0, kv_total);
-  if (e == hipSuccess && sc_total) e = hipMemset(p->ks, 0, sc_total);
-  if (e == hipSuccess && sc_total) e = hipMemset(p->vs, 0, sc_total);
+  const size_t total = layer_bytes * d.layers;
+  hipError_t e = hipMalloc(&p->blocks, total);
+  if (e == hipSuccess) e = hipMemset(p->blocks, 0, total);
   if (e != hipSuccess) {
     tge_kv_pool_destroy(p);
     return fail(e == hipErrorOutOfMemory ? TGE_ERR_CAPACITY : TGE_ERR_DEVICE,
                 std::string("kv_pool_create: ") + hipGetErrorString(e));
   }
-  p->bytes = 2 * kv_total + 2 * sc_total;
+  p->bytes = total;
   *out = p;
   return TGE_OK;
 }
 
 void tge_kv_pool_destroy(tge_kv_pool* p) {
   if (!p) return;
-  if (p->k) (void)hipFree(p->k);
-  if (p->v) (void)hipFree(p->v);
-  if (p->ks) (void)hipFree(p->ks);
-  if (p->vs) (void)hipFree(p->vs);
+  if (p->blocks) (void)hipFree(p->blocks);
   delete p;
 }
 
@@ -253,14 +236,15 @@ int tge_kv_pool_layer(const tge_kv_pool* p, int layer, tge_kv_layer_view* out) {
   if (!p || !out) return fail(TGE_ERR_INVALID, "kv_pool_layer: null argument");
   if (layer < 0 || layer >= p->desc.layers)
     return fail(TGE_ERR_INVALID, "kv_pool_layer: layer out of range");
-  const size_t kv = p->kv_block_bytes * p->layer_blocks * layer;
-  const size_t sc = p->scale_block_bytes * p->layer_blocks * layer;
-  out->k = static_cast<char*>(p->k) + kv;
-  out->v = static_cast<char*>(p->v) + kv;
-  out->k_scales = p->ks ? static_cast<char*>(p->ks) + sc : nullptr;
-  out->v_scales = p->vs ? static_cast<char*>(p->vs) + sc : nullptr;
-  out->kv_block_bytes = p->kv_block_bytes;
-  out->scale_block_bytes = p->scale_block_bytes;
+  char* base = static_cast<char*>(p->blocks) + (size_t)p->geom.block_bytes * p->layer_blocks * layer;
+  const bool i8 = p->desc.format == TGE_KV_I8;
+  out->k = base;
+  out->v = base + p->geom.v_off();
+  out->k_scales = i8 ? base + p->geom.ks_off() : nullptr;
+  out->v_scales = i8 ? base + p->geom.vs_off() : nullptr;
+  out->kv_block_bytes = (size_t)p->geom.kv_bytes;
+  out->scale_block_bytes = (size_t)p->geom.scale_bytes;
+  out->block_bytes = (size_t)p->geom.block_bytes;
   return TGE_OK;
 }
 
@@ -718,12 +702,9 @@ tge::AttnParams attn_params(const tge_batch* b, const tge_kv_pool* p, int layer,
   tge_kv_layer_view v{};
   tge_kv_pool_layer(p, layer, &v);
   tge::AttnParams a{};
-  a.kpool = v.k;
-  a.vpool = v.v;
-  a.kscale = v.k_scales;
-  a.vscale = v.v_scales;
-  a.kv_array_bytes = (uint32_t)(p->kv_block_bytes * p->layer_blocks);
-  a.scale_array_bytes = (uint32_t)(p->scale_block_bytes * p->layer_blocks);
+  a.pool = v.k;
+  a.array_bytes = (uint32_t)(p->geom.block_bytes * p->layer_blocks);
+  a.block_bytes = (uint32_t)p->geom.block_bytes;
   a.sessions = reinterpret_cast<const tge::SessionRec*>(b->dev + b->off_sessions);
   a.work = reinterpret_cast<const tge::WorkRec*>(pl.dev);
   a.wg_first = pl.wg_first.empty() ? nullptr : reinterpret_cast<const int*>(pl.dev + pl.off_first);
@@ -796,10 +777,8 @@ int tge_kv_append(const tge_batch* b, tge_kv_pool* p, int layer, const float* k,
   tge::AppendParams a{};
   a.k = k;
   a.v = v;
-  a.kpool = view.k;
-  a.vpool = view.v;
-  a.kscale = view.k_scales;
-  a.vscale = view.v_scales;
+  a.pool = view.k;
+  a.geom = p->geom;
   a.rows = reinterpret_cast<const tge::RowRec*>(b->dev + b->off_rows);
   a.n_rows = (int)b->rows.size();
   a.kv_heads = b->kv_heads;
@@ -852,10 +831,8 @@ int tge_kv_gather(const tge_batch* b, const tge_kv_pool* p, int layer, int sessi
   tge_kv_layer_view view{};
   tge_kv_pool_layer(p, layer, &view);
   tge::GatherParams g{};
-  g.kpool = view.k;
-  g.vpool = view.v;
-  g.kscale = view.k_scales;
-  g.vscale = view.v_scales;
+  g.pool = view.k;
+  g.geom = p->geom;
   g.table = reinterpret_cast<const int*>(b->dev + b->off_tables) + sr.table_off;
   g.count = count;
   g.kv_heads = b->kv_heads;

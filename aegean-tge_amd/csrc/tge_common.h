@@ -7,12 +7,36 @@
 
 namespace tge {
 
-constexpr int kPageTokens = 16;  // block_table.hpp:19 kBlockTokens
-constexpr int kWaves = 4;        // waves per decode workgroup
-constexpr int kMaxRows = 64;
-constexpr int kPrefillRows = 128;  // rows of one block-prefill work item (4 waves x 32)     // query rows (n_new * group) per decode unit
+constexpr int kPageTokens = 16;   // block_table.hpp:19 kBlockTokens
+constexpr int kWaves = 4;         // waves per block-prefill workgroup
+constexpr int kMaxRows = 64;      // query rows (n_new * group) per decode unit
+constexpr int kPrefillRows = 128; // rows of one block-prefill work item (4 waves x 32)
 
 enum Format { kF16 = 1, kI8 = 2 };
+
+// ---------------------------------------------------------------------------
+// Page blocks. One layer's pool is one array of pages*kv_heads page blocks;
+// block (page, kv_head) is number page*kv_heads + kv_head, and holds its 16
+// tokens' K codes, V codes and (I8) K and V scales back to back, so one
+// block is one contiguous run of HBM (I8, D=128, f16 scales: 4352 B):
+//   [ K: 16*D elements | V: 16*D elements | K scales: 16*D/32 | V scales ]
+// ---------------------------------------------------------------------------
+struct BlockGeom {
+  int kv_bytes;     // bytes of the K (= V) part
+  int scale_bytes;  // bytes of one scale part (0 for F16)
+  int block_bytes;  // bytes of a whole block (the block stride)
+  __host__ __device__ int v_off() const { return kv_bytes; }
+  __host__ __device__ int ks_off() const { return 2 * kv_bytes; }
+  __host__ __device__ int vs_off() const { return 2 * kv_bytes + scale_bytes; }
+};
+
+__host__ __device__ inline BlockGeom block_geom(int format, int head_dim, int scale_f32) {
+  BlockGeom g;
+  g.kv_bytes = 16 * head_dim * (format == kF16 ? 2 : 1);
+  g.scale_bytes = format == kF16 ? 0 : 16 * (head_dim / 32) * (scale_f32 ? 4 : 2);
+  g.block_bytes = 2 * g.kv_bytes + 2 * g.scale_bytes;
+  return g;
+}
 
 // ---------------------------------------------------------------------------
 // Page layout. One page block = 16 tokens x head_dim (D) of one KV head; NP =

@@ -11,10 +11,8 @@ namespace tge {
 struct AppendParams {
   const float* k;  // [n_rows][kv_heads*head_dim]
   const float* v;
-  void* kpool;  // layer base of the K page blocks
-  void* vpool;
-  void* kscale;  // I8 only
-  void* vscale;
+  void* pool;      // layer base: the layer's page blocks
+  BlockGeom geom;
   const RowRec* rows;  // device, n_rows
   int n_rows;
   int kv_heads;
@@ -23,10 +21,8 @@ struct AppendParams {
 };
 
 struct GatherParams {
-  const void* kpool;
-  const void* vpool;
-  const void* kscale;
-  const void* vscale;
+  const void* pool;  // layer base
+  BlockGeom geom;
   const int* table;  // device, the session's page ids
   int count;         // positions to gather
   int kv_heads;
@@ -39,12 +35,9 @@ struct GatherParams {
 };
 
 struct AttnParams {
-  const void* kpool;  // layer base pointers
-  uint32_t kv_array_bytes;     // bytes of one layer's K (= V) array, < 2^31
-  uint32_t scale_array_bytes;  // bytes of one layer's scale array (I8)
-  const void* vpool;
-  const void* kscale;
-  const void* vscale;
+  const void* pool;       // layer base: the layer's page blocks
+  uint32_t array_bytes;   // bytes of the layer's block array, < 2^31
+  uint32_t block_bytes;   // block stride
   const SessionRec* sessions;
   const WorkRec* work;
   const int* wg_first;  // [grid+1] first work item of each workgroup, or null
@@ -72,7 +65,7 @@ struct ReduceParams {
 hipError_t launch_kv_append(int format, const AppendParams& p, hipStream_t stream);
 hipError_t launch_kv_gather(int format, const GatherParams& p, hipStream_t stream);
 // Decode attention over a balanced plan (p.wg_first required): n_groups
-// persistent workgroups of four waves.
+// persistent workgroups (a fixed number per CU, see DecodeCfg).
 hipError_t launch_decode(int format, int scale_f32, int head_dim, int row_groups, int n_groups,
                          const AttnParams& p, hipStream_t stream);
 // Block prefill: one workgroup per work item (tiles of up to 128 rows).

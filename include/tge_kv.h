@@ -77,10 +77,13 @@ const char* tge_backend_arch(void);
 
 /* ---------------------------------------------------------------------------
  * Page pool. Device memory for `layers` x `pages` x `kv_heads` page blocks.
- * Each page block holds TGE_PAGE_TOKENS tokens of one KV head:
- *   K and V: 16 * head_dim elements (f16 bits or int8 codes)
- *   I8 only, K and V scales: 16 * head_dim/32 scales (f16 bits or fp32)
- * Element (token t, dim d) of a block sits at:
+ * Each page block holds TGE_PAGE_TOKENS tokens of one KV head, its parts
+ * back to back (one contiguous run of memory per block):
+ *   K part, then V part: 16 * head_dim elements each (f16 bits or int8 codes)
+ *   I8 only, K scales, then V scales: 16 * head_dim/32 scales each (f16 bits
+ *   or fp32)
+ * Block (page, kv_head) of a layer is block number page*kv_heads + kv_head.
+ * Element (token t, dim d) of a block's part sits at:
  *   K: tge_kv_k_index(t, d, head_dim)      V: tge_kv_v_index(t, d, head_dim)
  *   scale of (t, block b = d/32): tge_kv_scale_index(t, b, head_dim)
  * head_dim must be 64 or 128 (the configurations' head sizes).
@@ -96,13 +99,16 @@ typedef struct {
   int scale_format; /* enum tge_scale_format, I8 only */
 } tge_kv_pool_desc;
 
+/* One layer of a pool: the parts of block 0; the parts of block n sit
+ * n * block_bytes further on. */
 typedef struct {
-  void* k;        /* device, pages*kv_heads blocks for this layer */
-  void* v;
+  void* k;        /* device, K part of block 0 (the layer's base address) */
+  void* v;        /* V part of block 0 */
   void* k_scales; /* NULL for F16 */
   void* v_scales;
-  size_t kv_block_bytes;    /* bytes of one K (or V) page block */
-  size_t scale_block_bytes; /* bytes of one scale page block (0 for F16) */
+  size_t kv_block_bytes;    /* bytes of one K (or V) part */
+  size_t scale_block_bytes; /* bytes of one scale part (0 for F16) */
+  size_t block_bytes;       /* bytes of a whole page block: the block stride */
 } tge_kv_layer_view;
 
 int tge_kv_pool_create(const tge_kv_pool_desc* desc, tge_kv_pool** out);

@@ -26,9 +26,17 @@ def raw_pool_rows(case, layer, s, count):
     view = case.pool.layer(layer)
     pages = case.pool.pages
     elem = np.uint16 if case.fmt == tk.KV_F16 else np.int8
-    blk = 16 * case.hd
-    kraw = tk.hip().download(view.k, np.empty(pages * case.kvh * blk, elem))
-    vraw = tk.hip().download(view.v, np.empty(pages * case.kvh * blk, elem))
+    esz = np.dtype(elem).itemsize
+    bb = view.block_bytes
+    assert view.v - view.k == 16 * case.hd * esz == view.kv_block_bytes
+    if case.fmt == tk.KV_I8:
+        sbytes = 16 * (case.hd // 32) * (4 if case.sf == tk.SCALE_F32 else 2)
+        assert view.scale_block_bytes == sbytes and bb == 2 * view.kv_block_bytes + 2 * sbytes
+        assert view.k_scales - view.k == 2 * view.kv_block_bytes
+        assert view.v_scales - view.k_scales == sbytes
+    else:
+        assert bb == 2 * view.kv_block_bytes and not view.k_scales
+    raw = tk.hip().download(view.k, np.empty(pages * case.kvh * bb, np.uint8))
     t = np.arange(16)[:, None]
     d = np.arange(case.hd)[None, :]
     n = case.hd // 32
@@ -40,9 +48,11 @@ def raw_pool_rows(case, layer, s, count):
         page = case.pages[s][pos0 // 16]
         n = min(16, count - pos0)
         for h in range(case.kvh):
-            base = (page * case.kvh + h) * blk
-            k[pos0:pos0 + n, h * case.hd:(h + 1) * case.hd] = kraw[base + kidx][:n]
-            v[pos0:pos0 + n, h * case.hd:(h + 1) * case.hd] = vraw[base + vidx][:n]
+            blk = raw[(page * case.kvh + h) * bb:(page * case.kvh + h + 1) * bb]
+            kpart = blk[:view.kv_block_bytes].view(elem)
+            vpart = blk[view.kv_block_bytes:2 * view.kv_block_bytes].view(elem)
+            k[pos0:pos0 + n, h * case.hd:(h + 1) * case.hd] = kpart[kidx][:n]
+            v[pos0:pos0 + n, h * case.hd:(h + 1) * case.hd] = vpart[vidx][:n]
     return k, v
 
 
@@ -269,6 +279,26 @@ def test_page_permutation_invariance(gpu):
         case.close()
     assert outs[0][1] != outs[1][1], "the two tables should place pages differently"
     assert np.array_equal(bits(outs[0][0]), bits(outs[1][0]))
+
+
+def test_decode_many_units_per_workgroup(gpu):
+    """Sixty sessions of a few pages each give every workgroup more units
+    than its LDS table of Q operands holds, so the table is reloaded
+    mid-share; results match the oracle and are bit-reproducible."""
+    ctx = [17 + 23 * i for i in range(60)]
+    case = PagedCase(28, 4, 128, tk.KV_I8, ctx, 4, seed=41, outlier_frac=0.01)
+    case.fill()
+    want = case.oracle_out()
+    outs = []
+    for _ in range(2):
+        out, b = case.step()
+        say(f"  plan {b.info()}")
+        assert b.info()[1] > 4 * 64, "expected several units per workgroup"
+        assert_attention_close(out, want, "many units")
+        outs.append(out)
+        b.close()
+    assert np.array_equal(bits(outs[0]), bits(outs[1]))
+    case.close()
 
 
 def test_prefill_chunks_match_oracle(gpu):
