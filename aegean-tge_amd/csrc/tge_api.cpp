@@ -390,11 +390,11 @@ Residency resident_groups(int format, int scale_f32, int head_dim, int row_group
 // older wave wins issue, so equal page shares finish far apart (measured:
 // ~25 % slower for the second). Shares are weighted by rank^k.
 #ifndef TGE_DECODE_RANK_WEIGHT
-#define TGE_DECODE_RANK_WEIGHT 0.8
+#define TGE_DECODE_RANK_WEIGHT 0.76
 #endif
 // Fixed cost of one unit of a share (start-up and merge), in pages.
 #ifndef TGE_DECODE_UNIT_COST
-#define TGE_DECODE_UNIT_COST 16
+#define TGE_DECODE_UNIT_COST 22
 #endif
 
 // Decode schedule. Every (session, kv head) is a segment of pages whose rows
