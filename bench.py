@@ -369,7 +369,7 @@ def measured_traffic(workload):
     from the committed rocprofv3 counter summary (FETCH_SIZE and WRITE_SIZE
     per dispatch, each scaled by what the counter reads for a copy of known
     size), or None when no summary covers the workload."""
-    path = os.path.join(ROOT, "profiles", "decode_attention_c5_traffic.json")
+    path = os.path.join(ROOT, "profiles", "paged_decode_kernel_c5_traffic.json")
     if not os.path.exists(path):
         return None
     with open(path) as f:
@@ -478,7 +478,7 @@ def main():
         },
         "roofline": {
             "bound": "hbm",
-            "kernel": "paged_attention_kernel (decode, int8 KV, head_dim 128)",
+            "kernel": "paged_decode_kernel (int8 KV + f16 scales, head_dim 128, 2 row groups, 4 waves x 2 workgroups per CU)",
             "achieved": round(r["attn_kernel_gbs"], 2),
             "peak": HBM_PEAK_GBS,
             "unit": "GB/s",
