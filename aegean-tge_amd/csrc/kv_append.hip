@@ -2,10 +2,10 @@
 //
 // Append replaces the reference's per-token store loops (qwen2.cpp:2073-2093
 // forward, 1681-1702 forward_batch, 2308-2329 prefill_run; i8 via
-// store_kv_q8/quantize_kv_block, qwen2.cpp:88-120). One thread owns one
-// 32-value block of one K or V row of one KV head: it reads the 128 input
-// bytes, converts or quantizes them with the reference's bit recipe, and
-// writes them straight into the page block at the token's slot. This TU is
+// store_kv_q8/quantize_kv_block, qwen2.cpp:88-120). Four lanes own one
+// 32-value block of one K or V row of one KV head: they read its 128 input
+// bytes, convert or quantize them with the reference's bit recipe, and
+// write them straight into the page block at the token's slot. This TU is
 // built with -ffp-contract=off in addition to the explicit _rn intrinsics.
 #include "tge_common.h"
 #include "tge_kernels.h"
@@ -13,16 +13,26 @@
 namespace tge {
 namespace {
 
+// Append: four lanes per (row, K|V, kv head, 32-value block), each owning 8
+// consecutive values (two 16-byte loads). f16: each lane converts its 8
+// values with the reference's float_to_half recipe. int8: the four lanes
+// combine their absmax runs in order (see FoldRun), then each computes the
+// block's scale and inverse exactly as quantize_kv_block does (correctly
+// rounded fp32 division) and quantizes its 8 values.
 template <int FMT>
 __global__ __launch_bounds__(256) void kv_append_kernel(AppendParams p) {
   const int nb = p.head_dim >> 5;
-  const long total = (long)p.n_rows * 2 * p.kv_heads * nb;
+  const long total = (long)p.n_rows * 2 * p.kv_heads * nb * 4;
   const long idx = (long)blockIdx.x * blockDim.x + threadIdx.x;
-  if (idx >= total) return;
-  // idx -> (row, which, head, block), block fastest so neighbouring threads
-  // read neighbouring 128-byte slices of the same input row.
-  const int b = (int)(idx % nb);
-  long rest = idx / nb;
+  const bool live = idx < total;  // dead lanes still take part in the shuffles
+  const long id = live ? idx : total - 1;
+  // id -> (row, which, head, block, quarter), quarter fastest so the four
+  // lanes of a block are adjacent and neighbouring blocks read neighbouring
+  // 128-byte slices of the same input row.
+  const int quarter = (int)(id & 3);
+  long rest = id >> 2;
+  const int b = (int)(rest % nb);
+  rest /= nb;
   const int h = (int)(rest % p.kv_heads);
   rest /= p.kv_heads;
   const int which = (int)(rest & 1);
@@ -30,64 +40,75 @@ __global__ __launch_bounds__(256) void kv_append_kernel(AppendParams p) {
 
   const RowRec rr = p.rows[row];
   const int kv_dim = p.kv_heads * p.head_dim;
-  const float* src = (which ? p.v : p.k) + (size_t)row * kv_dim + h * p.head_dim + b * 32;
-  float x[32];
-#pragma unroll
-  for (int i = 0; i < 8; ++i) {
-    const float4 f = reinterpret_cast<const float4*>(src)[i];
-    x[4 * i + 0] = f.x;
-    x[4 * i + 1] = f.y;
-    x[4 * i + 2] = f.z;
-    x[4 * i + 3] = f.w;
+  const float* src = (which ? p.v : p.k) + (size_t)row * kv_dim + h * p.head_dim + b * 32 + quarter * 8;
+  float x[8];
+  {
+    const float4 f0 = reinterpret_cast<const float4*>(src)[0];
+    const float4 f1 = reinterpret_cast<const float4*>(src)[1];
+    x[0] = f0.x; x[1] = f0.y; x[2] = f0.z; x[3] = f0.w;
+    x[4] = f1.x; x[5] = f1.y; x[6] = f1.z; x[7] = f1.w;
   }
   char* const blk = static_cast<char*>(p.pool) + ((size_t)rr.page * p.kv_heads + h) * p.geom.block_bytes;
   const int t = rr.slot;
+  const int d0 = 32 * b + 8 * quarter;  // first dim of this lane
+  // K chunk of (token t, dims d0..d0+3) and (d0+4..d0+7): 4 contiguous
+  // elements each (k_index_np is contiguous in d&3).
+  const int k0 = k_index_np(t, d0, nb);
+  const int k1 = k_index_np(t, d0 + 4, nb);
 
   if (FMT == kF16) {
-    uint16_t hx[32];
+    uint16_t hx[8];
 #pragma unroll
-    for (int i = 0; i < 32; ++i) hx[i] = float_to_half_ref(x[i]);
+    for (int i = 0; i < 8; ++i) hx[i] = float_to_half_ref(x[i]);
+    if (!live) return;
     if (which == 0) {
       uint16_t* dst = reinterpret_cast<uint16_t*>(blk);
-#pragma unroll
-      for (int g = 0; g < 4; ++g) {
-        uint4 w;
-        w.x = hx[4 * g + 0] | ((uint32_t)hx[4 * g + 1] << 16);
-        w.y = hx[4 * g + 2] | ((uint32_t)hx[4 * g + 3] << 16);
-        w.z = hx[16 + 4 * g + 0] | ((uint32_t)hx[16 + 4 * g + 1] << 16);
-        w.w = hx[16 + 4 * g + 2] | ((uint32_t)hx[16 + 4 * g + 3] << 16);
-        *reinterpret_cast<uint4*>(dst + k_index_np(t, 32 * b + 4 * g, nb)) = w;
-      }
+      *reinterpret_cast<uint2*>(dst + k0) = make_uint2(hx[0] | ((uint32_t)hx[1] << 16), hx[2] | ((uint32_t)hx[3] << 16));
+      *reinterpret_cast<uint2*>(dst + k1) = make_uint2(hx[4] | ((uint32_t)hx[5] << 16), hx[6] | ((uint32_t)hx[7] << 16));
     } else {
       uint16_t* dst = reinterpret_cast<uint16_t*>(blk + p.geom.v_off());
 #pragma unroll
-      for (int d = 0; d < 32; ++d) dst[v_index_np(t, 32 * b + d, nb)] = hx[d];
+      for (int i = 0; i < 8; ++i) dst[v_index_np(t, d0 + i, nb)] = hx[i];
     }
   } else {
-    int8_t c[32];
-    const float scale = quantize_block_ref(x, c);
+    // the block's absmax: lane runs joined in lane order
+    const FoldRun mine = fold_run(x);
+    const int base = (threadIdx.x & 63) & ~3;
+    FoldRun all{false, -INFINITY};
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const FoldRun o{__shfl(mine.nan ? 1 : 0, base + j) != 0, __shfl(mine.v, base + j)};
+      all = j == 0 ? o : fold_join(all, o);
+    }
+    const float maximum = all.v;
+    const float scale = __fdiv_rn(maximum, 127.0f);
+    const float inverse = scale != 0.0f ? __fdiv_rn(1.0f, scale) : 0.0f;
+    uint32_t packed[2] = {0, 0};
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      const float scaled = __fmul_rn(x[i], inverse);
+      const float rounded = scaled >= 0.0f ? __fadd_rn(scaled, 0.5f) : __fadd_rn(scaled, -0.5f);
+      int c = trunc_to_int_x86(rounded);
+      c = c > 127 ? 127 : (c < -127 ? -127 : c);
+      packed[i >> 2] |= (uint32_t)(uint8_t)(int8_t)c << (8 * (i & 3));
+    }
+    if (!live) return;
     if (which == 0) {
       int8_t* dst = reinterpret_cast<int8_t*>(blk);
-#pragma unroll
-      for (int g = 0; g < 4; ++g) {
-        uint2 w;
-        w.x = (uint8_t)c[4 * g] | ((uint32_t)(uint8_t)c[4 * g + 1] << 8) |
-              ((uint32_t)(uint8_t)c[4 * g + 2] << 16) | ((uint32_t)(uint8_t)c[4 * g + 3] << 24);
-        w.y = (uint8_t)c[16 + 4 * g] | ((uint32_t)(uint8_t)c[16 + 4 * g + 1] << 8) |
-              ((uint32_t)(uint8_t)c[16 + 4 * g + 2] << 16) |
-              ((uint32_t)(uint8_t)c[16 + 4 * g + 3] << 24);
-        *reinterpret_cast<uint2*>(dst + k_index_np(t, 32 * b + 4 * g, nb)) = w;
-      }
+      *reinterpret_cast<uint32_t*>(dst + k0) = packed[0];
+      *reinterpret_cast<uint32_t*>(dst + k1) = packed[1];
     } else {
       int8_t* dst = reinterpret_cast<int8_t*>(blk + p.geom.v_off());
 #pragma unroll
-      for (int d = 0; d < 32; ++d) dst[v_index_np(t, 32 * b + d, nb)] = c[d];
+      for (int i = 0; i < 8; ++i) dst[v_index_np(t, d0 + i, nb)] = (int8_t)(packed[i >> 2] >> (8 * (i & 3)));
     }
-    char* sp = blk + (which ? p.geom.vs_off() : p.geom.ks_off());
-    if (p.scale_f32) {
-      reinterpret_cast<float*>(sp)[scale_index_np(t, b, nb)] = scale;
-    } else {
-      reinterpret_cast<uint16_t*>(sp)[scale_index_np(t, b, nb)] = float_to_half_ref(scale);
+    if (quarter == 0) {
+      char* sp = blk + (which ? p.geom.vs_off() : p.geom.ks_off());
+      if (p.scale_f32) {
+        reinterpret_cast<float*>(sp)[scale_index_np(t, b, nb)] = scale;
+      } else {
+        reinterpret_cast<uint16_t*>(sp)[scale_index_np(t, b, nb)] = float_to_half_ref(scale);
+      }
     }
   }
 }
@@ -125,7 +146,7 @@ __global__ __launch_bounds__(256) void kv_gather_kernel(GatherParams p) {
 }  // namespace
 
 hipError_t launch_kv_append(int format, const AppendParams& p, hipStream_t stream) {
-  const long total = (long)p.n_rows * 2 * p.kv_heads * (p.head_dim >> 5);
+  const long total = (long)p.n_rows * 2 * p.kv_heads * (p.head_dim >> 5) * 4;
   if (total == 0) return hipSuccess;
   const dim3 grid((unsigned)((total + 255) / 256)), block(256);
   if (format == kF16) {

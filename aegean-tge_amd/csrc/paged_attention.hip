@@ -271,6 +271,103 @@ struct Unit {
     return part ? qlo[rg][pp] : qhi[rg][pp];
   }
 
+  // S^T = K.Q^T of one page for every row group (fp32, K scales applied).
+  template <class QF>
+  __device__ __forceinline__ void scores(const Regs& r, const QF& qf, float4_t (&sacc)[NRG]) const {
+#pragma unroll
+    for (int rg = 0; rg < NRG; ++rg) sacc[rg] = float4_t{0, 0, 0, 0};
+#pragma unroll
+    for (int pp = 0; pp < NP; ++pp) {
+      const half8_t ka = k_operand<FMT, SF32, D>(r, pp);
+      if (FMT == kF16) {
+#pragma unroll
+        for (int rg = 0; rg < NRG; ++rg) {
+          sacc[rg] = MFMA16x16x32(ka, qf(rg, pp, 0), sacc[rg]);
+          if (QSPLIT) sacc[rg] = MFMA16x16x32(ka, qf(rg, pp, 1), sacc[rg]);
+        }
+      } else {
+        const float4_t ks = scales4<SF32>(r.ks, pp);
+#pragma unroll
+        for (int rg = 0; rg < NRG; ++rg) {
+          float4_t b = MFMA16x16x32(ka, qf(rg, pp, 0), (float4_t{0, 0, 0, 0}));
+          if (QSPLIT) b = MFMA16x16x32(ka, qf(rg, pp, 1), b);
+#pragma unroll
+          for (int e = 0; e < 4; ++e) sacc[rg][e] = fmaf(b[e], ks[e], sacc[rg][e]);
+        }
+      }
+    }
+  }
+
+  // V^T operand (16 dims x 4 tokens per lane) of 16-dim tile 2pp+h.
+  __device__ __forceinline__ half4_t v_operand(const Regs& r, int pp, int h) const {
+    if (FMT == kF16) {
+      return as_half4(r.v[4 * pp + 2 * h], r.v[4 * pp + 2 * h + 1]);
+    } else if (SF32) {
+      const float4_t sv = scales4<SF32>(r.vs, pp);
+      const half4_t c = i8x4_to_half4(r.v[2 * pp + h]);
+      return half4_t{(_Float16)((float)c[0] * sv[0]), (_Float16)((float)c[1] * sv[1]),
+                     (_Float16)((float)c[2] * sv[2]), (_Float16)((float)c[3] * sv[3])};
+    } else {
+      return i8x4_to_half4(r.v[2 * pp + h]) * as_half4(r.vs[2 * pp], r.vs[2 * pp + 1]);
+    }
+  }
+
+  // Two pages at once: the QK products of both, one softmax update over the
+  // 32 positions, and the value and row-sum products on 16x16x32 MFMAs with
+  // k = 8g + j = token 4g+j of page A (j < 4) or 4g+j-4 of page B: lane (g, c)
+  // already holds exactly those tokens of both pages, for P as for V.
+  template <class QF>
+  __device__ __forceinline__ void consume2(const Regs& ra, const Regs& rb, int pia, int pib, int grp,
+                                           bool masked_a, bool masked_b, const QF& qf) {
+    float4_t sa[NRG], sb[NRG];
+    scores(ra, qf, sa);
+    scores(rb, qf, sb);
+    half8_t pw[NRG];
+#pragma unroll
+    for (int rg = 0; rg < NRG; ++rg) {
+      sa[rg] -= base[rg];
+      sb[rg] -= base[rg];
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        if (masked_a && pia * 16 + 4 * grp + e > lim[rg]) sa[rg][e] = -INFINITY;
+        if (masked_b && pib * 16 + 4 * grp + e > lim[rg]) sb[rg][e] = -INFINITY;
+      }
+      const float lmax = fmaxf(fmaxf(fmaxf(sa[rg][0], sa[rg][1]), fmaxf(sa[rg][2], sa[rg][3])),
+                               fmaxf(fmaxf(sb[rg][0], sb[rg][1]), fmaxf(sb[rg][2], sb[rg][3])));
+      if (__builtin_expect(__any(lmax > thr[rg]), 0)) {
+        float rmax = fmaxf(lmax, __shfl_xor(lmax, 16));
+        rmax = fmaxf(rmax, __shfl_xor(rmax, 32));
+        const bool grow = rmax > thr[rg];
+        const float delta = grow ? ceilf(rmax) : 0.0f;
+        const float alpha = (grow && thr[rg] != -INFINITY) ? pow2i(-delta) : 1.0f;
+        base[rg] += delta;
+        thr[rg] = grow ? kLazyMax : thr[rg];
+        sa[rg] -= delta;
+        sb[rg] -= delta;
+        l4[rg] *= alpha;
+#pragma unroll
+        for (int t = 0; t < NT; ++t) o[rg][t] *= alpha;
+      }
+      pw[rg] = half8_t{(_Float16)__builtin_amdgcn_exp2f(sa[rg][0]), (_Float16)__builtin_amdgcn_exp2f(sa[rg][1]),
+                       (_Float16)__builtin_amdgcn_exp2f(sa[rg][2]), (_Float16)__builtin_amdgcn_exp2f(sa[rg][3]),
+                       (_Float16)__builtin_amdgcn_exp2f(sb[rg][0]), (_Float16)__builtin_amdgcn_exp2f(sb[rg][1]),
+                       (_Float16)__builtin_amdgcn_exp2f(sb[rg][2]), (_Float16)__builtin_amdgcn_exp2f(sb[rg][3])};
+      const half8_t ones = {(_Float16)1.0f, (_Float16)1.0f, (_Float16)1.0f, (_Float16)1.0f,
+                            (_Float16)1.0f, (_Float16)1.0f, (_Float16)1.0f, (_Float16)1.0f};
+      l4[rg] = MFMA16x16x32(ones, pw[rg], l4[rg]);
+    }
+#pragma unroll
+    for (int pp = 0; pp < NP; ++pp) {
+#pragma unroll
+      for (int h = 0; h < 2; ++h) {
+        const half4_t va = v_operand(ra, pp, h), vb = v_operand(rb, pp, h);
+        const half8_t v8 = {va[0], va[1], va[2], va[3], vb[0], vb[1], vb[2], vb[3]};
+#pragma unroll
+        for (int rg = 0; rg < NRG; ++rg) o[rg][2 * pp + h] = MFMA16x16x32(v8, pw[rg], o[rg][2 * pp + h]);
+      }
+    }
+  }
+
   // One page with the Q^T operands held in this unit's registers.
   __device__ __forceinline__ void consume(const Regs& r, int pi, int grp, bool masked) {
     consume_with(r, pi, grp, masked,
@@ -900,12 +997,18 @@ void paged_prefill_kernel(AttnParams p) {
     if (has_rows) {
       const char* tile = sh.ring + (k % NB) * SH::TILE;
 #pragma unroll
-      for (int j = 0; j < kWaves; ++j) {
+      for (int j = 0; j < kWaves; j += 2) {
         const int pg = k * kWaves + j;
-        if (pg < npages) {
+        const int pi = w.page_begin + pg;
+        if (pg + 1 < npages) {
+          Regs ra, rb;
+          read_page<FMT, SF32, D>(ra, tile + j * RG::SLOT, lane, grp);
+          read_page<FMT, SF32, D>(rb, tile + (j + 1) * RG::SLOT, lane, grp);
+          u.consume2(ra, rb, pi, pi + 1, grp, pi >= unmasked, pi + 1 >= unmasked,
+                     [&](int rg, int pp, int part) __attribute__((always_inline)) { return u.qop(rg, pp, part); });
+        } else if (pg < npages) {
           Regs r;
           read_page<FMT, SF32, D>(r, tile + j * RG::SLOT, lane, grp);
-          const int pi = w.page_begin + pg;
           u.consume(r, pi, grp, pi >= unmasked);
         }
       }
@@ -1108,7 +1211,11 @@ int decode_blocks_per_cu(int format, int scale_f32, int head_dim, int row_groups
 
 template <int FMT, bool SF32, int D, bool QSPLIT>
 hipError_t launch_prefill_d(int n_units, const AttnParams& p, hipStream_t stream) {
+#ifdef TGE_PREFILL_WPE
+  constexpr int wpe = TGE_PREFILL_WPE;
+#else
   constexpr int wpe = waves_per_eu<FMT, D, 2, QSPLIT>();
+#endif
   hipLaunchKernelGGL((paged_prefill_kernel<FMT, SF32, D, QSPLIT, wpe>), dim3((unsigned)n_units),
                      dim3(256), 0, stream, p);
   return hipGetLastError();

@@ -530,8 +530,12 @@ void build_prefill(tge_batch* b) {
     for (int a = 0; a < sr.n_new; a += tq)
       pages_total += (long)((sr.ctx + std::min(sr.n_new, a + tq) + 15) / 16) * b->kv_heads;
   }
+#ifndef TGE_PREFILL_MIN_SPLIT
+#define TGE_PREFILL_MIN_SPLIT 32
+#endif
   const long target_units = 2L * 256 * 2;
-  const int pps = (int)std::max<long>(32, ((pages_total + target_units - 1) / target_units + 3) / 4 * 4);
+  const int pps = (int)std::max<long>(TGE_PREFILL_MIN_SPLIT,
+                                      ((pages_total + target_units - 1) / target_units + 3) / 4 * 4);
   for (int s = 0; s < (int)b->sessions.size(); ++s) {
     const tge::SessionRec& sr = b->sessions[s];
     for (int h = 0; h < b->kv_heads; ++h) {

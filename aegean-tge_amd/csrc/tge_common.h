@@ -193,4 +193,42 @@ __host__ __device__ inline float quantize_block_ref(const float* x, int8_t* code
   return scale;
 }
 
+// The reference's absmax fold over a block, `if (!(m > a)) m = a` for
+// a = |x| as `x >= 0 ? x : -x` (qwen2.cpp:90-93), split over the 4 lanes that
+// hold 8 values each. A lane summarises its run as (nan, v): without a NaN,
+// v is the run's fold from -inf (its maximum; the later of equal values, so
+// an all-zero run keeps the sign of its last element); with a NaN, the fold
+// restarts after the last NaN whatever came before, and v is that restarted
+// fold (NaN itself when the run ends with a NaN). Runs combine in order:
+// a run with a NaN overrides what precedes it, otherwise the later run wins
+// unless the earlier value is strictly greater. Starting the block's fold
+// from +0 changes nothing (every a is >= -0 or NaN), so the block's maximum
+// is the combined v.
+struct FoldRun {
+  bool nan;
+  float v;
+};
+
+__host__ __device__ inline float fold_step(float m, float a) { return (m > a) ? m : a; }
+
+__host__ __device__ inline FoldRun fold_run(const float* x) {
+  FoldRun r{false, -__builtin_huge_valf()};
+#pragma unroll
+  for (int i = 0; i < 8; ++i) {
+    const float a = x[i] >= 0.0f ? x[i] : -x[i];
+    if (a != a) {
+      r.nan = true;
+      r.v = a;  // the state after a NaN is the NaN; the next value replaces it
+    } else {
+      r.v = fold_step(r.v, a);
+    }
+  }
+  return r;
+}
+
+__host__ __device__ inline FoldRun fold_join(FoldRun first, FoldRun then) {
+  if (then.nan) return then;
+  return FoldRun{first.nan, fold_step(first.v, then.v)};
+}
+
 }  // namespace tge
