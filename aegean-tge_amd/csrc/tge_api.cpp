@@ -248,6 +248,22 @@ int tge_kv_pool_layer(const tge_kv_pool* p, int layer, tge_kv_layer_view* out) {
   return TGE_OK;
 }
 
+int tge_kv_copy_page(tge_kv_pool* p, int src_page, int dst_page, void* stream) {
+  if (!p) return fail(TGE_ERR_INVALID, "kv_copy_page: null pool");
+  if (src_page < 0 || src_page >= p->desc.pages || dst_page < 0 || dst_page >= p->desc.pages)
+    return fail(TGE_ERR_INVALID, "kv_copy_page: page outside the pool");
+  if (src_page == dst_page) return TGE_OK;
+  // A page's blocks are kv_heads consecutive blocks in every layer's array:
+  // one strided copy of `layers` rows.
+  const size_t row = (size_t)p->geom.block_bytes * p->desc.kv_heads;
+  const size_t pitch = (size_t)p->geom.block_bytes * p->layer_blocks;
+  char* base = static_cast<char*>(p->blocks);
+  TGE_HIP(hipMemcpy2DAsync(base + row * dst_page, pitch, base + row * src_page, pitch, row,
+                           (size_t)p->desc.layers, hipMemcpyDeviceToDevice,
+                           static_cast<hipStream_t>(stream)));
+  return TGE_OK;
+}
+
 // ---------------------------------------------------------------------------
 // Batch plan
 // ---------------------------------------------------------------------------

@@ -77,6 +77,16 @@ const std::vector<int>& Qwen2KvPath::pages(int sequence) const {
   return pages_[static_cast<std::size_t>(sequence)];
 }
 
+// Pages [first, last] of `list` that the step writes and another sequence
+// also holds (reference count above one): they are copied before the write.
+static int shared_in(const BlockTable& table, const std::vector<int>& list, int first, int last) {
+  int n = 0;
+  for (int k = first; k <= last && k < static_cast<int>(list.size()); ++k) {
+    if (table.refcount(list[static_cast<std::size_t>(k)]) > 1) ++n;
+  }
+  return n;
+}
+
 void Qwen2KvPath::begin(const std::vector<Group>& groups, void* stream) {
   begun_ = false;
   // Validate everything before touching the table, so a failed call leaves
@@ -94,6 +104,7 @@ void Qwen2KvPath::begin(const std::vector<Group>& groups, void* stream) {
       extra += need - have;
       need_pages[s] = need;
     }
+    extra += shared_in(*table_, pages_[s], g.start / kBlockTokens, need - 1);
   }
   if (extra > table_->free_count()) throw std::runtime_error("BlockTable: table full");
 
@@ -102,6 +113,17 @@ void Qwen2KvPath::begin(const std::vector<Group>& groups, void* stream) {
   for (const Group& g : groups) {
     auto& list = pages_[static_cast<std::size_t>(g.sequence)];
     const int need = (g.start + g.count + kBlockTokens - 1) / kBlockTokens;
+    // Copy-on-write: a written page still held by another sequence is
+    // replaced by a private copy (all layers) before this step's append.
+    for (int k = g.start / kBlockTokens; k < need && k < static_cast<int>(list.size()); ++k) {
+      const int old = list[static_cast<std::size_t>(k)];
+      if (table_->refcount(old) > 1) {
+        const int fresh = table_->allocate();
+        check(tge_kv_copy_page(pool_, old, fresh, stream), "begin");
+        table_->release(old);
+        list[static_cast<std::size_t>(k)] = fresh;
+      }
+    }
     while (static_cast<int>(list.size()) < need) list.push_back(table_->allocate());
     length_[static_cast<std::size_t>(g.sequence)] = g.start + g.count;
     ctx.push_back(g.start);
@@ -205,6 +227,57 @@ void Qwen2KvPath::store(int layer, const float* k, const float* v, void* stream)
     throw std::invalid_argument("store: layer out of range");
   }
   check(tge_kv_append(batch_, pool_, layer, k, v, stream), "store");
+}
+
+int Qwen2KvPath::remember_prefix(int sequence, const int* tokens, int count) {
+  check_sequence(sequence, "remember_prefix");
+  if (count < 0 || (count > 0 && tokens == nullptr)) {
+    throw std::runtime_error("remember_prefix: invalid tokens");
+  }
+  const auto& list = pages_[static_cast<std::size_t>(sequence)];
+  const int full = std::min(count, length_[static_cast<std::size_t>(sequence)]) / kBlockTokens;
+  std::uint64_t h = BlockTable::hash_tokens(nullptr, 0);
+  for (int k = 0; k < full; ++k) {
+    h = BlockTable::hash_extend(h, tokens + k * kBlockTokens, kBlockTokens);
+    table_->remember_prefix(h, list[static_cast<std::size_t>(k)]);
+  }
+  return full;
+}
+
+int Qwen2KvPath::shared_prefix_len(const int* tokens, int count) const {
+  if (count < 0 || (count > 0 && tokens == nullptr)) {
+    throw std::runtime_error("shared_prefix_len: invalid tokens");
+  }
+  std::uint64_t h = BlockTable::hash_tokens(nullptr, 0);
+  int k = 0;
+  for (; (k + 1) * kBlockTokens <= count; ++k) {
+    h = BlockTable::hash_extend(h, tokens + k * kBlockTokens, kBlockTokens);
+    if (table_->find_prefix(h) < 0) break;
+  }
+  return k * kBlockTokens;
+}
+
+int Qwen2KvPath::attach_prefix(int sequence, const int* tokens, int count) {
+  check_sequence(sequence, "attach_prefix");
+  if (count < 0 || (count > 0 && tokens == nullptr)) {
+    throw std::runtime_error("attach_prefix: invalid tokens");
+  }
+  auto& list = pages_[static_cast<std::size_t>(sequence)];
+  if (!list.empty() || length_[static_cast<std::size_t>(sequence)] != 0) {
+    throw std::runtime_error("attach_prefix: the sequence is not empty");
+  }
+  std::uint64_t h = BlockTable::hash_tokens(nullptr, 0);
+  const int limit = std::min(count, config_.context);
+  for (int k = 0; (k + 1) * kBlockTokens <= limit; ++k) {
+    h = BlockTable::hash_extend(h, tokens + k * kBlockTokens, kBlockTokens);
+    const int block = table_->find_prefix(h);
+    if (block < 0) break;
+    table_->share(block);
+    list.push_back(block);
+  }
+  length_[static_cast<std::size_t>(sequence)] = static_cast<int>(list.size()) * kBlockTokens;
+  begun_ = false;
+  return length_[static_cast<std::size_t>(sequence)];
 }
 
 void Qwen2KvPath::reset_cache(int sequence) {
@@ -379,6 +452,24 @@ int tge_qwen2_kv_pages(const tge_qwen2_kv* m, int sequence, int* ids, int cap) {
     n = static_cast<int>(list.size());
     for (int i = 0; i < std::min(n, cap); ++i) ids[i] = list[static_cast<std::size_t>(i)];
   });
+  return s == TGE_OK ? n : s;
+}
+int tge_qwen2_kv_remember_prefix(tge_qwen2_kv* m, int sequence, const int* tokens, int count) {
+  if (!m) return TGE_ERR_INVALID;
+  int n = 0;
+  const int s = guarded([&] { n = m->impl.remember_prefix(sequence, tokens, count); });
+  return s == TGE_OK ? n : s;
+}
+int tge_qwen2_kv_shared_prefix_len(const tge_qwen2_kv* m, const int* tokens, int count) {
+  if (!m) return TGE_ERR_INVALID;
+  int n = 0;
+  const int s = guarded([&] { n = m->impl.shared_prefix_len(tokens, count); });
+  return s == TGE_OK ? n : s;
+}
+int tge_qwen2_kv_attach_prefix(tge_qwen2_kv* m, int sequence, const int* tokens, int count) {
+  if (!m) return TGE_ERR_INVALID;
+  int n = 0;
+  const int s = guarded([&] { n = m->impl.attach_prefix(sequence, tokens, count); });
   return s == TGE_OK ? n : s;
 }
 const tge_kv_pool* tge_qwen2_kv_pool(const tge_qwen2_kv* m) { return m ? m->impl.pool() : nullptr; }

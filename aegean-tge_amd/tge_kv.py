@@ -67,6 +67,7 @@ SIGNATURES = [
     ("tge_kv_pool_destroy", None, [_VP]),
     ("tge_kv_pool_layer", _I, [_VP, _I, C.POINTER(LayerView)]),
     ("tge_kv_pool_bytes", C.c_size_t, [_VP]),
+    ("tge_kv_copy_page", _I, [_VP, _I, _I, _VP]),
     ("tge_kv_k_index", _I, [_I, _I, _I]),
     ("tge_kv_v_index", _I, [_I, _I, _I]),
     ("tge_kv_scale_index", _I, [_I, _I, _I]),
@@ -107,6 +108,9 @@ SIGNATURES = [
     ("tge_qwen2_kv_batch", _VP, [_VP]),
     ("tge_qwen2_kv_free_pages", _I, [_VP]),
     ("tge_qwen2_kv_table", _VP, [_VP]),
+    ("tge_qwen2_kv_remember_prefix", _I, [_VP, _I, _PI, _I]),
+    ("tge_qwen2_kv_shared_prefix_len", _I, [_VP, _PI, _I]),
+    ("tge_qwen2_kv_attach_prefix", _I, [_VP, _I, _PI, _I]),
 ]
 
 
@@ -363,6 +367,9 @@ class KvPool:
     def bytes(self):
         return lib().tge_kv_pool_bytes(self.h)
 
+    def copy_page(self, src, dst, stream=None):
+        check(lib().tge_kv_copy_page(self.h, src, dst, stream), "kv_copy_page")
+
     def close(self):
         if self.h:
             lib().tge_kv_pool_destroy(self.h)
@@ -530,6 +537,28 @@ class Qwen2KvPath:
 
     def free_pages(self):
         return lib().tge_qwen2_kv_free_pages(self.h)
+
+    def _count(self, n, what):
+        if n < 0:
+            check(n, what)
+        return n
+
+    def remember_prefix(self, sequence, tokens):
+        """Keys the sequence's full cached pages among `tokens`; returns the pages keyed."""
+        arr = _ints(tokens) if len(tokens) else None
+        return self._count(lib().tge_qwen2_kv_remember_prefix(self.h, sequence, arr, len(tokens)),
+                           "remember_prefix")
+
+    def shared_prefix_len(self, tokens):
+        arr = _ints(tokens) if len(tokens) else None
+        return self._count(lib().tge_qwen2_kv_shared_prefix_len(self.h, arr, len(tokens)),
+                           "shared_prefix_len")
+
+    def attach_prefix(self, sequence, tokens):
+        """Shares the longest remembered page chain of `tokens`; returns the cached length."""
+        arr = _ints(tokens) if len(tokens) else None
+        return self._count(lib().tge_qwen2_kv_attach_prefix(self.h, sequence, arr, len(tokens)),
+                           "attach_prefix")
 
     def table(self):
         """A view of the driver's BlockTable (not owned)."""

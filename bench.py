@@ -64,7 +64,7 @@ def parse():
     ap.add_argument("--cpu", dest="cpu", action="store_true", default=True)
     ap.add_argument("--no-cpu", dest="cpu", action="store_false")
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
-    ap.add_argument("--only", default="", help="run one config key (c1..c5) and print it")
+    ap.add_argument("--only", default="", help="run one config key (c1..c5, prefix) and print it")
     ap.add_argument("--calibrate-copy", action="store_true",
                     help="only time 1 GiB device-to-device copies (counter calibration)")
     ap.add_argument("--fragment-c5", action="store_true",
@@ -297,6 +297,108 @@ def run_prefill(tk, synth, cfg, reps=3):
     return res
 
 
+def run_prefix(tk, synth, cfg, sessions=8, prefix=2048, private=256, reps=3):
+    """Shared-prefix serving on the c5 shape: `sessions` sessions whose first
+    `prefix` tokens are one remembered page chain (attached by reference
+    count), each followed by `private` tokens of its own, against the same
+    sessions holding every page privately. Reports the attach cost (host),
+    the prefix's store cost it replaces, pages saved, the copy-on-write cost
+    of one page, and the decode attention kernel (4-query verify) on both."""
+    sh = cfg.shape
+    L = sh.layers
+    rng = np.random.default_rng(cfg.seed + 7)
+    toks = [int(x) for x in rng.integers(0, 150000, prefix)]
+    span = prefix + private
+    pages_each = -(-(span + cfg.n_new) // 16)
+    kf, vf = synth.make_kv(rng, span, sh.kv_dim, cfg)
+    dk, dv = tk.DeviceArray.from_numpy(kf), tk.DeviceArray.from_numpy(vf)
+    rows = sessions * cfg.n_new
+    q = tk.DeviceArray.from_numpy(synth.make_q(rng, rows, sh.q_dim, cfg))
+    kn, vn = synth.make_kv(rng, rows, sh.kv_dim, cfg)
+    dkn, dvn = tk.DeviceArray.from_numpy(kn), tk.DeviceArray.from_numpy(vn)
+    out = tk.DeviceArray((rows, sh.q_dim), np.float32)
+    hip = tk.hip()
+    lib = tk.lib()
+    row_bytes = sh.kv_dim * 4
+
+    def store(model, s, start, count):
+        model.begin_prefill(s, start, count)
+        for layer in range(L):
+            model.store(layer, dk.ptr + start * row_bytes, dv.ptr + start * row_bytes)
+
+    def decode_kernel_us(model):
+        positions = [span + i for s in range(sessions) for i in range(cfg.n_new)]
+        seqs = [s for s in range(sessions) for _ in range(cfg.n_new)]
+        model.begin_forward_batch(positions, seqs)
+        for layer in range(L):
+            model.store(layer, dkn.ptr, dvn.ptr)
+        batch, pool = model.batch_handle(), model.pool_handle()
+        tk.check(lib.tge_batch_set_profiling(batch, 1))
+        for _ in range(reps):
+            for layer in range(L):
+                tk.check(lib.tge_decode_attention(batch, pool, layer, q.ptr, out.ptr, None))
+        n, a, m = C.c_int(), C.c_float(), C.c_float()
+        tk.check(lib.tge_batch_kernel_times(batch, C.byref(n), C.byref(a), C.byref(m)))
+        tk.check(lib.tge_batch_set_profiling(batch, 0))
+        return a.value / n.value, m.value / n.value
+
+    res = {"sessions": sessions, "prefix_tokens": prefix, "private_tokens": private,
+           "queries_per_session": cfg.n_new}
+    # shared: session 0 stores the prefix and keys it; the others attach it
+    shared = tk.Qwen2KvPath(L, sh.q_heads, sh.kv_heads, sh.head_dim, context=span + 64,
+                            sequences=sessions, pages=sessions * pages_each, fmt=cfg.fmt,
+                            scale_format=tk.SCALE_F16)
+    hip.sync()
+    t0 = time.perf_counter()
+    store(shared, 0, 0, prefix)
+    hip.sync()
+    res["prefix_store_ms"] = 1e3 * (time.perf_counter() - t0)
+    shared.remember_prefix(0, toks)
+    t0 = time.perf_counter()
+    for s in range(1, sessions):
+        assert shared.attach_prefix(s, toks) == prefix
+    res["attach_us_per_session"] = 1e6 * (time.perf_counter() - t0) / (sessions - 1)
+    for s in range(sessions):
+        store(shared, s, prefix, private)
+    hip.sync()
+    a_sh, m_sh = decode_kernel_us(shared)
+    # copy-on-write of one page (every layer) into a spare page, timed with events
+    pool = shared.pool_handle()
+    used = shared.pages(0)[0]
+    tab = shared.table()
+    fresh = tab.allocate()
+    e0, e1 = hip.event(), hip.event()
+    hip.record(e0)
+    for _ in range(10):
+        tk.check(lib.tge_kv_copy_page(pool, used, fresh, None))
+    hip.record(e1)
+    res["copy_page_us"] = hip.elapsed_ms(e0, e1) * 1e3 / 10
+    tab.release(fresh)
+    free_shared = shared.free_pages()
+    shared.close()
+    # private: every session stores the prefix itself
+    priv = tk.Qwen2KvPath(L, sh.q_heads, sh.kv_heads, sh.head_dim, context=span + 64,
+                          sequences=sessions, pages=sessions * pages_each, fmt=cfg.fmt,
+                          scale_format=tk.SCALE_F16)
+    for s in range(sessions):
+        store(priv, s, 0, span)
+    hip.sync()
+    a_pr, m_pr = decode_kernel_us(priv)
+    res["pages_saved"] = free_shared - priv.free_pages()
+    priv.close()
+    att_b = synth.algorithmic_bytes_decode(sh, cfg.fmt, [span + cfg.n_new] * sessions, cfg.n_new)
+    res.update({
+        "attn_bytes_per_launch": att_b,
+        "attn_kernel_us_shared": a_sh, "merge_kernel_us_shared": m_sh,
+        "attn_kernel_us_private": a_pr, "merge_kernel_us_private": m_pr,
+        "attn_gbs_shared": att_b / (a_sh * 1e-6) / 1e9,
+        "attn_gbs_private": att_b / (a_pr * 1e-6) / 1e9,
+    })
+    for a in (dk, dv, q, dkn, dvn, out):
+        a.close()
+    return res
+
+
 def cpu_baseline_c5(synth, cfg, seconds):
     """The reference's forward_batch attention schedule (per (row, head)
     attention_head_avx2, parallel over rows) with its own AVX2 kernels from
@@ -416,9 +518,14 @@ def main():
     tk.require_gpu()
     cfgs = synth.configs()
     others = {}
-    keys = [args.only] if args.only else (["c1", "c2", "c3", "c4"] if args.others else [])
+    keys = [args.only] if args.only else (["c1", "c2", "c3", "c4", "prefix"] if args.others else [])
     for key in keys:
         if key == "c5":
+            continue
+        if key == "prefix":
+            log("[bench] prefix: 8 sessions sharing a 2048-token prefix (c5 shape)")
+            others[key] = run_prefix(tk, synth, cfgs["c5"])
+            log(f"[bench] prefix: {json.dumps(others[key])}")
             continue
         cfg = cfgs[key]
         log(f"[bench] {key}: {cfg.note}")

@@ -77,10 +77,15 @@ class BlockTable {
   }
 
   static std::uint64_t hash_tokens(const int* tokens, int count) {
+    return hash_extend(kFnvBasis, tokens, count);
+  }
+
+  // The hash of a token run continued by `count` more tokens: hash_tokens of
+  // a longer run is hash_extend of its head's hash over the tail.
+  static std::uint64_t hash_extend(std::uint64_t h, const int* tokens, int count) {
     if (count < 0 || (count > 0 && tokens == nullptr)) {
       throw std::runtime_error("BlockTable: bad hash arguments");
     }
-    std::uint64_t h = kFnvBasis;
     for (int i = 0; i < count; ++i) {
       const auto word = static_cast<std::uint32_t>(tokens[i]);
       for (int shift = 0; shift < 32; shift += 8) {

@@ -69,6 +69,20 @@ class Qwen2KvPath {
   // qwen2.cpp:1973-2026, copies rows into a slot with no recompute).
   void store(int layer, const float* k, const float* v, void* stream = nullptr);
 
+  // Shared prefixes over pages. Page k of a sequence is keyed by the hash of
+  // its tokens [0, 16(k+1)), so one hit covers every page before it.
+  // remember_prefix keys the sequence's full cached pages among the first
+  // `count` tokens (the populate step, qwen2.cpp:2388-2465); returns the
+  // pages keyed. shared_prefix_len is the token length of the longest keyed
+  // page chain `tokens` starts with (qwen2.cpp:1948-1971, whole pages).
+  // attach_prefix gives an empty sequence that chain by reference count
+  // (BlockTable::share; qwen2.cpp:1973-2026 copies rows instead) and
+  // returns its cached length. A step that writes into a page another
+  // sequence also holds copies the page first (copy-on-write).
+  int remember_prefix(int sequence, const int* tokens, int count);
+  int shared_prefix_len(const int* tokens, int count) const;
+  int attach_prefix(int sequence, const int* tokens, int count);
+
   // reset_cache(sequence): the sequence's pages go back to the table in
   // logical order; reset_cache() does every sequence.
   void reset_cache(int sequence);

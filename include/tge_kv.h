@@ -117,6 +117,11 @@ int tge_kv_pool_layer(const tge_kv_pool* pool, int layer,
                       tge_kv_layer_view* out);
 /* Device bytes the pool holds. */
 size_t tge_kv_pool_bytes(const tge_kv_pool* pool);
+/* Copy page src's blocks (every layer, every KV head) over page dst: the copy
+ * of copy-on-write prefix sharing. The reference copies a prefix's flat rows
+ * into the new slot instead (prime_cache_from_table, qwen2.cpp:1973-2026).
+ * Asynchronous on `stream`. */
+int tge_kv_copy_page(tge_kv_pool* pool, int src_page, int dst_page, void* stream);
 
 /* In-page element index of (token, dim) for K and V blocks, and of the
  * scale of (token, 32-dim block). With NP = head_dim/32:
@@ -304,6 +309,29 @@ int tge_qwen2_kv_pages(const tge_qwen2_kv* model, int sequence, int* ids,
 const tge_kv_pool* tge_qwen2_kv_pool(const tge_qwen2_kv* model);
 const tge_batch* tge_qwen2_kv_batch(const tge_qwen2_kv* model);
 int tge_qwen2_kv_free_pages(const tge_qwen2_kv* model);
+/* Shared prefixes over pages (the BlockTable recipe of prefix sharing,
+ * replacing the reference's four-slot snapshot table, qwen2.cpp:40-72).
+ * A full page of a sequence is keyed by the hash of every token up to its
+ * end (hash_tokens of tokens[0, 16(k+1)) for page k), so a hit on page k
+ * implies the same tokens at the same positions for pages 0..k.
+ *
+ * remember_prefix: key the sequence's full, cached pages among the first
+ * `count` tokens (the populate step, qwen2.cpp:2388-2465, without its
+ * four-slot and 256-token caps).
+ * shared_prefix_len: tokens of the longest remembered page chain that
+ * `tokens` starts with (qwen2.cpp:1948-1971; whole pages here).
+ * attach_prefix: an empty sequence takes that chain by reference count
+ * (no copy; qwen2.cpp:1973-2026 copies rows) and is cached up to the
+ * returned length; the caller prefills from there. A later step that
+ * writes into a page another sequence still holds copies it first
+ * (copy-on-write), so sharers never see each other's writes. */
+int tge_qwen2_kv_remember_prefix(tge_qwen2_kv* model, int sequence,
+                                 const int* tokens, int count);
+int tge_qwen2_kv_shared_prefix_len(const tge_qwen2_kv* model, const int* tokens,
+                                   int count);
+int tge_qwen2_kv_attach_prefix(tge_qwen2_kv* model, int sequence,
+                               const int* tokens, int count);
+
 /* The driver's own block table (a view, owned by the driver; do not destroy).
  * Lets a caller pre-shape the free list before the first step; pages held by
  * sequences must not be released through it. */

@@ -229,3 +229,46 @@ int main() {
                     str(exe)], check=True)
     out = subprocess.run([str(exe)], check=True, capture_output=True, text=True).stdout.split()
     assert out == ["0", "1", "0", "1", "1", "1"]
+
+
+def test_prefix_chain_hashes(tmp_path):
+    """hash_extend continues a token run's hash: the chain the driver keys
+    page k under (tokens [0, 16(k+1))) equals hash_tokens of each whole
+    prefix, restated independently by the oracle's FNV-1a."""
+    gxx = shutil.which("g++")
+    if gxx is None:
+        pytest.skip("g++ not available")
+    src = tmp_path / "h.cpp"
+    src.write_text(r'''
+#include "tge_amd/block_table.hpp"
+#include <cinttypes>
+#include <cstdio>
+int main() {
+  using tge::models::BlockTable;
+  int toks[50];
+  for (int i = 0; i < 50; ++i) toks[i] = 1000 + 37 * i - (i % 3 == 0 ? 5000 : 0);
+  std::uint64_t h = BlockTable::hash_tokens(nullptr, 0);
+  for (int k = 0; k < 3; ++k) {
+    h = BlockTable::hash_extend(h, toks + 16 * k, 16);
+    std::printf("%" PRIu64 " %" PRIu64 "\n", h, BlockTable::hash_tokens(toks, 16 * (k + 1)));
+  }
+  return 0;
+}
+''')
+    exe = tmp_path / "h"
+    subprocess.run([gxx, "-std=c++20", "-O1", "-I", os.path.join(ROOT, "include"), str(src), "-o",
+                    str(exe)], check=True)
+    lines = subprocess.run([str(exe)], check=True, capture_output=True, text=True).stdout.split("\n")
+    toks = [1000 + 37 * i - (5000 if i % 3 == 0 else 0) for i in range(50)]
+    for k in range(3):
+        chained, whole = (int(x) for x in lines[k].split())
+        assert chained == whole == O.OracleBlockTable.hash_tokens(toks[:16 * (k + 1)])
+
+
+def test_prefix_entry_points_reject_null_handles(tk):
+    L = tk.lib()
+    toks = (C.c_int * 4)(1, 2, 3, 4)
+    assert L.tge_qwen2_kv_remember_prefix(None, 0, toks, 4) == tk.ERR_INVALID
+    assert L.tge_qwen2_kv_shared_prefix_len(None, toks, 4) == tk.ERR_INVALID
+    assert L.tge_qwen2_kv_attach_prefix(None, 0, toks, 4) == tk.ERR_INVALID
+    assert L.tge_kv_copy_page(None, 0, 1, None) == tk.ERR_INVALID
