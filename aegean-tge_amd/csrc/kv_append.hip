@@ -5,49 +5,28 @@
 // store_kv_q8/quantize_kv_block, qwen2.cpp:88-120). Four lanes own one
 // 32-value block of one K or V row of one KV head: they read its 128 input
 // bytes, convert or quantize them with the reference's bit recipe, and
-// write them straight into the page block at the token's slot. This TU is
-// built with -ffp-contract=off in addition to the explicit _rn intrinsics.
+// write them straight into the page block at the token's slot. A second
+// entry fuses the step before the store (bias add and NeoX RoPE of q and k).
+// This TU is built with -ffp-contract=off in addition to the explicit _rn
+// intrinsics.
 #include "tge_common.h"
 #include "tge_kernels.h"
 
 namespace tge {
 namespace {
 
-// Append: four lanes per (row, K|V, kv head, 32-value block), each owning 8
-// consecutive values (two 16-byte loads). f16: each lane converts its 8
-// values with the reference's float_to_half recipe. int8: the four lanes
-// combine their absmax runs in order (see FoldRun), then each computes the
-// block's scale and inverse exactly as quantize_kv_block does (correctly
-// rounded fp32 division) and quantizes its 8 values.
+// Store one lane's 8 values of a 32-value block (dims 32b + 8*quarter ..)
+// of K (which = 0) or V row `rr` of KV head h. f16: each lane converts its 8
+// values with the reference's float_to_half recipe. int8: the four lanes of
+// the block (adjacent, aligned to 4 in the wave) combine their absmax runs
+// in order (see FoldRun), then each computes the block's scale and inverse
+// exactly as quantize_kv_block does (correctly rounded fp32 division) and
+// quantizes its 8 values. Dead lanes (`live` false) take part in the
+// shuffles and store nothing.
 template <int FMT>
-__global__ __launch_bounds__(256) void kv_append_kernel(AppendParams p) {
+__device__ __forceinline__ void store_lane(const AppendParams& p, const float (&x)[8], const RowRec rr,
+                                           int which, int h, int b, int quarter, bool live) {
   const int nb = p.head_dim >> 5;
-  const long total = (long)p.n_rows * 2 * p.kv_heads * nb * 4;
-  const long idx = (long)blockIdx.x * blockDim.x + threadIdx.x;
-  const bool live = idx < total;  // dead lanes still take part in the shuffles
-  const long id = live ? idx : total - 1;
-  // id -> (row, which, head, block, quarter), quarter fastest so the four
-  // lanes of a block are adjacent and neighbouring blocks read neighbouring
-  // 128-byte slices of the same input row.
-  const int quarter = (int)(id & 3);
-  long rest = id >> 2;
-  const int b = (int)(rest % nb);
-  rest /= nb;
-  const int h = (int)(rest % p.kv_heads);
-  rest /= p.kv_heads;
-  const int which = (int)(rest & 1);
-  const int row = (int)(rest >> 1);
-
-  const RowRec rr = p.rows[row];
-  const int kv_dim = p.kv_heads * p.head_dim;
-  const float* src = (which ? p.v : p.k) + (size_t)row * kv_dim + h * p.head_dim + b * 32 + quarter * 8;
-  float x[8];
-  {
-    const float4 f0 = reinterpret_cast<const float4*>(src)[0];
-    const float4 f1 = reinterpret_cast<const float4*>(src)[1];
-    x[0] = f0.x; x[1] = f0.y; x[2] = f0.z; x[3] = f0.w;
-    x[4] = f1.x; x[5] = f1.y; x[6] = f1.z; x[7] = f1.w;
-  }
   char* const blk = static_cast<char*>(p.pool) + ((size_t)rr.page * p.kv_heads + h) * p.geom.block_bytes;
   const int t = rr.slot;
   const int d0 = 32 * b + 8 * quarter;  // first dim of this lane
@@ -113,6 +92,157 @@ __global__ __launch_bounds__(256) void kv_append_kernel(AppendParams p) {
   }
 }
 
+__device__ __forceinline__ void load8(float (&x)[8], const float* src) {
+  const float4 f0 = reinterpret_cast<const float4*>(src)[0];
+  const float4 f1 = reinterpret_cast<const float4*>(src)[1];
+  x[0] = f0.x; x[1] = f0.y; x[2] = f0.z; x[3] = f0.w;
+  x[4] = f1.x; x[5] = f1.y; x[6] = f1.z; x[7] = f1.w;
+}
+
+// Append: four lanes per (row, K|V, kv head, 32-value block), each owning 8
+// consecutive values (two 16-byte loads).
+template <int FMT>
+__global__ __launch_bounds__(256) void kv_append_kernel(AppendParams p) {
+  const int nb = p.head_dim >> 5;
+  const long total = (long)p.n_rows * 2 * p.kv_heads * nb * 4;
+  const long idx = (long)blockIdx.x * blockDim.x + threadIdx.x;
+  const bool live = idx < total;  // dead lanes still take part in the shuffles
+  const long id = live ? idx : total - 1;
+  // id -> (row, which, head, block, quarter), quarter fastest so the four
+  // lanes of a block are adjacent and neighbouring blocks read neighbouring
+  // 128-byte slices of the same input row.
+  const int quarter = (int)(id & 3);
+  long rest = id >> 2;
+  const int b = (int)(rest % nb);
+  rest /= nb;
+  const int h = (int)(rest % p.kv_heads);
+  rest /= p.kv_heads;
+  const int which = (int)(rest & 1);
+  const int row = (int)(rest >> 1);
+
+  const int kv_dim = p.kv_heads * p.head_dim;
+  float x[8];
+  load8(x, (which ? p.v : p.k) + (size_t)row * kv_dim + h * p.head_dim + b * 32 + quarter * 8);
+  store_lane<FMT>(p, x, p.rows[row], which, h, b, quarter, live);
+}
+
+// NeoX rotation of one (low, high) pair by (c, s), in the rounding of
+// apply_rope_avx2 (attention's default CPU path: l*c - (h*s) and
+// l*s + (h*c) with one rounding each, norm_rope_avx2.cpp:97-131) or of
+// apply_rope_scalar (every product and the sum rounded,
+// norm_rope_scalar.cpp:23-40).
+__device__ __forceinline__ void rope_pair(float l, float h, float c, float s, bool fma, float& lo,
+                                          float& hi) {
+  if (fma) {
+    lo = __fmaf_rn(l, c, -__fmul_rn(h, s));
+    hi = __fmaf_rn(l, s, __fmul_rn(h, c));
+  } else {
+    lo = __fsub_rn(__fmul_rn(l, c), __fmul_rn(h, s));
+    hi = __fadd_rn(__fmul_rn(l, s), __fmul_rn(h, c));
+  }
+}
+
+// Bias + RoPE + append in one launch: the reference's per-token sequence
+// q += q_bias, k += k_bias, v += v_bias, apply_rope(q), apply_rope(k), store
+// (qwen2.cpp:2062-2093, 1665-1702, 2286-2329). Per row, the lanes are
+// [K lanes | V lanes | Q lanes]:
+//   - K/V: four lanes per (K|V, kv head, 32-value block), as in the plain
+//     append; a K lane also reads the 8 partner values half a head away
+//     (NeoX halves) and rotates its own 8;
+//   - Q: one lane per (q head, 8 low dims): it rotates those 8 and their 8
+//     high partners together and writes both, so q_out may alias q.
+template <int FMT>
+__global__ __launch_bounds__(256) void kv_append_rope_kernel(AppendParams p) {
+  const int D = p.head_dim, half = D >> 1, nb = D >> 5;
+  const int kv_lanes = 2 * p.kv_heads * nb * 4;
+  const int q_lanes = p.q ? p.q_heads * (half >> 3) : 0;
+  const int per_row = kv_lanes + q_lanes;  // a multiple of 4: blocks stay aligned
+  const long total = (long)p.n_rows * per_row;
+  const long idx = (long)blockIdx.x * blockDim.x + threadIdx.x;
+  const bool live = idx < total;
+  const long id = live ? idx : total - 1;
+  const int row = (int)(id / per_row);
+  const int r = (int)(id % per_row);
+  const RowRec rr = p.rows[row];
+  const float* cs = p.rope_cos + (size_t)rr.pos * half;
+  const float* sn = p.rope_sin + (size_t)rr.pos * half;
+  const bool fma = p.rope_fma != 0;
+
+  if (r >= kv_lanes) {  // Q lane (whole quads of lanes: no block shares a quad with it)
+    if (!live) return;
+    const int qi = r - kv_lanes;
+    const int hq = qi / (half >> 3);
+    const int j = 8 * (qi % (half >> 3));
+    const size_t o = (size_t)row * p.q_heads * D + (size_t)hq * D;
+    float lo[8], hi[8];
+    load8(lo, p.q + o + j);
+    load8(hi, p.q + o + half + j);
+    if (p.q_bias) {
+      float bl[8], bh[8];
+      load8(bl, p.q_bias + hq * D + j);
+      load8(bh, p.q_bias + hq * D + half + j);
+#pragma unroll
+      for (int i = 0; i < 8; ++i) {
+        lo[i] = __fadd_rn(lo[i], bl[i]);
+        hi[i] = __fadd_rn(hi[i], bh[i]);
+      }
+    }
+    float c[8], s[8], ol[8], oh[8];
+    load8(c, cs + j);
+    load8(s, sn + j);
+#pragma unroll
+    for (int i = 0; i < 8; ++i) rope_pair(lo[i], hi[i], c[i], s[i], fma, ol[i], oh[i]);
+    float* dst = p.q_out + o;
+    reinterpret_cast<float4*>(dst + j)[0] = make_float4(ol[0], ol[1], ol[2], ol[3]);
+    reinterpret_cast<float4*>(dst + j)[1] = make_float4(ol[4], ol[5], ol[6], ol[7]);
+    reinterpret_cast<float4*>(dst + half + j)[0] = make_float4(oh[0], oh[1], oh[2], oh[3]);
+    reinterpret_cast<float4*>(dst + half + j)[1] = make_float4(oh[4], oh[5], oh[6], oh[7]);
+    return;
+  }
+  const int quarter = r & 3;
+  int rest = r >> 2;
+  const int b = rest % nb;
+  rest /= nb;
+  const int h = rest % p.kv_heads;
+  const int which = rest / p.kv_heads;
+  const int kv_dim = p.kv_heads * D;
+  const int d0 = 32 * b + 8 * quarter;
+  const float* src = (which ? p.v : p.k) + (size_t)row * kv_dim + h * D;
+  const float* bias = which ? p.v_bias : p.k_bias;
+  float x[8];
+  load8(x, src + d0);
+  if (bias) {
+    float bx[8];
+    load8(bx, bias + h * D + d0);
+#pragma unroll
+    for (int i = 0; i < 8; ++i) x[i] = __fadd_rn(x[i], bx[i]);
+  }
+  if (which == 0) {
+    // the partner half: dims d0 +- half (a 32-value block lies in one half)
+    const bool low = d0 < half;
+    const int dp = low ? d0 + half : d0 - half;
+    float y[8];
+    load8(y, src + dp);
+    if (bias) {
+      float by[8];
+      load8(by, bias + h * D + dp);
+#pragma unroll
+      for (int i = 0; i < 8; ++i) y[i] = __fadd_rn(y[i], by[i]);
+    }
+    const int j = low ? d0 : dp;  // table index of the pair
+    float c[8], s[8];
+    load8(c, cs + j);
+    load8(s, sn + j);
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      float ol, oh;
+      rope_pair(low ? x[i] : y[i], low ? y[i] : x[i], c[i], s[i], fma, ol, oh);
+      x[i] = low ? ol : oh;
+    }
+  }
+  store_lane<FMT>(p, x, rr, which, h, b, quarter, live);
+}
+
 // One thread per (position, kv head, element) of the gathered rows.
 template <typename T>
 __global__ __launch_bounds__(256) void kv_gather_kernel(GatherParams p) {
@@ -153,6 +283,20 @@ hipError_t launch_kv_append(int format, const AppendParams& p, hipStream_t strea
     hipLaunchKernelGGL(kv_append_kernel<kF16>, grid, block, 0, stream, p);
   } else {
     hipLaunchKernelGGL(kv_append_kernel<kI8>, grid, block, 0, stream, p);
+  }
+  return hipGetLastError();
+}
+
+hipError_t launch_kv_append_rope(int format, const AppendParams& p, hipStream_t stream) {
+  const int nb = p.head_dim >> 5;
+  const long per_row = 2L * p.kv_heads * nb * 4 + (p.q ? (long)p.q_heads * (p.head_dim >> 4) : 0);
+  const long total = (long)p.n_rows * per_row;
+  if (total == 0) return hipSuccess;
+  const dim3 grid((unsigned)((total + 255) / 256)), block(256);
+  if (format == kF16) {
+    hipLaunchKernelGGL(kv_append_rope_kernel<kF16>, grid, block, 0, stream, p);
+  } else {
+    hipLaunchKernelGGL(kv_append_rope_kernel<kI8>, grid, block, 0, stream, p);
   }
   return hipGetLastError();
 }

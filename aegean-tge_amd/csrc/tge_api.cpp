@@ -624,7 +624,7 @@ int tge_batch_plan(tge_batch* b, const tge_kv_pool* pool, const tge_batch_desc* 
     b->sessions[s] = tge::SessionRec{ctx, nn, q_row, lo};
     for (int j = 0; j < nn; ++j) {
       const int pos = ctx + j;
-      b->rows.push_back(tge::RowRec{d->page_ids[lo + pos / 16], pos % 16});
+      b->rows.push_back(tge::RowRec{d->page_ids[lo + pos / 16], pos % 16, pos});
     }
     q_row += nn;
   }
@@ -805,6 +805,65 @@ int tge_kv_append(const tge_batch* b, tge_kv_pool* p, int layer, const float* k,
   a.head_dim = b->head_dim;
   a.scale_f32 = p->desc.scale_format == TGE_SCALE_F32;
   TGE_HIP(tge::launch_kv_append(p->desc.format, a, static_cast<hipStream_t>(stream)));
+  return TGE_OK;
+}
+
+int tge_kv_append_rope(const tge_batch* b, tge_kv_pool* p, int layer,
+                       const tge_rope_append_args* r, void* stream) {
+  int s = check_use(b, p, layer, "kv_append_rope");
+  if (s != TGE_OK) return s;
+  if (!r || !r->k || !r->v || !r->rope_cos || !r->rope_sin)
+    return fail(TGE_ERR_INVALID, "kv_append_rope: null k/v/tables");
+  if (r->q && !r->q_out) return fail(TGE_ERR_INVALID, "kv_append_rope: q without q_out");
+  int max_pos = -1;
+  for (const auto& row : b->rows) max_pos = std::max(max_pos, row.pos);
+  if (max_pos >= r->rope_positions)
+    return fail(TGE_ERR_INVALID, "kv_append_rope: a position is past the rotary tables");
+  tge_kv_layer_view view{};
+  tge_kv_pool_layer(p, layer, &view);
+  tge::AppendParams a{};
+  a.k = r->k;
+  a.v = r->v;
+  a.pool = view.k;
+  a.geom = p->geom;
+  a.rows = reinterpret_cast<const tge::RowRec*>(b->dev + b->off_rows);
+  a.n_rows = (int)b->rows.size();
+  a.kv_heads = b->kv_heads;
+  a.head_dim = b->head_dim;
+  a.scale_f32 = p->desc.scale_format == TGE_SCALE_F32;
+  a.q = r->q;
+  a.q_out = r->q_out;
+  a.q_bias = r->q_bias;
+  a.k_bias = r->k_bias;
+  a.v_bias = r->v_bias;
+  a.rope_cos = r->rope_cos;
+  a.rope_sin = r->rope_sin;
+  a.q_heads = b->q_heads;
+  a.rope_fma = r->rope_fma ? 1 : 0;
+  TGE_HIP(tge::launch_kv_append_rope(p->desc.format, a, static_cast<hipStream_t>(stream)));
+  return TGE_OK;
+}
+
+int tge_rope_tables(int head_dim, int positions, float theta, float attn_factor,
+                    const float* factors, float* cos_out, float* sin_out) {
+  if (head_dim <= 0 || (head_dim & 1) || positions < 0 || !cos_out || !sin_out)
+    return fail(TGE_ERR_INVALID, "rope_tables: bad arguments");
+  const int half = head_dim / 2;
+  std::vector<float> freq((size_t)half);
+  for (int i = 0; i < half; ++i) {
+    freq[(size_t)i] = std::pow(theta, -2.0f * (float)i / (float)head_dim);
+    if (factors) {
+      if (!(factors[i] > 0.0f)) return fail(TGE_ERR_INVALID, "rope_tables: non-positive factor");
+      freq[(size_t)i] /= factors[i];
+    }
+  }
+  for (int pos = 0; pos < positions; ++pos) {
+    for (int i = 0; i < half; ++i) {
+      const float angle = (float)pos * freq[(size_t)i];
+      cos_out[(size_t)pos * half + i] = std::cos(angle) * attn_factor;
+      sin_out[(size_t)pos * half + i] = std::sin(angle) * attn_factor;
+    }
+  }
   return TGE_OK;
 }
 

@@ -113,9 +113,10 @@ struct ReduceRec {
   int pad;
 };
 
-struct RowRec {  // one new token: destination page and slot
+struct RowRec {  // one new token: destination page and slot, logical position
   int page;
   int slot;
+  int pos;
 };
 
 // ---------------------------------------------------------------------------

@@ -18,6 +18,17 @@ struct AppendParams {
   int kv_heads;
   int head_dim;
   int scale_f32;
+  // Fused bias + RoPE (launch_kv_append_rope only): k/v above are the
+  // pre-bias, pre-RoPE rows; q (optional) is rotated into q_out.
+  const float* q;  // [n_rows][q_heads*head_dim], or null
+  float* q_out;    // may alias q
+  const float* q_bias;  // [q_heads*head_dim] or null
+  const float* k_bias;  // [kv_heads*head_dim] or null
+  const float* v_bias;
+  const float* rope_cos;  // [positions][head_dim/2]
+  const float* rope_sin;
+  int q_heads;
+  int rope_fma;  // 1: one rounding per output (FMA), 0: product, product, sum
 };
 
 struct GatherParams {
@@ -63,6 +74,7 @@ struct ReduceParams {
 };
 
 hipError_t launch_kv_append(int format, const AppendParams& p, hipStream_t stream);
+hipError_t launch_kv_append_rope(int format, const AppendParams& p, hipStream_t stream);
 hipError_t launch_kv_gather(int format, const GatherParams& p, hipStream_t stream);
 // Decode attention over a balanced plan (p.wg_first required): n_groups
 // persistent workgroups (a fixed number per CU, see DecodeCfg).

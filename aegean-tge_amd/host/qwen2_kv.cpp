@@ -221,6 +221,21 @@ void Qwen2KvPath::layer(int layer, const float* q, const float* k, const float* 
   }
 }
 
+void Qwen2KvPath::layer_rope(int layer, const tge_rope_append_args& args, float* out,
+                             void* stream) {
+  if (!begun_) throw std::runtime_error("layer: no step begun");
+  if (layer < 0 || layer >= config_.layers) {
+    throw std::invalid_argument("layer: layer out of range");
+  }
+  if (!args.q || !args.q_out) throw std::invalid_argument("layer: q and q_out are required");
+  check(tge_kv_append_rope(batch_, pool_, layer, &args, stream), "layer");
+  if (prefill_) {
+    check(tge_prefill_attention(batch_, pool_, layer, args.q_out, out, stream), "layer");
+  } else {
+    check(tge_decode_attention(batch_, pool_, layer, args.q_out, out, stream), "layer");
+  }
+}
+
 void Qwen2KvPath::store(int layer, const float* k, const float* v, void* stream) {
   if (!begun_) throw std::runtime_error("store: no step begun");
   if (layer < 0 || layer >= config_.layers) {
@@ -428,6 +443,11 @@ int tge_qwen2_kv_layer(tge_qwen2_kv* m, int layer, const float* q, const float* 
                        const float* v, float* out, void* stream) {
   if (!m) return TGE_ERR_INVALID;
   return guarded([&] { m->impl.layer(layer, q, k, v, out, stream); });
+}
+int tge_qwen2_kv_layer_rope(tge_qwen2_kv* m, int layer, const tge_rope_append_args* args,
+                            float* out, void* stream) {
+  if (!m || !args) return TGE_ERR_INVALID;
+  return guarded([&] { m->impl.layer_rope(layer, *args, out, stream); });
 }
 int tge_qwen2_kv_store(tge_qwen2_kv* m, int layer, const float* k, const float* v,
                        void* stream) {

@@ -58,6 +58,35 @@ class Qwen2Config(C.Structure):
 
 # (name, restype, argtypes) of every symbol include/tge_kv.h declares.
 _VP, _I, _PI = C.c_void_p, C.c_int, C.POINTER(C.c_int)
+class RopeAppendArgs(C.Structure):
+    _fields_ = [("q", C.c_void_p), ("q_out", C.c_void_p), ("k", C.c_void_p), ("v", C.c_void_p),
+                ("q_bias", C.c_void_p), ("k_bias", C.c_void_p), ("v_bias", C.c_void_p),
+                ("rope_cos", C.c_void_p), ("rope_sin", C.c_void_p),
+                ("rope_positions", C.c_int), ("rope_fma", C.c_int)]
+
+
+def rope_args(k, v, rope_cos, rope_sin, positions, q=None, q_out=None, q_bias=None, k_bias=None,
+              v_bias=None, fma=True):
+    """tge_rope_append_args from DeviceArrays (or raw addresses / None)."""
+    def ptr(a):
+        return None if a is None else (a if isinstance(a, int) else a.ptr)
+    return RopeAppendArgs(ptr(q), ptr(q_out), ptr(k), ptr(v), ptr(q_bias), ptr(k_bias),
+                          ptr(v_bias), ptr(rope_cos), ptr(rope_sin), int(positions), int(bool(fma)))
+
+
+def rope_tables(head_dim, positions, theta=10000.0, attn_factor=1.0, factors=None):
+    """Host rotary tables (tge_rope_tables): cos, sin as [positions][head_dim/2]."""
+    half = head_dim // 2
+    c = np.empty((positions, half), np.float32)
+    s = np.empty((positions, half), np.float32)
+    f = None if factors is None else np.ascontiguousarray(factors, dtype=np.float32)
+    check(lib().tge_rope_tables(head_dim, positions, theta, attn_factor,
+                                None if f is None else f.ctypes.data_as(C.c_void_p),
+                                c.ctypes.data_as(C.c_void_p), s.ctypes.data_as(C.c_void_p)),
+          "rope_tables")
+    return c, s
+
+
 SIGNATURES = [
     ("tge_status_string", C.c_char_p, [_I]),
     ("tge_last_error", C.c_char_p, []),
@@ -68,6 +97,9 @@ SIGNATURES = [
     ("tge_kv_pool_layer", _I, [_VP, _I, C.POINTER(LayerView)]),
     ("tge_kv_pool_bytes", C.c_size_t, [_VP]),
     ("tge_kv_copy_page", _I, [_VP, _I, _I, _VP]),
+    ("tge_kv_append_rope", _I, [_VP, _VP, _I, C.POINTER(RopeAppendArgs), _VP]),
+    ("tge_rope_tables", _I, [_I, _I, C.c_float, C.c_float, _VP, _VP, _VP]),
+    ("tge_qwen2_kv_layer_rope", _I, [_VP, _I, C.POINTER(RopeAppendArgs), _VP, _VP]),
     ("tge_kv_k_index", _I, [_I, _I, _I]),
     ("tge_kv_v_index", _I, [_I, _I, _I]),
     ("tge_kv_scale_index", _I, [_I, _I, _I]),
@@ -436,6 +468,11 @@ class Batch:
     def append(self, pool, layer, k, v, stream=None):
         check(lib().tge_kv_append(self.h, pool.h, layer, k.ptr, v.ptr, stream), "kv_append")
 
+    def append_rope(self, pool, layer, args, stream=None):
+        """tge_kv_append_rope with a RopeAppendArgs (see rope_args)."""
+        check(lib().tge_kv_append_rope(self.h, pool.h, layer, C.byref(args), stream),
+              "kv_append_rope")
+
     def decode(self, pool, layer, q, out, stream=None):
         check(lib().tge_decode_attention(self.h, pool.h, layer, q.ptr, out.ptr, stream),
               "decode_attention")
@@ -503,6 +540,10 @@ class Qwen2KvPath:
 
     def layer(self, layer, q, k, v, out):
         check(lib().tge_qwen2_kv_layer(self.h, layer, q.ptr, k.ptr, v.ptr, out.ptr, None), "layer")
+
+    def layer_rope(self, layer, args, out):
+        """layer() with bias + RoPE fused into the append; attention reads args.q_out."""
+        check(lib().tge_qwen2_kv_layer_rope(self.h, layer, C.byref(args), out.ptr, None), "layer")
 
     def store(self, layer, k, v):
         """Append-only (cache priming); k/v are DeviceArrays or raw device addresses."""

@@ -205,9 +205,33 @@ class DecodeBench:
             for layer in range(L):
                 tk.check(lib.tge_kv_append(batch, pool, layer, self.k.ptr, self.v.ptr, None))
         hip.record(e2)
+        # The fused variant of the same append: bias + NeoX RoPE of q and k
+        # before the store (tge_kv_append_rope), rotated q to its own buffer.
+        sh = self.sh
+        rng = np.random.default_rng(self.cfg.seed + 5)
+        max_pos = max(spans) + 1
+        cos_t, sin_t = tk.rope_tables(sh.head_dim, max_pos)
+        dcos, dsin = tk.DeviceArray.from_numpy(cos_t), tk.DeviceArray.from_numpy(sin_t)
+        biases = [tk.DeviceArray.from_numpy(rng.standard_normal(n).astype(np.float32))
+                  for n in (sh.q_dim, sh.kv_dim, sh.kv_dim)]
+        q_rot = tk.DeviceArray((self.rows, sh.q_dim), np.float32)
+        args = tk.rope_args(self.k, self.v, dcos, dsin, max_pos, q=self.q, q_out=q_rot,
+                            q_bias=biases[0], k_bias=biases[1], v_bias=biases[2])
+        e2r, e3 = hip.event(), hip.event()
+        hip.record(e2r)
+        for _ in range(replay):
+            for layer in range(L):
+                tk.check(lib.tge_kv_append_rope(batch, pool, layer, C.byref(args), None))
+        hip.record(e3)
         att_ms = hip.elapsed_ms(e0, e1) / (replay * L)
         app_ms = hip.elapsed_ms(e1, e2) / (replay * L)
+        rope_ms = hip.elapsed_ms(e2r, e3) / (replay * L)
         att_b, app_b = self.bytes_per_layer(spans)
+        # + q read and written, the two table rows of each token, the biases
+        rope_b = (app_b + self.rows * sh.q_dim * 8 + self.rows * sh.head_dim * 4
+                  + (sh.q_dim + 2 * sh.kv_dim) * 4)
+        for a in [dcos, dsin, q_rot] + biases:
+            a.close()
         rows, work_items, splits = tk.batch_info(batch)
         return {
             "steps": steps,
@@ -224,6 +248,9 @@ class DecodeBench:
             "append_launch_us": app_ms * 1e3,
             "append_bytes_per_launch": app_b,
             "append_gbs": app_b / (app_ms * 1e-3) / 1e9,
+            "append_rope_launch_us": rope_ms * 1e3,
+            "append_rope_bytes_per_launch": rope_b,
+            "append_rope_gbs": rope_b / (rope_ms * 1e-3) / 1e9,
             "work_items": work_items,
             "max_splits": splits,
             "pool_pages": self.pages,
@@ -580,6 +607,7 @@ def main():
             "attn_kernel_us": round(r["attn_kernel_us"], 3),
             "merge_kernel_us": round(r["merge_kernel_us"], 3),
             "append_launch_us": round(r["append_launch_us"], 3),
+            "append_rope_launch_us": round(r["append_rope_launch_us"], 3),
             "decode_work_items": r["work_items"], "max_splits": r["max_splits"],
             "pool": "fragmented" if cfg.fragmented else "fresh (LIFO reuse after churn)",
         },

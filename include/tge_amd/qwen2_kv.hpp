@@ -64,6 +64,12 @@ class Qwen2KvPath {
   void layer(int layer, const float* q, const float* k, const float* v, float* out,
              void* stream = nullptr);
 
+  // layer() with bias + RoPE fused into the append (tge_kv_append_rope):
+  // args.k/v/q are the rows before bias and RoPE; attention reads
+  // args.q_out.
+  void layer_rope(int layer, const tge_rope_append_args& args, float* out,
+                  void* stream = nullptr);
+
   // Store this step's K/V rows for `layer` without attending: the cache-
   // priming path (prime_cache_from_table, qwen2.hpp:283-288 and
   // qwen2.cpp:1973-2026, copies rows into a slot with no recompute).

@@ -231,6 +231,40 @@ int tge_kv_gather(const tge_batch* batch, const tge_kv_pool* pool, int layer,
                   void* k_scales, void* v_scales, void* stream);
 
 /* ---------------------------------------------------------------------------
+ * Fused bias + RoPE + append: the per-token sequence before the store in
+ * forward / forward_batch / prefill_run (qwen2.cpp:2062-2093, 1665-1702,
+ * 2286-2329): q += q_bias; k += k_bias; v += v_bias; apply_rope(q);
+ * apply_rope(k) (NeoX halves, qwen2.cpp:1196-1230); store k and v. One
+ * launch does it for every row of the plan; the rotated q goes to q_out
+ * (which may be q itself) for the attention call. Row i's position is its
+ * plan position (ctx + j of its session) and indexes the tables.
+ * ------------------------------------------------------------------------ */
+typedef struct {
+  const float* q;        /* [rows][q_heads*head_dim] or NULL (K/V only) */
+  float* q_out;          /* [rows][q_heads*head_dim]; may equal q */
+  const float* k;        /* [rows][kv_dim], before bias and RoPE */
+  const float* v;        /* [rows][kv_dim], before bias */
+  const float* q_bias;   /* [q_heads*head_dim] or NULL */
+  const float* k_bias;   /* [kv_dim] or NULL */
+  const float* v_bias;   /* [kv_dim] or NULL */
+  const float* rope_cos; /* device [positions][head_dim/2]: rope_cos_ of */
+  const float* rope_sin; /* qwen2.cpp:608-681 (tge_rope_tables builds them) */
+  int rope_positions;    /* rows of the tables; every plan position < this */
+  int rope_fma;          /* 1: apply_rope_avx2 rounding (the default CPU
+                            path), 0: apply_rope_scalar rounding */
+} tge_rope_append_args;
+
+int tge_kv_append_rope(const tge_batch* batch, tge_kv_pool* pool, int layer,
+                       const tge_rope_append_args* args, void* stream);
+
+/* Host: the rotary tables of qwen2.cpp:608-681 for positions [0, positions):
+ * freq_i = theta^(-2i/head_dim) / factor_i (factors NULL: all ones),
+ * angle = position * freq_i, cos/sin(angle) * attn_factor, in float with
+ * the C library's powf/cosf/sinf. Outputs are host [positions][head_dim/2]. */
+int tge_rope_tables(int head_dim, int positions, float theta, float attn_factor,
+                    const float* factors, float* cos_out, float* sin_out);
+
+/* ---------------------------------------------------------------------------
  * Block table (block_table.hpp:21-130), host-side page-id allocator.
  * allocate: LIFO free list (a fresh table hands out 0,1,2,...); release at
  * refcount 0 returns the page to the free list; misuse -> TGE_ERR_RUNTIME.
@@ -296,6 +330,12 @@ int tge_qwen2_kv_begin_verify(tge_qwen2_kv* model, int sequence,
 int tge_qwen2_kv_layer(tge_qwen2_kv* model, int layer, const float* q,
                        const float* k, const float* v, float* out,
                        void* stream);
+/* layer() with the step before the store fused: args->k/v/q are the rows
+ * before bias and RoPE (tge_kv_append_rope); attention then reads
+ * args->q_out. */
+int tge_qwen2_kv_layer_rope(tge_qwen2_kv* model, int layer,
+                            const tge_rope_append_args* args, float* out,
+                            void* stream);
 /* Store the step's K/V rows for `layer` without attending: cache priming
  * (prime_cache_from_table, qwen2.hpp:283-288). */
 int tge_qwen2_kv_store(tge_qwen2_kv* model, int layer, const float* k,

@@ -446,3 +446,57 @@ int orc_attention_block_head(int format, const float* queries,
   }
   return 0;
 }
+
+/* norm_rope_avx2.cpp:97-131 / norm_rope_scalar.cpp:23-40 */
+void orc_rope_neox(float* values, int heads, int head_dim, const float* cos_t,
+                   const float* sin_t, int fma) {
+  const int half = head_dim / 2;
+  for (int h = 0; h < heads; ++h) {
+    float* v = values + (size_t)h * head_dim;
+    for (int i = 0; i < half; ++i) {
+      const float l = v[i], hi = v[i + half], c = cos_t[i], s = sin_t[i];
+      if (fma) {
+        const float hs = hi * s, hc = hi * c;
+        v[i] = fmaf(l, c, -hs);
+        v[i + half] = fmaf(l, s, hc);
+      } else {
+        const float lc = l * c, hs = hi * s, ls = l * s, hc = hi * c;
+        v[i] = lc - hs;
+        v[i + half] = ls + hc;
+      }
+    }
+  }
+}
+
+/* qwen2.cpp:2062-2071 (forward), 1671-1680 (forward_batch),
+ * 2290-2300 (prefill_run) */
+void orc_bias_rope_row(float* q, float* k, float* v, const float* q_bias,
+                       const float* k_bias, const float* v_bias, int q_heads,
+                       int kv_heads, int head_dim, const float* cos_t,
+                       const float* sin_t, int fma) {
+  const int dim = q_heads * head_dim, kv_dim = kv_heads * head_dim;
+  if (q && q_bias)
+    for (int i = 0; i < dim; ++i) q[i] += q_bias[i];
+  for (int i = 0; i < kv_dim; ++i) {
+    if (k_bias) k[i] += k_bias[i];
+    if (v_bias) v[i] += v_bias[i];
+  }
+  if (q) orc_rope_neox(q, q_heads, head_dim, cos_t, sin_t, fma);
+  orc_rope_neox(k, kv_heads, head_dim, cos_t, sin_t, fma);
+}
+
+/* qwen2.cpp:608-681 (the YaRN factor set, when given, divides the
+ * frequencies; attn_factor scales every entry) */
+void orc_rope_tables(int head_dim, int positions, float theta, float attn_factor,
+                     const float* factors, float* cos_out, float* sin_out) {
+  const int half = head_dim / 2;
+  for (int pos = 0; pos < positions; ++pos) {
+    for (int i = 0; i < half; ++i) {
+      float f = powf(theta, -2.0f * (float)i / (float)head_dim);
+      if (factors) f /= factors[i];
+      const float angle = (float)pos * f;
+      cos_out[(size_t)pos * half + i] = cosf(angle) * attn_factor;
+      sin_out[(size_t)pos * half + i] = sinf(angle) * attn_factor;
+    }
+  }
+}

@@ -28,6 +28,15 @@
  *                            closed forms
  *   orc_attention_block_head vs orc_attention_head per query (1e-5), vs
  *                            oracle/_ref attention_block_head_avx2 (1e-4)
+ *   orc_rope_neox            vs oracle/_ref apply_rope_avx2 (fma = 1) and
+ *                            apply_rope_scalar (fma = 0), bit-exact; closed
+ *                            forms (position 0 is the identity, the two
+ *                            roundings differ only through the fused step)
+ *   orc_bias_rope_row        composition of the above with fp32 bias adds
+ *                            (the reference's loop order, checked through
+ *                            orc_rope_neox and a float64 model)
+ *   orc_rope_tables          same C library calls as the reference loader;
+ *                            within 2 ulp of float64 truth
  */
 #ifndef TGE_ORACLE_H
 #define TGE_ORACLE_H
@@ -147,6 +156,26 @@ int orc_attention_block_head(int format, const float* queries,
                              int start_position, int head_dim, int kv_stride,
                              int kv_head_offset, int query_stride, int head,
                              float scale, float* scores, float* out);
+
+/* apply_rope over `heads` vectors of head_dim (NeoX halves: element i pairs
+ * with i + head_dim/2), tables of one position (head_dim/2 entries).
+ * fma = 1: norm_rope_avx2.cpp:97-131 (l*c - (h*s), l*s + (h*c), one rounding
+ * each); fma = 0: norm_rope_scalar.cpp:23-40 (every product and sum rounded). */
+void orc_rope_neox(float* values, int heads, int head_dim, const float* cos_t,
+                   const float* sin_t, int fma);
+
+/* One token's q/k/v before the store (qwen2.cpp:2062-2071, 1671-1680):
+ * q += q_bias, k += k_bias, v += v_bias (each may be NULL), then apply_rope
+ * on q (q_heads heads) and k (kv_heads heads). In place. */
+void orc_bias_rope_row(float* q, float* k, float* v, const float* q_bias,
+                       const float* k_bias, const float* v_bias, int q_heads,
+                       int kv_heads, int head_dim, const float* cos_t,
+                       const float* sin_t, int fma);
+
+/* qwen2.cpp:608-681 rotary tables ([positions][head_dim/2]); factors NULL
+ * means all ones. */
+void orc_rope_tables(int head_dim, int positions, float theta, float attn_factor,
+                     const float* factors, float* cos_out, float* sin_out);
 
 #ifdef __cplusplus
 }

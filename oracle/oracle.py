@@ -60,6 +60,9 @@ def orc():
         L.orc_attention_gqa.argtypes = [_I, _VP, _VP, _VP, _VP, _VP, _I, _I, _I, _I, _I, _VP]
         L.orc_gqa_chunks.restype = _I
         L.orc_gqa_chunks.argtypes = [_I, _I, _I, C.POINTER(_I)]
+        L.orc_rope_neox.argtypes = [_VP, _I, _I, _VP, _VP, _I]
+        L.orc_bias_rope_row.argtypes = [_VP, _VP, _VP, _VP, _VP, _VP, _I, _I, _I, _VP, _VP, _I]
+        L.orc_rope_tables.argtypes = [_I, _I, _F, _F, _VP, _VP, _VP]
         L.orc_attention_block_head.restype = _I
         L.orc_attention_block_head.argtypes = [_I, _VP, _VP, _VP, _I, _I, _I, _I, _I, _I, _I,
                                                _F, _VP, _VP]
@@ -116,6 +119,7 @@ def ref():
         L.ref_baseline_block_prefill.argtypes = [_VP, _I, _VP, _VP, _VP, _I, _I, _I, _I, _I, _I,
                                                  _VP, _VP]
         L.ref_baseline_append_f16.argtypes = [_VP, _VP, _I, _I, _VP, _VP]
+        L.ref_apply_rope.argtypes = [_I, _VP, _I, _I, _I, _VP, _VP]
         _ref = L
     return _ref
 
@@ -135,6 +139,64 @@ def half_to_float(h):
     out = np.empty(h.shape, np.float32)
     orc().orc_half_to_float_n(_fp(h), _fp(out), h.size)
     return out
+
+
+def rope_neox(values, heads, head_dim, cos_t, sin_t, fma=True):
+    """apply_rope (NeoX halves) of every row of `values` ([rows][heads*head_dim])
+    with per-row tables cos_t/sin_t ([rows][head_dim/2]); returns a copy."""
+    v = np.ascontiguousarray(values, dtype=np.float32).copy()
+    c = np.ascontiguousarray(cos_t, dtype=np.float32)
+    s = np.ascontiguousarray(sin_t, dtype=np.float32)
+    L = orc()
+    half = head_dim // 2
+    for r in range(v.shape[0]):
+        L.orc_rope_neox(v[r].ctypes.data_as(C.c_void_p), heads, head_dim,
+                        c[r].ctypes.data_as(C.c_void_p), s[r].ctypes.data_as(C.c_void_p), int(fma))
+    assert c.shape[1] == half
+    return v
+
+
+def bias_rope_rows(q, k, v, q_bias, k_bias, v_bias, q_heads, kv_heads, head_dim, cos_t, sin_t,
+                   fma=True):
+    """The per-token sequence before the store (bias adds, then RoPE of q and
+    k) for every row; per-row tables. Returns new (q, k, v) arrays."""
+    q = None if q is None else np.ascontiguousarray(q, dtype=np.float32).copy()
+    k = np.ascontiguousarray(k, dtype=np.float32).copy()
+    v = np.ascontiguousarray(v, dtype=np.float32).copy()
+    c = np.ascontiguousarray(cos_t, dtype=np.float32)
+    s = np.ascontiguousarray(sin_t, dtype=np.float32)
+    qb, kb, vb = (None if b is None else np.ascontiguousarray(b, dtype=np.float32)
+                  for b in (q_bias, k_bias, v_bias))
+    L = orc()
+    for r in range(k.shape[0]):
+        L.orc_bias_rope_row(None if q is None else q[r].ctypes.data_as(C.c_void_p),
+                            k[r].ctypes.data_as(C.c_void_p), v[r].ctypes.data_as(C.c_void_p),
+                            _fp(qb), _fp(kb), _fp(vb), q_heads, kv_heads, head_dim,
+                            c[r].ctypes.data_as(C.c_void_p), s[r].ctypes.data_as(C.c_void_p),
+                            int(fma))
+    return q, k, v
+
+
+def rope_tables(head_dim, positions, theta=10000.0, attn_factor=1.0, factors=None):
+    half = head_dim // 2
+    c = np.empty((positions, half), np.float32)
+    s = np.empty((positions, half), np.float32)
+    f = None if factors is None else np.ascontiguousarray(factors, dtype=np.float32)
+    orc().orc_rope_tables(head_dim, positions, theta, attn_factor, _fp(f), _fp(c), _fp(s))
+    return c, s
+
+
+def ref_rope(values, heads, head_dim, cos_t, sin_t, avx2=True):
+    """The reference's own apply_rope_avx2 / apply_rope_scalar (oracle/_ref)
+    over every row; per-row tables. Returns a copy."""
+    v = np.ascontiguousarray(values, dtype=np.float32).copy()
+    c = np.ascontiguousarray(cos_t, dtype=np.float32)
+    s = np.ascontiguousarray(sin_t, dtype=np.float32)
+    R = ref()
+    for r in range(v.shape[0]):
+        R.ref_apply_rope(int(avx2), v[r].ctypes.data_as(C.c_void_p), heads, head_dim, 0,
+                         c[r].ctypes.data_as(C.c_void_p), s[r].ctypes.data_as(C.c_void_p))
+    return v
 
 
 def quantize_rows(x):

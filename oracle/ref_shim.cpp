@@ -4,7 +4,8 @@
 // baseline; never part of the product).
 //
 // Reference sources linked in: src/cpu/scalar/attention_scalar.cpp,
-// src/cpu/avx2/attention_avx2.cpp. Header-only reference code used here:
+// src/cpu/avx2/attention_avx2.cpp, src/cpu/scalar/norm_rope_scalar.cpp,
+// src/cpu/avx2/norm_rope_avx2.cpp. Header-only reference code used here:
 // include/tge/cpu/kernels.hpp (float_to_half/half_to_float, arg structs),
 // include/tge/models/block_table.hpp, include/tge/models/kv_block_layout.hpp.
 // Exceptions never cross this boundary: they become negative return codes.
@@ -270,3 +271,13 @@ int ref_gather_blocks(const float* pool, int nblocks, int block_elems,
 }
 
 }  // extern "C"
+
+// apply_rope_avx2 / apply_rope_scalar (norm_rope_*.cpp), in place.
+extern "C" void ref_apply_rope(int avx2, float* values, int heads, int head_dim, int position,
+                               const float* cos_t, const float* sin_t) {
+  if (avx2) {
+    tge::cpu::apply_rope_avx2(values, heads, head_dim, position, cos_t, sin_t);
+  } else {
+    tge::cpu::apply_rope_scalar(values, heads, head_dim, position, cos_t, sin_t);
+  }
+}

@@ -294,3 +294,41 @@ def test_prefix_sharing_and_copy_on_write(gpu):
     md.m.reset(1)
     assert md.m.shared_prefix_len(toks) == 0
     md.close()
+
+
+def test_layer_rope_flow_matches_oracle(gpu):
+    """The driver's fused layer (bias + RoPE + append, then attention on the
+    rotated q) over a prefill and a decode step equals the oracle running
+    the reference's per-token sequence on the same raw rows."""
+    say("driver layer_rope")
+    md = Model(2, 14, 2, 64, tk.KV_I8, sequences=1, pages=20, context=256, seed=8)
+    cos_t, sin_t = tk.rope_tables(64, 256)
+    dc, ds = tk.DeviceArray.from_numpy(cos_t), tk.DeviceArray.from_numpy(sin_t)
+    rng = np.random.default_rng(4)
+    biases = [[rng.standard_normal(n).astype(np.float32) for n in (14 * 64, 128, 128)]
+              for _ in range(md.layers)]
+    for start, count in ((0, 70), (70, 1)):
+        if count > 1:
+            md.m.begin_prefill(0, start, count)
+        else:
+            md.m.begin_forward(0, start)
+        q, k, v = md.rows(count)
+        pos = np.arange(start, start + count)
+        for l in range(md.layers):
+            qb, kb, vb = biases[l]
+            q_o, k_o, v_o = O.bias_rope_rows(q[l], k[l], v[l], qb, kb, vb, 14, 2, 64,
+                                             cos_t[pos], sin_t[pos], True)
+            empty = np.zeros((0, 128), np.float32)
+            md.k[(l, 0)] = np.concatenate([md.k.get((l, 0), empty)[:start], k_o])
+            md.v[(l, 0)] = np.concatenate([md.v.get((l, 0), empty)[:start], v_o])
+            a = {n: tk.DeviceArray.from_numpy(x) for n, x in
+                 (("q", q[l]), ("k", k[l]), ("v", v[l]), ("qb", qb), ("kb", kb), ("vb", vb))}
+            out = tk.DeviceArray(q[l].shape, np.float32).zero()
+            args = tk.rope_args(a["k"], a["v"], dc, ds, 256, q=a["q"], q_out=a["q"],
+                                q_bias=a["qb"], k_bias=a["kb"], v_bias=a["vb"])
+            md.m.layer_rope(l, args, out)
+            tk.hip().sync()
+            assert np.array_equal(a["q"].numpy(), q_o)
+            assert_attention_close(out.numpy(), md.oracle(l, 0, q_o, start),
+                                   f"layer_rope start {start} layer {l}")
+    md.close()

@@ -335,3 +335,89 @@ def test_prefill_i8_matches_oracle(gpu):
     got, _ = case.step(kind="prefill")
     assert_attention_close(got, case.oracle_out(), "i8 prefill")
     case.close()
+
+
+@pytest.mark.parametrize("fmt,sf,kvh,hd,fma", [
+    (tk.KV_F16, tk.SCALE_F16, 4, 128, True),
+    (tk.KV_I8, tk.SCALE_F16, 4, 128, True),
+    (tk.KV_I8, tk.SCALE_F32, 2, 64, False),
+    (tk.KV_F16, tk.SCALE_F16, 2, 64, False),
+])
+def test_append_rope_bitexact(gpu, fmt, sf, kvh, hd, fma):
+    """Fused bias + RoPE + append (tge_kv_append_rope): the pool contents and
+    the rotated q equal the oracle's per-token sequence (fp32 bias adds,
+    apply_rope of q and k, then the store; qwen2.cpp:2062-2093) bit for bit,
+    in either rounding of apply_rope; q may be rotated in place; decode over
+    the result matches the oracle within tolerance."""
+    say(f"append_rope fmt={fmt} sf={sf} kvh={kvh} hd={hd} fma={fma}")
+    qh = kvh * 7
+    case = PagedCase(qh, kvh, hd, fmt, [37, 0, 100], [3, 5, 1], scale_format=sf, seed=31,
+                     outlier_frac=0.01 if fmt == tk.KV_I8 else 0)
+    case.fill()
+    rng = np.random.default_rng(77)
+    rows = sum(case.n_new)
+    kv_dim = kvh * hd
+    pos = np.concatenate([np.arange(c, c + n) for c, n in zip(case.contexts, case.n_new)])
+    raw_q = rng.standard_normal((rows, qh * hd)).astype(np.float32)
+    raw_k = rng.standard_normal((rows, kv_dim)).astype(np.float32)
+    raw_v = rng.standard_normal((rows, kv_dim)).astype(np.float32)
+    raw_k[:, :3] *= np.float32(6)  # rotation mixes large and small halves into a block
+    qb = rng.standard_normal(qh * hd).astype(np.float32)
+    kb = rng.standard_normal(kv_dim).astype(np.float32)
+    vb = rng.standard_normal(kv_dim).astype(np.float32)
+    cos_t, sin_t = tk.rope_tables(hd, 512)
+    q_o, k_o, v_o = O.bias_rope_rows(raw_q, raw_k, raw_v, qb, kb, vb, qh, kvh, hd,
+                                     cos_t[pos], sin_t[pos], fma)
+    row = 0
+    for s, (c, n) in enumerate(zip(case.contexts, case.n_new)):
+        case.k[s][c:c + n] = k_o[row:row + n]
+        case.v[s][c:c + n] = v_o[row:row + n]
+        row += n
+    b = tk.Batch().plan(case.pool, case.sessions(True), qh)
+    d = {name: tk.DeviceArray.from_numpy(a) for name, a in
+         (("q", raw_q), ("k", raw_k), ("v", raw_v), ("qb", qb), ("kb", kb), ("vb", vb),
+          ("c", cos_t), ("s", sin_t))}
+    q_out = tk.DeviceArray(raw_q.shape, np.float32).zero()
+    args = tk.rope_args(d["k"], d["v"], d["c"], d["s"], 512, q=d["q"], q_out=q_out, q_bias=d["qb"],
+                        k_bias=d["kb"], v_bias=d["vb"], fma=fma)
+    b.append_rope(case.pool, 0, args)
+    tk.hip().sync()
+    assert np.array_equal(q_out.numpy().view(np.uint32), q_o.view(np.uint32)), "rotated q differs"
+    b.close()
+    check_contents(case)
+    # in place: q_out is q
+    b = tk.Batch().plan(case.pool, case.sessions(True), qh)
+    args = tk.rope_args(d["k"], d["v"], d["c"], d["s"], 512, q=d["q"], q_out=d["q"],
+                        q_bias=d["qb"], k_bias=d["kb"], v_bias=d["vb"], fma=fma)
+    b.append_rope(case.pool, 0, args)
+    out = tk.DeviceArray(raw_q.shape, np.float32).zero()
+    b.decode(case.pool, 0, d["q"], out)
+    tk.hip().sync()
+    assert np.array_equal(d["q"].numpy().view(np.uint32), q_o.view(np.uint32)), "in-place q differs"
+    case.q = q_o
+    assert_attention_close(out.numpy(), case.oracle_out(), "decode after append_rope")
+    b.close()
+    check_contents(case)
+    case.close()
+
+
+def test_append_rope_checks(gpu):
+    """Argument checks of the fused append: tables must cover every position
+    of the plan; q needs q_out; no bias and no q are allowed (K/V only)."""
+    case = PagedCase(14, 2, 64, tk.KV_F16, [20], [2], seed=3)
+    b = tk.Batch().plan(case.pool, case.sessions(True), 14)
+    k = tk.DeviceArray.from_numpy(np.ones((2, 128), np.float32))
+    c = tk.DeviceArray.from_numpy(np.ones((22, 32), np.float32))
+    s = tk.DeviceArray.from_numpy(np.zeros((22, 32), np.float32))
+    with pytest.raises(tk.TgeError) as e:
+        b.append_rope(case.pool, 0, tk.rope_args(k, k, c, s, 21))  # position 21 not covered
+    assert e.value.status == tk.ERR_INVALID
+    with pytest.raises(tk.TgeError) as e:
+        b.append_rope(case.pool, 0, tk.rope_args(k, k, c, s, 22, q=k))
+    assert e.value.status == tk.ERR_INVALID
+    b.append_rope(case.pool, 0, tk.rope_args(k, k, c, s, 22))
+    tk.hip().sync()
+    gk, gv, _, _ = b.gather(case.pool, 0, 0, 22)
+    assert np.array_equal(gk[20:], O.float_to_half(np.ones((2, 128), np.float32)))
+    b.close()
+    case.close()

@@ -418,3 +418,93 @@ def test_split_absmax_fold_matches_sequential():
         assert out["blocks_with_nan"] > 100000 and out["zero_max_blocks"] > 100000, out
     finally:
         shutil.rmtree(d, ignore_errors=True)
+
+
+def _rope_inputs(rows, heads, hd, seed):
+    rng = np.random.default_rng(seed)
+    x = (rng.standard_normal((rows, heads * hd)) * rng.choice([1e-3, 1, 30, 3e4], (rows, 1))
+         ).astype(np.float32)
+    x[0, :4] = [0.0, -0.0, 1e-40, -3e-41]  # signed zeros and subnormals
+    c, s = O.rope_tables(hd, 4096)
+    pos = rng.integers(0, 4096, rows)
+    return x, c[pos], s[pos]
+
+
+@pytest.mark.parametrize("hd", [64, 128])
+@pytest.mark.parametrize("fma", [True, False])
+def test_rope_matches_reference_bitexact(hd, fma):
+    """orc_rope_neox against the reference's own apply_rope_avx2 (FMA
+    rounding) and apply_rope_scalar, built from norm_rope_*.cpp."""
+    if not O.ref_available():
+        pytest.skip("oracle/_ref not built (reference tree absent)")
+    x, c, s = _rope_inputs(300, 7, hd, 21 + hd)
+    a = O.rope_neox(x, 7, hd, c, s, fma)
+    b = O.ref_rope(x, 7, hd, c, s, avx2=fma)
+    assert np.array_equal(a.view(np.uint32), b.view(np.uint32))
+    # the two roundings really differ, so a swapped recipe cannot pass
+    other = O.rope_neox(x, 7, hd, c, s, not fma)
+    assert (other.view(np.uint32) != a.view(np.uint32)).mean() > 0.05
+
+
+def test_rope_closed_forms():
+    """Position 0 (cos 1, sin 0) is the identity (a zero may change sign:
+    -0 - (h*0) is +0 when h*0 is -0); a rotation keeps each pair's norm;
+    rotating by +a then -a returns the input (float64 model bounds)."""
+    x, _, _ = _rope_inputs(64, 4, 128, 5)
+    c, s = O.rope_tables(128, 1)
+    c0, s0 = np.repeat(c, 64, 0), np.repeat(s, 64, 0)
+    for fma in (True, False):
+        y = O.rope_neox(x, 4, 128, c0, s0, fma)
+        assert np.array_equal(y, x)
+        nz = x != 0
+        assert np.array_equal(y.view(np.uint32)[nz], x.view(np.uint32)[nz])
+    rng = np.random.default_rng(9)
+    ang = rng.uniform(-3, 3, (64, 64)).astype(np.float32)
+    ca, sa = np.cos(ang).astype(np.float32), np.sin(ang).astype(np.float32)
+    y = O.rope_neox(x, 4, 128, ca, sa, True).astype(np.float64).reshape(64, 4, 2, 64)
+    x64 = x.astype(np.float64).reshape(64, 4, 2, 64)
+    n0 = np.hypot(x64[:, :, 0], x64[:, :, 1])
+    n1 = np.hypot(y[:, :, 0], y[:, :, 1])
+    assert np.all(np.abs(n1 - n0) <= 1e-5 * n0 + 1e-30)
+    back = O.rope_neox(y.reshape(64, -1).astype(np.float32), 4, 128, ca, -sa, True)
+    assert np.allclose(back, x, rtol=1e-5, atol=1e-6 * np.abs(x).max())
+
+
+def test_bias_rope_row_order():
+    """orc_bias_rope_row is: fp32 bias adds, then RoPE of q and k, v only
+    biased — composed here from numpy float32 adds and orc_rope_neox."""
+    rng = np.random.default_rng(13)
+    rows, qh, kvh, hd = 20, 14, 2, 64
+    q = rng.standard_normal((rows, qh * hd)).astype(np.float32)
+    k = rng.standard_normal((rows, kvh * hd)).astype(np.float32)
+    v = rng.standard_normal((rows, kvh * hd)).astype(np.float32)
+    qb, kb, vb = (rng.standard_normal(n).astype(np.float32) for n in (qh * hd, kvh * hd, kvh * hd))
+    c, s = O.rope_tables(hd, 100)
+    pos = rng.integers(0, 100, rows)
+    q2, k2, v2 = O.bias_rope_rows(q, k, v, qb, kb, vb, qh, kvh, hd, c[pos], s[pos])
+    assert np.array_equal(q2, O.rope_neox(q + qb, qh, hd, c[pos], s[pos], True))
+    assert np.array_equal(k2, O.rope_neox(k + kb, kvh, hd, c[pos], s[pos], True))
+    assert np.array_equal(v2, v + vb)
+
+
+def test_rope_tables_against_float64_and_product(tk):
+    """Tables within 2 ulp of float64 truth of the same float angles, the
+    YaRN factor and attn_factor terms applied, and the product's host builder
+    (tge_rope_tables) bit-identical to the oracle (same C library calls)."""
+    hd, n = 128, 2048
+    c, s = O.rope_tables(hd, n)
+    i = np.arange(hd // 2, dtype=np.float32)
+    freq = np.array([np.float32(10000.0) ** np.float32(-2.0 * j / hd) for j in i], np.float32)
+    ang = np.arange(n, dtype=np.float32)[:, None] * freq[None, :]
+    ulp = np.spacing(np.abs(np.cos(ang.astype(np.float64))).astype(np.float32))
+    assert np.all(np.abs(c - np.cos(ang.astype(np.float64))) <= 2 * ulp + 1e-12)
+    ulp = np.spacing(np.abs(np.sin(ang.astype(np.float64))).astype(np.float32))
+    assert np.all(np.abs(s - np.sin(ang.astype(np.float64))) <= 2 * ulp + 1e-12)
+    pc, ps = tk.rope_tables(hd, n)
+    assert np.array_equal(pc.view(np.uint32), c.view(np.uint32))
+    assert np.array_equal(ps.view(np.uint32), s.view(np.uint32))
+    f = np.linspace(1, 8, hd // 2).astype(np.float32)
+    c2, s2 = O.rope_tables(hd, 64, 1e6, 1.19024, f)
+    p2, q2 = tk.rope_tables(hd, 64, 1e6, 1.19024, f)
+    assert np.array_equal(p2, c2) and np.array_equal(q2, s2)
+    assert np.isclose(c2[0, 0], 1.19024) and s2[0, 5] == 0
