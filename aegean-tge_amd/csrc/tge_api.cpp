@@ -119,6 +119,10 @@ struct tge_batch {
   int max_rows = 0;  // largest n_new * group
   bool planned = false;
   AttnPlan decode, prefill;
+  // Mixed steps (tge_batch_attention): the decode kernel over the sessions
+  // whose rows fit a decode unit, the prefill kernel over the others.
+  AttnPlan mix_decode, mix_prefill;
+  bool mix_built = false;
 
   // Device image: sessions | tables | rows (one allocation), pinned staging.
   char* dev = nullptr;
@@ -418,13 +422,25 @@ Residency resident_groups(int format, int scale_f32, int head_dim, int row_group
 // cut into one equal share of pages per resident workgroup, so all
 // workgroups of the launch finish together; a segment cut into several
 // items is merged by the split reduction.
-void build_decode(tge_batch* b, Residency res) {
-  AttnPlan& pl = b->decode;
+// Sessions of a mixed step that the decode kernel takes: rows fit one unit.
+bool decode_session(const tge_batch* b, const tge::SessionRec& sr) {
+  return sr.n_new * b->group <= tge::kMaxRows;
+}
+
+// `only`: 0 every session, 1 decode sessions only, 2 the others only.
+bool take_session(const tge_batch* b, const tge::SessionRec& sr, int only) {
+  return only == 0 || (only == 1) == decode_session(b, sr);
+}
+
+void build_decode(tge_batch* b, Residency res, AttnPlan& pl, int only) {
   pl.work.clear();
   pl.reduce.clear();
   pl.wg_first.clear();
   pl.parts = pl.max_splits = 0;
-  pl.row_groups = std::max(1, std::min(4, (b->max_rows + 15) / 16));
+  int max_rows = 0;
+  for (const auto& sr : b->sessions)
+    if (take_session(b, sr, only)) max_rows = std::max(max_rows, sr.n_new * b->group);
+  pl.row_groups = std::max(1, std::min(4, (max_rows + 15) / 16));
 
   struct Seg {
     int session, head, pages;
@@ -433,6 +449,7 @@ void build_decode(tge_batch* b, Residency res) {
   long total = 0;
   for (int s = 0; s < (int)b->sessions.size(); ++s) {
     const tge::SessionRec& sr = b->sessions[s];
+    if (!take_session(b, sr, only)) continue;
     const int pages = (sr.ctx + sr.n_new + 15) / 16;
     for (int h = 0; h < b->kv_heads; ++h) segs.push_back(Seg{s, h, pages});
     total += (long)pages * b->kv_heads;
@@ -530,8 +547,7 @@ void build_decode(tge_batch* b, Residency res) {
 // head's query group, so every K/V page a tile reads serves the whole group.
 // Long spans are split so the launch has work for every CU; items are
 // ordered longest first.
-void build_prefill(tge_batch* b) {
-  AttnPlan& pl = b->prefill;
+void build_prefill(tge_batch* b, AttnPlan& pl, int only) {
   pl.work.clear();
   pl.reduce.clear();
   pl.wg_first.clear();
@@ -543,6 +559,7 @@ void build_prefill(tge_batch* b) {
   // on each of 256 CUs, at least 32 pages (eight tiles of four).
   long pages_total = 0;
   for (const auto& sr : b->sessions) {
+    if (!take_session(b, sr, only)) continue;
     for (int a = 0; a < sr.n_new; a += tq)
       pages_total += (long)((sr.ctx + std::min(sr.n_new, a + tq) + 15) / 16) * b->kv_heads;
   }
@@ -554,6 +571,7 @@ void build_prefill(tge_batch* b) {
                                       ((pages_total + target_units - 1) / target_units + 3) / 4 * 4);
   for (int s = 0; s < (int)b->sessions.size(); ++s) {
     const tge::SessionRec& sr = b->sessions[s];
+    if (!take_session(b, sr, only)) continue;
     for (int h = 0; h < b->kv_heads; ++h) {
       for (int a = 0; a < sr.n_new; a += tq) {
         tge::WorkRec w{};
@@ -636,6 +654,7 @@ int tge_batch_plan(tge_batch* b, const tge_kv_pool* pool, const tge_batch_desc* 
   b->max_rows = max_rows;
   b->prefill.built = false;
   b->decode.built = false;
+  b->mix_built = false;
 
   hipStream_t st = static_cast<hipStream_t>(stream);
   const size_t o_sess = 0;
@@ -660,7 +679,8 @@ int tge_batch_plan(tge_batch* b, const tge_kv_pool* pool, const tge_batch_desc* 
   if (max_rows <= tge::kMaxRows) {
     const int rg = std::max(1, std::min(4, (max_rows + 15) / 16));
     build_decode(b, resident_groups(pool->desc.format, pool->desc.scale_format == TGE_SCALE_F32,
-                                    hd, rg));
+                                    hd, rg),
+                 b->decode, 0);
     s = upload_plan(b->decode, hd, st);
     if (s != TGE_OK) return s;
   }
@@ -886,12 +906,47 @@ int tge_prefill_attention(const tge_batch* b, const tge_kv_pool* p, int layer,
   // steps never pay for them) and reused by every layer.
   tge_batch* mb = const_cast<tge_batch*>(b);
   if (!mb->prefill.built) {
-    build_prefill(mb);
+    build_prefill(mb, mb->prefill, 0);
     s = upload_plan(mb->prefill, b->head_dim, static_cast<hipStream_t>(stream));
     if (s != TGE_OK) return s;
   }
   return run_attention(b, p, layer, q, out, stream, b->prefill, p->desc.format == TGE_KV_I8,
                        false);
+}
+
+int tge_batch_attention(const tge_batch* b, const tge_kv_pool* p, int layer, const float* q,
+                        float* out, void* stream) {
+  int s = check_use(b, p, layer, "batch_attention");
+  if (s != TGE_OK) return s;
+  if (!q || !out) return fail(TGE_ERR_INVALID, "batch_attention: null q/out");
+  tge_batch* mb = const_cast<tge_batch*>(b);
+  int n_dec = 0, n_pf = 0;
+  for (const auto& sr : b->sessions) (decode_session(b, sr) ? n_dec : n_pf)++;
+  if (n_pf == 0) return tge_decode_attention(b, p, layer, q, out, stream);
+  if (n_dec == 0) return tge_prefill_attention(b, p, layer, q, out, stream);
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  if (!mb->mix_built) {
+    // Built on first use after each plan, reused by every layer.
+    int max_rows = 0;
+    for (const auto& sr : b->sessions)
+      if (decode_session(b, sr)) max_rows = std::max(max_rows, sr.n_new * b->group);
+    const int rg = std::max(1, std::min(4, (max_rows + 15) / 16));
+    build_decode(mb, resident_groups(p->desc.format, p->desc.scale_format == TGE_SCALE_F32,
+                                     b->head_dim, rg),
+                 mb->mix_decode, 1);
+    s = upload_plan(mb->mix_decode, b->head_dim, st);
+    if (s != TGE_OK) return s;
+    build_prefill(mb, mb->mix_prefill, 2);
+    s = upload_plan(mb->mix_prefill, b->head_dim, st);
+    if (s != TGE_OK) return s;
+    mb->mix_built = true;
+  }
+  // Long chunks first: the prefill tiles are MFMA-bound, the persistent
+  // decode workgroups HBM-bound; both write disjoint rows of `out`.
+  s = run_attention(b, p, layer, q, out, stream, b->mix_prefill, p->desc.format == TGE_KV_I8,
+                    false);
+  if (s != TGE_OK) return s;
+  return run_attention(b, p, layer, q, out, stream, b->mix_decode, true, true);
 }
 
 int tge_kv_gather(const tge_batch* b, const tge_kv_pool* p, int layer, int session,

@@ -141,7 +141,9 @@ void Qwen2KvPath::begin(const std::vector<Group>& groups, void* stream) {
   d.q_heads = config_.q_heads;
   check(tge_batch_plan(batch_, pool_, &d, stream), "begin");
   const int group = config_.q_heads / config_.kv_heads;
-  prefill_ = max_count > kSpeculativeBatch || max_count * group > 64;
+  // some session's rows exceed a decode unit: its attention runs on the
+  // block-prefill kernel (tge_batch_attention picks per session)
+  prefill_ = max_count * group > 64;
   step_rows_ = 0;
   for (int c : n_new) step_rows_ += c;
   begun_ = true;
@@ -214,11 +216,7 @@ void Qwen2KvPath::layer(int layer, const float* q, const float* k, const float* 
     throw std::invalid_argument("layer: layer out of range");
   }
   check(tge_kv_append(batch_, pool_, layer, k, v, stream), "layer");
-  if (prefill_) {
-    check(tge_prefill_attention(batch_, pool_, layer, q, out, stream), "layer");
-  } else {
-    check(tge_decode_attention(batch_, pool_, layer, q, out, stream), "layer");
-  }
+  check(tge_batch_attention(batch_, pool_, layer, q, out, stream), "layer");
 }
 
 void Qwen2KvPath::layer_rope(int layer, const tge_rope_append_args& args, float* out,
@@ -229,11 +227,7 @@ void Qwen2KvPath::layer_rope(int layer, const tge_rope_append_args& args, float*
   }
   if (!args.q || !args.q_out) throw std::invalid_argument("layer: q and q_out are required");
   check(tge_kv_append_rope(batch_, pool_, layer, &args, stream), "layer");
-  if (prefill_) {
-    check(tge_prefill_attention(batch_, pool_, layer, args.q_out, out, stream), "layer");
-  } else {
-    check(tge_decode_attention(batch_, pool_, layer, args.q_out, out, stream), "layer");
-  }
+  check(tge_batch_attention(batch_, pool_, layer, args.q_out, out, stream), "layer");
 }
 
 void Qwen2KvPath::store(int layer, const float* k, const float* v, void* stream) {

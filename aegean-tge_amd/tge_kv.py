@@ -98,6 +98,7 @@ SIGNATURES = [
     ("tge_kv_pool_bytes", C.c_size_t, [_VP]),
     ("tge_kv_copy_page", _I, [_VP, _I, _I, _VP]),
     ("tge_kv_append_rope", _I, [_VP, _VP, _I, C.POINTER(RopeAppendArgs), _VP]),
+    ("tge_batch_attention", _I, [_VP, _VP, _I, _VP, _VP, _VP]),
     ("tge_rope_tables", _I, [_I, _I, C.c_float, C.c_float, _VP, _VP, _VP]),
     ("tge_qwen2_kv_layer_rope", _I, [_VP, _I, C.POINTER(RopeAppendArgs), _VP, _VP]),
     ("tge_kv_k_index", _I, [_I, _I, _I]),
@@ -476,6 +477,11 @@ class Batch:
     def decode(self, pool, layer, q, out, stream=None):
         check(lib().tge_decode_attention(self.h, pool.h, layer, q.ptr, out.ptr, stream),
               "decode_attention")
+
+    def attention(self, pool, layer, q, out, stream=None):
+        """tge_batch_attention: decode kernel for short sessions, prefill kernel for the rest."""
+        check(lib().tge_batch_attention(self.h, pool.h, layer, q.ptr, out.ptr, stream),
+              "batch_attention")
 
     def prefill(self, pool, layer, q, out, stream=None):
         check(lib().tge_prefill_attention(self.h, pool.h, layer, q.ptr, out.ptr, stream),

@@ -64,7 +64,7 @@ def parse():
     ap.add_argument("--cpu", dest="cpu", action="store_true", default=True)
     ap.add_argument("--no-cpu", dest="cpu", action="store_false")
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
-    ap.add_argument("--only", default="", help="run one config key (c1..c5, prefix) and print it")
+    ap.add_argument("--only", default="", help="run one config key (c1..c5, prefix, mixed) and print it")
     ap.add_argument("--calibrate-copy", action="store_true",
                     help="only time 1 GiB device-to-device copies (counter calibration)")
     ap.add_argument("--fragment-c5", action="store_true",
@@ -426,6 +426,77 @@ def run_prefix(tk, synth, cfg, sessions=8, prefix=2048, private=256, reps=3):
     return res
 
 
+def run_mixed(tk, synth, cfg, decode_sessions=32, chunk=512, prompt_done=1536, reps=5):
+    """A continuous-batching step on the c5 shape (one layer's attention):
+    `decode_sessions` sessions verifying 4 draft tokens next to one session
+    prefilling a `chunk`-token chunk after `prompt_done` prompt tokens.
+    Times the mixed call (tge_batch_attention: decode kernel for the short
+    sessions, block-prefill kernel for the chunk), the same step forced
+    through the block-prefill kernel alone, and the two kinds as separate
+    steps."""
+    from types import SimpleNamespace
+    sh = cfg.shape
+    ctxs = list(cfg.contexts[:decode_sessions]) + [prompt_done]
+    n_new = [cfg.n_new] * decode_sessions + [chunk]
+    totals = [c + n for c, n in zip(ctxs, n_new)]
+    pages = sum(-(-t // 16) for t in totals) + 8
+    table = synth.fragmented_table(pages, cfg.seed + 3)
+    pool = tk.KvPool(1, pages, sh.kv_heads, sh.head_dim, cfg.fmt, tk.SCALE_F16)
+    ids = [[table.allocate() for _ in range(-(-t // 16))] for t in totals]
+    rng = np.random.default_rng(cfg.seed + 11)
+    src_rows = max(totals)
+    kf, vf = synth.make_kv(rng, src_rows, sh.kv_dim, cfg)
+    dk, dv = tk.DeviceArray.from_numpy(kf), tk.DeviceArray.from_numpy(vf)
+    for c, p in zip(ctxs, ids):  # context rows, one plan per session
+        b = tk.Batch().plan(pool, [tk.Session(0, c, p)], sh.q_heads)
+        b.append(pool, 0, dk, dv)
+        b.close()
+    rows = sum(n_new)
+    q = tk.DeviceArray.from_numpy(synth.make_q(rng, rows, sh.q_dim, cfg))
+    out = tk.DeviceArray((rows, sh.q_dim), np.float32)
+    hip = tk.hip()
+    sess = [tk.Session(c, n, p) for c, n, p in zip(ctxs, n_new, ids)]
+
+    def timed(calls):
+        for f in calls:  # warm: builds the lazily planned lists
+            f()
+        hip.sync()
+        e0, e1 = hip.event(), hip.event()
+        hip.record(e0)
+        for _ in range(reps):
+            for f in calls:
+                f()
+        hip.record(e1)
+        return hip.elapsed_ms(e0, e1) * 1e3 / reps
+
+    mixed = tk.Batch().plan(pool, sess, sh.q_heads)
+    mixed.append(pool, 0, SimpleNamespace(ptr=dk.ptr), SimpleNamespace(ptr=dv.ptr))
+    t_mixed = timed([lambda: mixed.attention(pool, 0, q, out)])
+    t_prefill_only = timed([lambda: mixed.prefill(pool, 0, q, out)])
+    dec = tk.Batch().plan(pool, sess[:-1], sh.q_heads)
+    pf = tk.Batch().plan(pool, sess[-1:], sh.q_heads)
+    q_pf = SimpleNamespace(ptr=q.ptr + decode_sessions * cfg.n_new * sh.q_dim * 4)
+    out_pf = SimpleNamespace(ptr=out.ptr + decode_sessions * cfg.n_new * sh.q_dim * 4)
+    t_split = timed([lambda: dec.decode(pool, 0, q, out), lambda: pf.prefill(pool, 0, q_pf, out_pf)])
+    for b in (mixed, dec, pf):
+        b.close()
+    att_b = synth.algorithmic_bytes_decode(sh, cfg.fmt, [c + n for c, n in zip(ctxs[:-1], n_new[:-1])],
+                                           cfg.n_new)
+    flops = synth.prefill_flops(sh, prompt_done, chunk)
+    res = {
+        "decode_sessions": decode_sessions, "queries_per_session": cfg.n_new,
+        "prefill_chunk": chunk, "prefill_after": prompt_done,
+        "decode_attn_bytes": att_b, "prefill_flops": flops,
+        "us_mixed_call": t_mixed, "us_prefill_kernel_only": t_prefill_only,
+        "us_separate_steps": t_split,
+        "tokens_per_s_mixed": rows / (t_mixed * 1e-6),
+    }
+    for a in (dk, dv, q, out):
+        a.close()
+    pool.close()
+    return res
+
+
 def cpu_baseline_c5(synth, cfg, seconds):
     """The reference's forward_batch attention schedule (per (row, head)
     attention_head_avx2, parallel over rows) with its own AVX2 kernels from
@@ -545,7 +616,8 @@ def main():
     tk.require_gpu()
     cfgs = synth.configs()
     others = {}
-    keys = [args.only] if args.only else (["c1", "c2", "c3", "c4", "prefix"] if args.others else [])
+    keys = [args.only] if args.only else (["c1", "c2", "c3", "c4", "prefix", "mixed"]
+                                          if args.others else [])
     for key in keys:
         if key == "c5":
             continue
@@ -553,6 +625,11 @@ def main():
             log("[bench] prefix: 8 sessions sharing a 2048-token prefix (c5 shape)")
             others[key] = run_prefix(tk, synth, cfgs["c5"])
             log(f"[bench] prefix: {json.dumps(others[key])}")
+            continue
+        if key == "mixed":
+            log("[bench] mixed: 32 verify sessions + one 512-token prefill chunk (c5 shape)")
+            others[key] = run_mixed(tk, synth, cfgs["c5"])
+            log(f"[bench] mixed: {json.dumps(others[key])}")
             continue
         cfg = cfgs[key]
         log(f"[bench] {key}: {cfg.note}")

@@ -59,8 +59,10 @@ class Qwen2KvPath {
   void begin_verify_draft(int sequence, int start_position, int count,
                           void* stream = nullptr);
 
-  // Store this step's K/V rows for `layer`, then attend (decode kernel for
-  // short steps, MFMA block-prefill kernel for long f16 chunks).
+  // Store this step's K/V rows for `layer`, then attend: per session, the
+  // decode kernel when its rows fit a decode unit (n_new * group <= 64),
+  // else the MFMA block-prefill kernel (tge_batch_attention), so one
+  // forward_batch step may mix decoding and prefilling sessions.
   void layer(int layer, const float* q, const float* k, const float* v, float* out,
              void* stream = nullptr);
 

@@ -213,11 +213,23 @@ int tge_decode_attention(const tge_batch* batch, const tge_kv_pool* pool,
  * attention_avx2.cpp:660-864): each new token attends causally to every
  * prior page and the chunk itself, on f16 MFMA (Q rounded to f16 for F16
  * pools; I8 pools keep Q as f16 hi + lo, the reference's per-token i8 path
- * qwen2.cpp:1535-1538 computes the same values). Tiles of 32 queries of one
- * head; long prefixes are split and merged like decode.
+ * qwen2.cpp:1535-1538 computes the same values). Tiles of up to 128
+ * (query, head) rows of one KV head's query group; long prefixes are split
+ * and merged like decode.
  */
 int tge_prefill_attention(const tge_batch* batch, const tge_kv_pool* pool,
                           int layer, const float* q, float* out, void* stream);
+
+/*
+ * Attention for a mixed step (continuous batching: forward_batch rows of
+ * many sessions, some decoding, some prefilling a chunk; qwen2.cpp:1613-1747
+ * handles any mix per token): sessions with n_new*group <= 64 go through the
+ * decode kernel, the others through the block-prefill kernel, in one call on
+ * one plan. A step of only one kind is exactly tge_decode_attention or
+ * tge_prefill_attention.
+ */
+int tge_batch_attention(const tge_batch* batch, const tge_kv_pool* pool,
+                        int layer, const float* q, float* out, void* stream);
 
 /*
  * Device gather of one session's positions [0, count) back to the flat

@@ -332,3 +332,29 @@ def test_layer_rope_flow_matches_oracle(gpu):
             assert_attention_close(out.numpy(), md.oracle(l, 0, q_o, start),
                                    f"layer_rope start {start} layer {l}")
     md.close()
+
+
+def test_forward_batch_mixing_prefill_and_decode(gpu):
+    """forward_batch rows of one sequence prefilling a 90-token chunk next
+    to two sequences decoding one token each: one plan, one layer call, the
+    decode kernel for the short sessions and the prefill kernel for the
+    chunk, against the oracle."""
+    say("driver mixed forward_batch")
+    md = Model(1, 14, 2, 64, tk.KV_F16, sequences=3, pages=60, seed=9, fragment=3)
+    for s, n in ((0, 130), (1, 40)):
+        _, k, v = md.rows(n)
+        md.m.begin_prefill(s, 0, n)
+        md.keep(s, 0, k, v)
+        md.run_layers(None, k, v, attend=False)
+    positions = [130] + [40] + list(range(0, 90))
+    seqs = [0, 1] + [2] * 90
+    q, k, v = md.rows(len(positions))
+    md.m.begin_forward_batch(positions, seqs)
+    md.keep(0, 130, [k[0][:1]], [v[0][:1]])
+    md.keep(1, 40, [k[0][1:2]], [v[0][1:2]])
+    md.keep(2, 0, [k[0][2:]], [v[0][2:]])
+    out = md.run_layers(q, k, v)[0]
+    want = np.concatenate([md.oracle(0, 0, q[0][:1], 130), md.oracle(0, 1, q[0][1:2], 40),
+                           md.oracle(0, 2, q[0][2:], 0)])
+    assert_attention_close(out, want, "mixed forward_batch")
+    md.close()

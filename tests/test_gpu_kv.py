@@ -421,3 +421,38 @@ def test_append_rope_checks(gpu):
     assert np.array_equal(gk[20:], O.float_to_half(np.ones((2, 128), np.float32)))
     b.close()
     case.close()
+
+
+@pytest.mark.parametrize("fmt", [tk.KV_F16, tk.KV_I8])
+def test_mixed_step_attention(gpu, fmt):
+    """One step mixing decoding sessions (1-4 new rows, the decode kernel)
+    and prefilling ones (long chunks, the block-prefill kernel) through
+    tge_batch_attention, against the oracle; a step of one kind runs exactly
+    the single-kind entry point (bit-identical)."""
+    say(f"mixed step fmt={fmt}")
+    case = PagedCase(28, 4, 128, fmt, [300, 0, 5000, 64, 1000], [4, 150, 1, 40, 9], seed=41,
+                     outlier_frac=0.01 if fmt == tk.KV_I8 else 0)
+    case.fill()
+    b = tk.Batch().plan(case.pool, case.sessions(True), case.qh)
+    kk = np.concatenate([k[c:] for k, c in zip(case.k, case.contexts)])
+    vv = np.concatenate([v[c:] for v, c in zip(case.v, case.contexts)])
+    dk, dv = tk.DeviceArray.from_numpy(kk), tk.DeviceArray.from_numpy(vv)
+    dq = tk.DeviceArray.from_numpy(case.q)
+    out = tk.DeviceArray(case.q.shape, np.float32).zero()
+    b.append(case.pool, 0, dk, dv)
+    b.attention(case.pool, 0, dq, out)
+    tk.hip().sync()
+    assert_attention_close(out.numpy(), case.oracle_out(), "mixed step")
+    b.close()
+    case.close()
+    # decode-only step: tge_batch_attention == tge_decode_attention, bit for bit
+    case = PagedCase(28, 4, 128, fmt, [300, 700], [4, 1], seed=42)
+    case.fill()
+    got, b = case.step()
+    dq = tk.DeviceArray.from_numpy(case.q)
+    out = tk.DeviceArray(case.q.shape, np.float32).zero()
+    b.attention(case.pool, 0, dq, out)
+    tk.hip().sync()
+    assert np.array_equal(out.numpy(), got)
+    b.close()
+    case.close()
