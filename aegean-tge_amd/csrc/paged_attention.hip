@@ -259,6 +259,49 @@ struct Unit {
   half8_t qhi[NRG][NP];
   half8_t qlo[NRG][NP];
   int lim[NRG];
+  // Static sparse subset (attention_head_static_sparse_avx2 / _fp16_avx2,
+  // attention_avx2.cpp:263-490; the kept set of build_sparse_index,
+  // qwen2.cpp:192-220): a row whose span exceeds sink + window keeps the
+  // positions below sink, every stride-th one from sink on, and the last
+  // `window`; other rows are dense. mid[rg] is where the row's window
+  // starts (sink for a dense row); sp_hi the largest mid of the unit's rows
+  // (wave-uniform). sp_stride 0: off.
+  int sp_sink, sp_stride, sp_hi;
+  int mid[NRG];
+
+  __device__ __forceinline__ void set_sparse(int sink, int window, int stride, int span_max) {
+    sp_sink = sink;
+    sp_stride = stride;
+    sp_hi = span_max > sink + window ? span_max - window : sink;
+#pragma unroll
+    for (int rg = 0; rg < NRG; ++rg) {
+      const int span = lim[rg] + 1;
+      mid[rg] = span > sink + window ? span - window : sink;
+    }
+  }
+  // Whether page pi holds a position some row may drop (wave-uniform).
+  __device__ __forceinline__ bool sparse_page(int pi) const {
+    return sp_stride > 0 && pi * 16 + 15 >= sp_sink && pi * 16 < sp_hi;
+  }
+  // Phase of the lane's first position p0 on the stride: (p0 - sink) mod
+  // stride in [0, stride), also when p0 < sink (a lane's 4 positions may
+  // straddle sink).
+  __device__ __forceinline__ int sparse_phase(int p0) const {
+    const int r = (p0 - sp_sink) % sp_stride;
+    return r < 0 ? r + sp_stride : r;
+  }
+  // Drop the lane's 4 positions p0..p0+3 of row group rg that fall between
+  // sink and the row's window off the stride; `ph` = sparse_phase(p0).
+  // ph + e < stride + 4 <= 3 * stride, so on-stride means ph + e is 0,
+  // stride or 2 * stride.
+  __device__ __forceinline__ void sparse_mask(float4_t& s, int p0, int ph, int rg) const {
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      const int p = p0 + e, x = ph + e;
+      const bool on = x == 0 || x == sp_stride || x == 2 * sp_stride;
+      if (p >= sp_sink && p < mid[rg] && !on) s[e] = -INFINITY;
+    }
+  }
   // Online softmax state per row, log2 domain. Scores are kept relative to
   // `base`; the weights exp2(s - base) never exceed 2^kLazyMax because base
   // moves (rarely) whenever a score passes base + kLazyMax. `thr` is that
@@ -369,16 +412,18 @@ struct Unit {
   }
 
   // One page with the Q^T operands held in this unit's registers.
+  template <bool SPARSE>
   __device__ __forceinline__ void consume(const Regs& r, int pi, int grp, bool masked) {
-    consume_with(r, pi, grp, masked,
-                 [&](int rg, int pp, int part) __attribute__((always_inline)) { return qop(rg, pp, part); });
+    consume_with<SPARSE>(r, pi, grp, masked,
+                         [&](int rg, int pp, int part) __attribute__((always_inline)) { return qop(rg, pp, part); });
   }
 
   // One page: scores relative to base, online softmax, value accumulation.
   // `masked` pages hold positions beyond the unit's smallest visible limit.
   // qf(rg, pp, part) yields the Q^T operand of row group rg, 32-dim block pp
   // (part 1: the f16 low part, used when QSPLIT).
-  template <class QF>
+  // SPARSE: the static sparse subset may apply (see set_sparse).
+  template <bool SPARSE, class QF>
   __device__ __forceinline__ void consume_with(const Regs& r, int pi, int grp, bool masked,
                                                const QF& qf) {
     float4_t sacc[NRG];
@@ -405,6 +450,8 @@ struct Unit {
       }
     }
 
+    const bool sp = SPARSE && sparse_page(pi);
+    const int ph = sp ? sparse_phase(pi * 16 + 4 * grp) : 0;
     half4_t pw[NRG];
 #pragma unroll
     for (int rg = 0; rg < NRG; ++rg) {
@@ -415,6 +462,7 @@ struct Unit {
           if (pi * 16 + 4 * grp + e > lim[rg]) sacc[rg][e] = -INFINITY;
         }
       }
+      if (sp) sparse_mask(sacc[rg], pi * 16 + 4 * grp, ph, rg);
       const float lmax = fmaxf(fmaxf(sacc[rg][0], sacc[rg][1]), fmaxf(sacc[rg][2], sacc[rg][3]));
       if (__builtin_expect(__any(lmax > thr[rg]), 0)) {
         // rare: some row passed its threshold; move that row's base
@@ -671,17 +719,70 @@ void paged_decode_kernel(AttnParams p) {
   // Next page to fetch: share index (-1: none), page id and KV head. The id
   // is used only at the next fetch, so its scalar load is waited for there.
   int pend_g = -1, pend_id = 0, pend_head = 0;
+  // Static sparse subsets with stride > 16 leave whole pages with nothing
+  // kept for any row of a unit; those are never fetched. The unit's kept
+  // pages are, in order: A, the pages holding a sink position; M, the pages
+  // wholly inside every row's strided middle that hold a stride position
+  // (one per stride step k: page (sink + k*stride)/16, since stride > 16);
+  // C, the pages from the first row's window start on (row 0 has the
+  // unit's smallest span). The waves split the kept ordinals round-robin
+  // (wave w takes w, w+W, ...), so a periodic skip pattern never leaves
+  // one wave all the work.
+  const bool skipping = p.sp_stride > 16;
+  int ka0 = 0, kna = 0, kk0 = 0, knm = 0, kc0 = 0, knc = 0;  // A start/count, M first k/count, C
+  auto kept_geometry = [&](const WorkRec& w) __attribute__((always_inline)) -> void {
+    const int pb = w.page_begin, pe = w.page_end;
+    const int span0 = w.ctx + w.row_begin + 1;
+    const int mid0 = span0 > p.sp_sink + p.sp_window ? span0 - p.sp_window : p.sp_sink;
+    const int ma = (p.sp_sink + 15) >> 4;    // pages below hold a sink position
+    const int mb = max(ma, mid0 >> 4);       // pages from here reach row 0's window
+    ka0 = pb;
+    kna = max(0, min(pe, ma) - pb);
+    const int lo = max(pb, ma), hi = min(pe, mb);
+    knm = 0;
+    if (hi > lo) {
+      kk0 = (16 * lo - p.sp_sink + p.sp_stride - 1) / p.sp_stride;
+      knm = (16 * hi - p.sp_sink + p.sp_stride - 1) / p.sp_stride - kk0;
+    }
+    kc0 = max(pb, mb);
+    knc = max(0, pe - kc0);
+  };
+  auto kept_page = [&](int o) __attribute__((always_inline)) -> int {  // session page of ordinal o
+    if (o < kna) return ka0 + o;
+    o -= kna;
+    if (o < knm) return (p.sp_sink + (kk0 + o) * p.sp_stride) >> 4;
+    return kc0 + (o - knm);
+  };
+  int ko = wave;  // next kept ordinal of this wave in the issue unit
+  if (skipping) kept_geometry(iw);
   auto request = [&]() __attribute__((always_inline)) -> void {
     bool ok = true;
-    while (ok && jn >= iw.page_end - iw.page_begin) {
-      if (ik + 1 >= last) {
-        ok = false;  // past the share: the cursor stays on its last unit
-      } else {
+    if (skipping) {
+      while (ko >= kna + knm + knc) {
+        if (ik + 1 >= last) {
+          ok = false;
+          break;
+        }
         ibase += iw.page_end - iw.page_begin;
         ++ik;
-        jn = wave;
         iw = iw_next;
         iw_next = load_work(work + (ik + 1 < last ? ik + 1 : ik));
+        kept_geometry(iw);
+        ko = wave;
+      }
+      jn = ok ? kept_page(ko) - iw.page_begin : 0;
+      ko += W;
+    } else {
+      while (ok && jn >= iw.page_end - iw.page_begin) {
+        if (ik + 1 >= last) {
+          ok = false;  // past the share: the cursor stays on its last unit
+        } else {
+          ibase += iw.page_end - iw.page_begin;
+          ++ik;
+          jn = wave;
+          iw = iw_next;
+          iw_next = load_work(work + (ik + 1 < last ? ik + 1 : ik));
+        }
       }
     }
     // (index 0 when past the share keeps the table read inside the unit)
@@ -690,7 +791,7 @@ void paged_decode_kernel(AttnParams p) {
     pend_g = ok ? ibase + jn : -1;
     pend_id = id;
     pend_head = iw.kv_head;
-    jn += W;
+    if (!skipping) jn += W;
   };
   // Fetch the pending page into `slot`; returns the fetched page's share
   // index, or -1 when the share is exhausted. The caller then takes the
@@ -721,6 +822,8 @@ void paged_decode_kernel(AttnParams p) {
       for (int t = 0; t < NT; ++t) u.o[rg][t] = float4_t{0, 0, 0, 0};
     }
     unmasked = (cw.ctx + cw.row_begin + 1) / 16;  // pages with no masked position
+    u.set_sparse(p.sp_sink, p.sp_window, p.sp_stride,
+                 cw.ctx + cw.row_begin + (cw.rows - 1) / cw.rows_per_query + 1);
   };
   // Merge the W waves' states of unit `cw` and write the output rows (or the
   // unit's partial). Every wave calls this once per unit, at a point where
@@ -879,7 +982,7 @@ void paged_decode_kernel(AttnParams p) {
     if (gn >= 0) request();
     const int pi = cw.page_begin + (g - cbase);
     const half8_t* qt = sh.q + (ck - qfirst) * QUNIT + lane;
-    u.consume_with(r, pi, grp, pi >= unmasked,
+    u.template consume_with<true>(r, pi, grp, pi >= unmasked,
                    [&](int rg, int pp, int) __attribute__((always_inline)) { return qt[(rg * NP + pp) * 64]; });
     head = head + 1 == NB ? 0 : head + 1;
     --count;
@@ -908,7 +1011,7 @@ struct PrefillShared {
   alignas(16) char ring[NB * TILE];
 };
 
-template <int FMT, bool SF32, int D, bool QSPLIT, int WPE>
+template <int FMT, bool SF32, int D, bool QSPLIT, int WPE, bool SP>
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(WPE, WPE)))
 void paged_prefill_kernel(AttnParams p) {
   constexpr int NRG = 2;  // 32 rows per wave
@@ -964,6 +1067,8 @@ void paged_prefill_kernel(AttnParams p) {
 #pragma unroll
     for (int t = 0; t < NT; ++t) u.o[rg][t] = float4_t{0, 0, 0, 0};
   }
+  u.set_sparse(p.sp_sink, p.sp_window, p.sp_stride,
+               w.ctx + w.row_begin + (w.rows - 1) / w.rows_per_query + 1);
   // Pages at or past `unmasked` hold a position some row of the wave may not see.
   const int unmasked = (w.ctx + w.row_begin + row0 / w.rows_per_query + 1) / 16;
 
@@ -1000,7 +1105,14 @@ void paged_prefill_kernel(AttnParams p) {
       for (int j = 0; j < kWaves; j += 2) {
         const int pg = k * kWaves + j;
         const int pi = w.page_begin + pg;
-        if (pg + 1 < npages) {
+        if (SP) {  // static sparse subsets take the pages one by one
+          for (int jj = j; jj < j + 2 && k * kWaves + jj < npages; ++jj) {
+            Regs r;
+            read_page<FMT, SF32, D>(r, tile + jj * RG::SLOT, lane, grp);
+            u.template consume<true>(r, w.page_begin + k * kWaves + jj, grp,
+                                     w.page_begin + k * kWaves + jj >= unmasked);
+          }
+        } else if (pg + 1 < npages) {
           Regs ra, rb;
           read_page<FMT, SF32, D>(ra, tile + j * RG::SLOT, lane, grp);
           read_page<FMT, SF32, D>(rb, tile + (j + 1) * RG::SLOT, lane, grp);
@@ -1009,7 +1121,7 @@ void paged_prefill_kernel(AttnParams p) {
         } else if (pg < npages) {
           Regs r;
           read_page<FMT, SF32, D>(r, tile + j * RG::SLOT, lane, grp);
-          u.consume(r, pi, grp, pi >= unmasked);
+          u.template consume<false>(r, pi, grp, pi >= unmasked);
         }
       }
     }
@@ -1216,8 +1328,13 @@ hipError_t launch_prefill_d(int n_units, const AttnParams& p, hipStream_t stream
 #else
   constexpr int wpe = waves_per_eu<FMT, D, 2, QSPLIT>();
 #endif
-  hipLaunchKernelGGL((paged_prefill_kernel<FMT, SF32, D, QSPLIT, wpe>), dim3((unsigned)n_units),
-                     dim3(256), 0, stream, p);
+  if (p.sp_stride > 0) {
+    hipLaunchKernelGGL((paged_prefill_kernel<FMT, SF32, D, QSPLIT, wpe, true>), dim3((unsigned)n_units),
+                       dim3(256), 0, stream, p);
+  } else {
+    hipLaunchKernelGGL((paged_prefill_kernel<FMT, SF32, D, QSPLIT, wpe, false>), dim3((unsigned)n_units),
+                       dim3(256), 0, stream, p);
+  }
   return hipGetLastError();
 }
 

@@ -123,6 +123,8 @@ struct tge_batch {
   // whose rows fit a decode unit, the prefill kernel over the others.
   AttnPlan mix_decode, mix_prefill;
   bool mix_built = false;
+  // Static sparse subset of every attention call (stride 0: dense).
+  int sp_sink = 0, sp_window = 0, sp_stride = 0;
 
   // Device image: sessions | tables | rows (one allocation), pinned staging.
   char* dev = nullptr;
@@ -697,6 +699,21 @@ int tge_batch_info(const tge_batch* b, int* rows, int* work_items, int* max_spli
   return TGE_OK;
 }
 
+int tge_batch_set_sparse(tge_batch* b, int enabled, int sink, int window, int stride) {
+  if (!b) return fail(TGE_ERR_INVALID, "batch_set_sparse: null batch");
+  if (!enabled) {
+    b->sp_sink = b->sp_window = b->sp_stride = 0;
+    return TGE_OK;
+  }
+  // set_sparse_config's rules (qwen2.cpp:182-189)
+  if (stride < 2) return fail(TGE_ERR_RUNTIME, "sparse: stride must be >= 2");
+  if (sink < 0 || window < 1) return fail(TGE_ERR_RUNTIME, "sparse: sink must be >= 0 and window >= 1");
+  b->sp_sink = sink;
+  b->sp_window = window;
+  b->sp_stride = stride;
+  return TGE_OK;
+}
+
 int tge_batch_set_profiling(tge_batch* b, int enable) {
   if (!b) return fail(TGE_ERR_INVALID, "batch_set_profiling: null batch");
   b->profiling = enable != 0;
@@ -749,6 +766,9 @@ tge::AttnParams attn_params(const tge_batch* b, const tge_kv_pool* p, int layer,
   a.work = reinterpret_cast<const tge::WorkRec*>(pl.dev);
   a.wg_first = pl.wg_first.empty() ? nullptr : reinterpret_cast<const int*>(pl.dev + pl.off_first);
   a.tables = reinterpret_cast<const int*>(b->dev + b->off_tables);
+  a.sp_sink = b->sp_sink;
+  a.sp_window = b->sp_window;
+  a.sp_stride = b->sp_stride;
   a.q = q;
   a.out = out;
   a.part_o = pl.part_o;

@@ -61,6 +61,10 @@ struct AttnParams {
   int kv_heads;
   int q_heads;
   float scale_log2;  // log2(e) / sqrt(head_dim)
+  // Static sparse subset (sp_stride 0: dense): rows whose span exceeds
+  // sp_sink + sp_window keep positions < sp_sink, every sp_stride-th one
+  // from sp_sink on, and the last sp_window.
+  int sp_sink, sp_window, sp_stride;
 };
 
 struct ReduceParams {

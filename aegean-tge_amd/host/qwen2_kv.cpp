@@ -238,6 +238,17 @@ void Qwen2KvPath::store(int layer, const float* k, const float* v, void* stream)
   check(tge_kv_append(batch_, pool_, layer, k, v, stream), "store");
 }
 
+void Qwen2KvPath::set_sparse_config(const SparseConfig& config) {
+  if (config.enabled && config.stride < 2) throw std::runtime_error("sparse: stride must be >= 2");
+  if (config.enabled && (config.sink < 0 || config.window < 1)) {
+    throw std::runtime_error("sparse: sink must be >= 0 and window >= 1");
+  }
+  sparse_ = config;
+  const bool on = config.enabled && config_.format == TGE_KV_F16;
+  check(tge_batch_set_sparse(batch_, on ? 1 : 0, config.sink, config.window, config.stride),
+        "set_sparse_config");
+}
+
 int Qwen2KvPath::remember_prefix(int sequence, const int* tokens, int count) {
   check_sequence(sequence, "remember_prefix");
   if (count < 0 || (count > 0 && tokens == nullptr)) {
@@ -467,6 +478,12 @@ int tge_qwen2_kv_pages(const tge_qwen2_kv* m, int sequence, int* ids, int cap) {
     for (int i = 0; i < std::min(n, cap); ++i) ids[i] = list[static_cast<std::size_t>(i)];
   });
   return s == TGE_OK ? n : s;
+}
+int tge_qwen2_kv_set_sparse(tge_qwen2_kv* m, int enabled, int sink, int window, int stride) {
+  if (!m) return TGE_ERR_INVALID;
+  return guarded([&] {
+    m->impl.set_sparse_config(tge::models::SparseConfig{enabled != 0, sink, window, stride});
+  });
 }
 int tge_qwen2_kv_remember_prefix(tge_qwen2_kv* m, int sequence, const int* tokens, int count) {
   if (!m) return TGE_ERR_INVALID;

@@ -99,6 +99,7 @@ SIGNATURES = [
     ("tge_kv_copy_page", _I, [_VP, _I, _I, _VP]),
     ("tge_kv_append_rope", _I, [_VP, _VP, _I, C.POINTER(RopeAppendArgs), _VP]),
     ("tge_batch_attention", _I, [_VP, _VP, _I, _VP, _VP, _VP]),
+    ("tge_batch_set_sparse", _I, [_VP, _I, _I, _I, _I]),
     ("tge_rope_tables", _I, [_I, _I, C.c_float, C.c_float, _VP, _VP, _VP]),
     ("tge_qwen2_kv_layer_rope", _I, [_VP, _I, C.POINTER(RopeAppendArgs), _VP, _VP]),
     ("tge_kv_k_index", _I, [_I, _I, _I]),
@@ -141,6 +142,7 @@ SIGNATURES = [
     ("tge_qwen2_kv_batch", _VP, [_VP]),
     ("tge_qwen2_kv_free_pages", _I, [_VP]),
     ("tge_qwen2_kv_table", _VP, [_VP]),
+    ("tge_qwen2_kv_set_sparse", _I, [_VP, _I, _I, _I, _I]),
     ("tge_qwen2_kv_remember_prefix", _I, [_VP, _I, _PI, _I]),
     ("tge_qwen2_kv_shared_prefix_len", _I, [_VP, _PI, _I]),
     ("tge_qwen2_kv_attach_prefix", _I, [_VP, _I, _PI, _I]),
@@ -455,6 +457,12 @@ class Batch:
     def info(self):
         return batch_info(self.h)
 
+    def set_sparse(self, sink=4, window=512, stride=4, enabled=True):
+        """Static sparse attention (tge_batch_set_sparse); enabled=False: dense."""
+        check(lib().tge_batch_set_sparse(self.h, int(bool(enabled)), sink, window, stride),
+              "batch_set_sparse")
+        return self
+
     def set_profiling(self, enable):
         check(lib().tge_batch_set_profiling(self.h, int(bool(enable))), "batch_set_profiling")
 
@@ -589,6 +597,11 @@ class Qwen2KvPath:
         if n < 0:
             check(n, what)
         return n
+
+    def set_sparse(self, sink=4, window=512, stride=4, enabled=True):
+        """set_sparse_config: static sparse attention (f16 caches; i8 stays dense)."""
+        check(lib().tge_qwen2_kv_set_sparse(self.h, int(bool(enabled)), sink, window, stride),
+              "set_sparse_config")
 
     def remember_prefix(self, sequence, tokens):
         """Keys the sequence's full cached pages among `tokens`; returns the pages keyed."""

@@ -226,6 +226,18 @@ class DecodeBench:
         att_ms = hip.elapsed_ms(e0, e1) / (replay * L)
         app_ms = hip.elapsed_ms(e1, e2) / (replay * L)
         rope_ms = hip.elapsed_ms(e2r, e3) / (replay * L)
+        # Static sparse attention (sink 4, window 512) at stride 4 (every
+        # page still read) and 32 (middle pages with nothing kept skipped).
+        sparse_us = {}
+        for stride in (4, 32):
+            tk.check(lib.tge_batch_set_sparse(batch, 1, 4, 512, stride))
+            tk.check(lib.tge_batch_set_profiling(batch, 1))
+            for layer in range(L):
+                tk.check(lib.tge_decode_attention(batch, pool, layer, self.q.ptr, self.out.ptr, None))
+            tk.check(lib.tge_batch_kernel_times(batch, C.byref(n_calls), C.byref(a_us), C.byref(mg_us)))
+            tk.check(lib.tge_batch_set_profiling(batch, 0))
+            sparse_us[f"sink4_window512_stride{stride}"] = a_us.value / n_calls.value
+        tk.check(lib.tge_batch_set_sparse(batch, 0, 0, 0, 0))
         att_b, app_b = self.bytes_per_layer(spans)
         # + q read and written, the two table rows of each token, the biases
         rope_b = (app_b + self.rows * sh.q_dim * 8 + self.rows * sh.head_dim * 4
@@ -249,6 +261,7 @@ class DecodeBench:
             "append_bytes_per_launch": app_b,
             "append_gbs": app_b / (app_ms * 1e-3) / 1e9,
             "append_rope_launch_us": rope_ms * 1e3,
+            "sparse_attn_kernel_us": sparse_us,
             "append_rope_bytes_per_launch": rope_b,
             "append_rope_gbs": rope_b / (rope_ms * 1e-3) / 1e9,
             "work_items": work_items,
@@ -685,6 +698,7 @@ def main():
             "merge_kernel_us": round(r["merge_kernel_us"], 3),
             "append_launch_us": round(r["append_launch_us"], 3),
             "append_rope_launch_us": round(r["append_rope_launch_us"], 3),
+            "sparse_attn_kernel_us": {k: round(v, 3) for k, v in r["sparse_attn_kernel_us"].items()},
             "decode_work_items": r["work_items"], "max_splits": r["max_splits"],
             "pool": "fragmented" if cfg.fragmented else "fresh (LIFO reuse after churn)",
         },

@@ -25,6 +25,14 @@
 
 namespace tge::models {
 
+// Static sparse attention (qwen2.hpp:30-35).
+struct SparseConfig {
+  bool enabled = false;
+  int sink = 4;
+  int window = 512;
+  int stride = 4;
+};
+
 struct Qwen2KvConfig {
   int layers = 0;
   int q_heads = 0;
@@ -77,6 +85,12 @@ class Qwen2KvPath {
   // qwen2.cpp:1973-2026, copies rows into a slot with no recompute).
   void store(int layer, const float* k, const float* v, void* stream = nullptr);
 
+  // set_sparse_config (qwen2.cpp:182-189): stride >= 2, sink >= 0 and
+  // window >= 1 or runtime_error. Like the reference (uses_sparse,
+  // qwen2.cpp:1313-1317) it applies to f16 caches only; i8 stays dense.
+  void set_sparse_config(const SparseConfig& config);
+  const SparseConfig& sparse_config() const { return sparse_; }
+
   // Shared prefixes over pages. Page k of a sequence is keyed by the hash of
   // its tokens [0, 16(k+1)), so one hit covers every page before it.
   // remember_prefix keys the sequence's full cached pages among the first
@@ -126,6 +140,7 @@ class Qwen2KvPath {
   int step_rows_ = 0;
   bool prefill_ = false;
   bool begun_ = false;
+  SparseConfig sparse_;
 };
 
 }  // namespace tge::models

@@ -179,6 +179,20 @@ int tge_batch_info(const tge_batch* batch, int* rows, int* work_items,
  * events to merge_us). Calls issued back to back keep the launch latency of
  * the host out of the bracketed intervals. */
 int tge_batch_set_profiling(tge_batch* batch, int enable);
+
+/* Static sparse attention for the batch's attention calls (SparseConfig,
+ * qwen2.hpp:30-35; set_sparse_config, qwen2.cpp:182-189; kernels
+ * attention_head_static_sparse_*_avx2, attention_avx2.cpp:263-490): a query
+ * whose span exceeds sink + window attends to positions < sink, every
+ * stride-th position from sink on, and the last `window` positions (the
+ * kept set of build_sparse_index, qwen2.cpp:192-220); shorter spans stay
+ * dense. enabled 0 turns it off. stride < 2, sink < 0 or window < 1 ->
+ * TGE_ERR_RUNTIME (the reference's runtime_error). With stride > 16 the
+ * decode kernel skips pages holding no kept position. The reference applies
+ * it to f32/f16 caches only (uses_sparse, qwen2.cpp:1313-1317); here any
+ * pool format. Persists across plans. */
+int tge_batch_set_sparse(tge_batch* batch, int enabled, int sink, int window,
+                         int stride);
 int tge_batch_kernel_times(const tge_batch* batch, int* calls, float* attention_us,
                            float* merge_us);
 
@@ -361,6 +375,12 @@ int tge_qwen2_kv_pages(const tge_qwen2_kv* model, int sequence, int* ids,
 const tge_kv_pool* tge_qwen2_kv_pool(const tge_qwen2_kv* model);
 const tge_batch* tge_qwen2_kv_batch(const tge_qwen2_kv* model);
 int tge_qwen2_kv_free_pages(const tge_qwen2_kv* model);
+/* set_sparse_config (qwen2.cpp:182-189): static sparse attention for every
+ * later step, applied to F16 caches only as in the reference (i8 stays
+ * dense, uses_sparse qwen2.cpp:1313-1317). See tge_batch_set_sparse. */
+int tge_qwen2_kv_set_sparse(tge_qwen2_kv* model, int enabled, int sink,
+                            int window, int stride);
+
 /* Shared prefixes over pages (the BlockTable recipe of prefix sharing,
  * replacing the reference's four-slot snapshot table, qwen2.cpp:40-72).
  * A full page of a sequence is keyed by the hash of every token up to its

@@ -500,3 +500,67 @@ void orc_rope_tables(int head_dim, int positions, float theta, float attn_factor
     }
   }
 }
+
+/* build_sparse_index (qwen2.cpp:192-220): ascending kept positions of a
+ * span; dense (0..span-1) when the span fits sink + window. Returns the
+ * count; `kept` holds at least span entries. */
+int orc_sparse_index(int span, int sink, int window, int stride, int* kept) {
+  int n = 0;
+  if (span <= 0) return 0;
+  if (span <= sink + window) {
+    for (int p = 0; p < span; ++p) kept[n++] = p;
+    return n;
+  }
+  if (stride < 2) stride = 2;
+  const int sink_end = sink < span ? sink : span;
+  for (int p = 0; p < sink_end; ++p) kept[n++] = p;
+  const int window_start = span - window;
+  for (int p = sink_end; p < window_start; p += stride) kept[n++] = p;
+  for (int p = window_start > sink_end ? window_start : sink_end; p < span; ++p) kept[n++] = p;
+  return n;
+}
+
+/* attention_head over the kept positions only: the static sparse kernels
+ * (attention_head_static_sparse_avx2 / _fp16_avx2, attention_avx2.cpp:263-490)
+ * restated with attention_head_scalar's arithmetic (std::exp, in-order
+ * sums); the kept set as above. */
+int orc_attention_head_sparse(int format, const float* query, const void* keys,
+                              const void* values, const float* k_scales,
+                              const float* v_scales, int kv_stride, int span,
+                              int head_dim, float scale, int sink, int window,
+                              int stride, float* scores, float* out) {
+  if (check_head_args(format, query, keys, values, k_scales, v_scales,
+                      kv_stride, span, head_dim, scores, out))
+    return -1;
+  int* kept = (int*)malloc(sizeof(int) * (size_t)span);
+  if (!kept) return -1;
+  const int n = orc_sparse_index(span, sink, window, stride, kept);
+  float maximum = -INFINITY;
+  for (int i = 0; i < n; ++i) {
+    float product = 0.0f;
+    for (int d = 0; d < head_dim; ++d) {
+      const float term = query[d] * load_elem(format, keys, k_scales, kv_stride, kept[i], d);
+      product += term;
+    }
+    const float scaled = product * scale;
+    scores[i] = scaled;
+    maximum = (maximum < scaled) ? scaled : maximum;
+  }
+  float total = 0.0f;
+  for (int i = 0; i < n; ++i) {
+    const float e = expf(scores[i] - maximum);
+    scores[i] = e;
+    total += e;
+  }
+  const float inverse = 1.0f / total;
+  for (int d = 0; d < head_dim; ++d) out[d] = 0.0f;
+  for (int i = 0; i < n; ++i) {
+    const float weight = scores[i] * inverse;
+    for (int d = 0; d < head_dim; ++d) {
+      const float term = weight * load_elem(format, values, v_scales, kv_stride, kept[i], d);
+      out[d] += term;
+    }
+  }
+  free(kept);
+  return 0;
+}

@@ -37,6 +37,14 @@
  *                            orc_rope_neox and a float64 model)
  *   orc_rope_tables          same C library calls as the reference loader;
  *                            within 2 ulp of float64 truth
+ *   orc_sparse_index         closed forms (dense below sink + window, sink /
+ *                            strided middle / window parts), and the kept set
+ *                            the reference kernels walk (through them)
+ *   orc_attention_head_sparse vs oracle/_ref attention_head_static_sparse_avx2
+ *                            and _fp16_avx2 (1e-5: their exp is a vectorised
+ *                            approximation); equals orc_attention_head when
+ *                            the span fits sink + window, and on a cache
+ *                            whose dropped rows were removed
  */
 #ifndef TGE_ORACLE_H
 #define TGE_ORACLE_H
@@ -171,6 +179,18 @@ void orc_bias_rope_row(float* q, float* k, float* v, const float* q_bias,
                        const float* k_bias, const float* v_bias, int q_heads,
                        int kv_heads, int head_dim, const float* cos_t,
                        const float* sin_t, int fma);
+
+/* build_sparse_index (qwen2.cpp:192-220); `kept` holds >= span entries. */
+int orc_sparse_index(int span, int sink, int window, int stride, int* kept);
+
+/* attention_head over the static sparse subset (attention_avx2.cpp:263-490)
+ * with the scalar kernel's arithmetic; f32 and f16 (the reference has no i8
+ * sparse kernel; the oracle also accepts i8 for the GPU path's extension). */
+int orc_attention_head_sparse(int format, const float* query, const void* keys,
+                              const void* values, const float* k_scales,
+                              const float* v_scales, int kv_stride, int span,
+                              int head_dim, float scale, int sink, int window,
+                              int stride, float* scores, float* out);
 
 /* qwen2.cpp:608-681 rotary tables ([positions][head_dim/2]); factors NULL
  * means all ones. */

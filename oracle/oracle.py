@@ -61,6 +61,11 @@ def orc():
         L.orc_gqa_chunks.restype = _I
         L.orc_gqa_chunks.argtypes = [_I, _I, _I, C.POINTER(_I)]
         L.orc_rope_neox.argtypes = [_VP, _I, _I, _VP, _VP, _I]
+        L.orc_sparse_index.restype = _I
+        L.orc_sparse_index.argtypes = [_I, _I, _I, _I, _VP]
+        L.orc_attention_head_sparse.restype = _I
+        L.orc_attention_head_sparse.argtypes = [_I, _VP, _VP, _VP, _VP, _VP, _I, _I, _I, _F, _I, _I,
+                                                _I, _VP, _VP]
         L.orc_bias_rope_row.argtypes = [_VP, _VP, _VP, _VP, _VP, _VP, _I, _I, _I, _VP, _VP, _I]
         L.orc_rope_tables.argtypes = [_I, _I, _F, _F, _VP, _VP, _VP]
         L.orc_attention_block_head.restype = _I
@@ -120,6 +125,9 @@ def ref():
                                                  _VP, _VP]
         L.ref_baseline_append_f16.argtypes = [_VP, _VP, _I, _I, _VP, _VP]
         L.ref_apply_rope.argtypes = [_I, _VP, _I, _I, _I, _VP, _VP]
+        L.ref_attention_head_sparse.restype = _I
+        L.ref_attention_head_sparse.argtypes = [_I, _VP, _VP, _VP, _I, _I, _I, _F, _I, _I, _I, _VP,
+                                                _VP]
         _ref = L
     return _ref
 
@@ -221,6 +229,37 @@ def attention_head(fmt, q, keys, values, k_scales, v_scales, kv_stride, span, he
     return out
 
 
+def attention_head_sparse(fmt, q, keys, values, k_scales, v_scales, kv_stride, span, head_dim,
+                          scale, sink, window, stride):
+    scores = np.empty(span, np.float32)
+    out = np.empty(head_dim, np.float32)
+    rc = orc().orc_attention_head_sparse(fmt, _fp(q), _fp(keys), _fp(values), _fp(k_scales),
+                                         _fp(v_scales), kv_stride, span, head_dim,
+                                         C.c_float(scale), sink, window, stride, _fp(scores),
+                                         _fp(out))
+    if rc != 0:
+        raise ValueError("orc_attention_head_sparse rejected its arguments")
+    return out
+
+
+def sparse_index(span, sink, window, stride):
+    kept = np.empty(max(span, 1), np.int32)
+    n = orc().orc_sparse_index(span, sink, window, stride, _fp(kept))
+    return kept[:n]
+
+
+def ref_attention_head_sparse(fmt, q, keys, values, kv_stride, span, head_dim, scale, sink,
+                              window, stride):
+    scores = np.empty(span, np.float32)
+    out = np.empty(head_dim, np.float32)
+    rc = ref().ref_attention_head_sparse(fmt, _fp(q), _fp(keys), _fp(values), kv_stride, span,
+                                         head_dim, C.c_float(scale), sink, window, stride,
+                                         _fp(scores), _fp(out))
+    if rc != 0:
+        raise ValueError("reference sparse kernel rejected its arguments")
+    return out
+
+
 class FlatCache:
     """The reference's flat KV cache for one (sequence, layer):
     rows [position][kv_dim] as f16 bits, int8 codes (+fp32 scales) or fp32."""
@@ -231,6 +270,7 @@ class FlatCache:
         v = np.ascontiguousarray(v, np.float32)
         self.rows, self.kv_dim = k.shape
         self.ks = self.vs = None
+        self.sparse = None  # (sink, window, stride): the static sparse subset
         if fmt == F16:
             self.k, self.v = float_to_half(k), float_to_half(v)
         elif fmt == I8:
@@ -238,6 +278,11 @@ class FlatCache:
             self.v, self.vs = quantize_rows(v)
         else:
             self.k, self.v = k, v
+
+    def with_sparse(self, sink, window, stride):
+        """Attend over the static sparse subset (orc_attention_head_sparse)."""
+        self.sparse = (sink, window, stride)
+        return self
 
     def with_scales(self, ks, vs):
         """Replace the fp32 scales (e.g. by f16-rounded ones)."""
@@ -263,6 +308,9 @@ class FlatCache:
             if rc != 0:
                 raise ValueError("orc_attention_head_f64 rejected its arguments")
             return out
+        if self.sparse is not None:
+            return attention_head_sparse(self.fmt, q, kb, vb, ks, vs, kv, span, head_dim,
+                                         float(np.float32(scale)), *self.sparse)
         return attention_head(self.fmt, q, kb, vb, ks, vs, kv, span, head_dim,
                               float(np.float32(scale)))
 

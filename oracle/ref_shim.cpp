@@ -281,3 +281,23 @@ extern "C" void ref_apply_rope(int avx2, float* values, int heads, int head_dim,
     tge::cpu::apply_rope_scalar(values, heads, head_dim, position, cos_t, sin_t);
   }
 }
+
+// attention_head_static_sparse_avx2 (f32) / _fp16_avx2 (f16), with the
+// stride rule of Qwen2::attention_head (stride < 2 -> 2, qwen2.cpp:1293).
+extern "C" int ref_attention_head_sparse(int format, const float* query, const void* keys,
+                                         const void* values, int kv_stride, int span,
+                                         int head_dim, float scale, int sink, int window,
+                                         int stride, float* scores, float* out) {
+  try {
+    tge::cpu::AttentionArgs a = head_args(format, query, keys, values, nullptr, nullptr,
+                                          kv_stride, span, head_dim, scale, scores, out);
+    if (format == kF16) {
+      tge::cpu::attention_head_static_sparse_fp16_avx2(a, sink, window, stride < 2 ? 2 : stride);
+    } else {
+      tge::cpu::attention_head_static_sparse_avx2(a, sink, window, stride < 2 ? 2 : stride);
+    }
+    return 0;
+  } catch (const std::exception&) {
+    return -1;
+  }
+}

@@ -79,6 +79,8 @@ class PagedCase:
         """The reference flat cache of session s (scales as the pool stores
         them: f16-rounded for SCALE_F16)."""
         fc = O.FlatCache({tk.KV_F16: O.F16, tk.KV_I8: O.I8}[self.fmt], self.k[s], self.v[s])
+        if getattr(self, "sparse", None):
+            fc.with_sparse(*self.sparse)
         if self.fmt == tk.KV_I8 and self.sf == tk.SCALE_F16:
             fc.with_scales(O.half_to_float(O.float_to_half(fc.ks)),
                            O.half_to_float(O.float_to_half(fc.vs)))

@@ -358,3 +358,32 @@ def test_forward_batch_mixing_prefill_and_decode(gpu):
                            md.oracle(0, 2, q[0][2:], 0)])
     assert_attention_close(out, want, "mixed forward_batch")
     md.close()
+
+
+def test_driver_sparse_config(gpu):
+    """set_sparse_config on the driver: f16 caches attend over the static
+    sparse subset, i8 caches stay dense (uses_sparse, qwen2.cpp:1313-1317),
+    bad strides are a runtime error (qwen2.cpp:182-189)."""
+    say("driver sparse")
+    for fmt in (tk.KV_F16, tk.KV_I8):
+        md = Model(1, 14, 2, 64, fmt, sequences=1, pages=40, context=600, seed=12)
+        _, k, v = md.rows(400)
+        md.m.begin_prefill(0, 0, 400)
+        md.keep(0, 0, k, v)
+        md.run_layers(None, k, v, attend=False)
+        md.m.set_sparse(4, 100, 7)
+        q, k, v = md.rows(2)
+        md.m.begin_verify(0, 400, 2)
+        md.keep(0, 400, k, v)
+        out = md.run_layers(q, k, v)[0]
+        fc = O.FlatCache({tk.KV_F16: O.F16, tk.KV_I8: O.I8}[fmt], md.k[(0, 0)], md.v[(0, 0)])
+        if fmt == tk.KV_I8:
+            fc.with_scales(O.half_to_float(O.float_to_half(fc.ks)),
+                           O.half_to_float(O.float_to_half(fc.vs)))
+        else:
+            fc.with_sparse(4, 100, 7)
+        assert_attention_close(out, fc.attend(q[0], 14, 2, 64, 400), f"driver sparse fmt={fmt}")
+        with pytest.raises(tk.TgeError) as e:
+            md.m.set_sparse(4, 100, 1)
+        assert e.value.status == tk.ERR_RUNTIME
+        md.close()

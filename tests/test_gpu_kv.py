@@ -456,3 +456,48 @@ def test_mixed_step_attention(gpu, fmt):
     assert np.array_equal(out.numpy(), got)
     b.close()
     case.close()
+
+
+@pytest.mark.parametrize("fmt,sparse,kind", [
+    (tk.KV_F16, (4, 64, 4), "decode"),
+    (tk.KV_F16, (4, 100, 37), "decode"),   # stride > 16: pages with nothing kept are skipped
+    (tk.KV_I8, (20, 40, 17), "decode"),    # sink straddles a page; most middle pages kept
+    (tk.KV_I8, (0, 48, 3), "decode"),
+    (tk.KV_F16, (4, 64, 5), "prefill"),
+    (tk.KV_F16, (2, 80, 24), "mixed"),
+])
+def test_static_sparse_attention(gpu, fmt, sparse, kind):
+    """Static sparse attention (sink + strided middle + window, the kept set
+    of build_sparse_index) on the decode, block-prefill and mixed paths,
+    against the oracle's sparse head (pinned against the reference's
+    attention_head_static_sparse kernels); spans on both sides of
+    sink + window, multi-query rows whose windows differ by one."""
+    say(f"sparse fmt={fmt} {sparse} {kind}")
+    contexts = {"decode": [30, 700, 3000, 150], "prefill": [300, 0],
+                "mixed": [2000, 500]}[kind]
+    n_new = {"decode": [1, 4, 2, 3], "prefill": [120, 200], "mixed": [3, 160]}[kind]
+    case = PagedCase(28, 4, 128, fmt, contexts, n_new, seed=51)
+    case.fill()
+    case.sparse = sparse
+    b = tk.Batch().plan(case.pool, case.sessions(True), case.qh).set_sparse(*sparse)
+    kk = np.concatenate([k[c:] for k, c in zip(case.k, case.contexts)])
+    vv = np.concatenate([v[c:] for v, c in zip(case.v, case.contexts)])
+    dk, dv = tk.DeviceArray.from_numpy(kk), tk.DeviceArray.from_numpy(vv)
+    dq = tk.DeviceArray.from_numpy(case.q)
+    out = tk.DeviceArray(case.q.shape, np.float32).zero()
+    b.append(case.pool, 0, dk, dv)
+    {"decode": b.decode, "prefill": b.prefill, "mixed": b.attention}[kind](case.pool, 0, dq, out)
+    tk.hip().sync()
+    assert_attention_close(out.numpy(), case.oracle_out(), f"sparse {sparse} {kind}")
+    # turning it off gives dense attention again
+    b.set_sparse(enabled=False)
+    out2 = tk.DeviceArray(case.q.shape, np.float32).zero()
+    {"decode": b.decode, "prefill": b.prefill, "mixed": b.attention}[kind](case.pool, 0, dq, out2)
+    tk.hip().sync()
+    case.sparse = None
+    assert_attention_close(out2.numpy(), case.oracle_out(), "dense again")
+    with pytest.raises(tk.TgeError) as e:
+        b.set_sparse(4, 64, 1)
+    assert e.value.status == tk.ERR_RUNTIME
+    b.close()
+    case.close()

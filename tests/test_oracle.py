@@ -508,3 +508,44 @@ def test_rope_tables_against_float64_and_product(tk):
     p2, q2 = tk.rope_tables(hd, 64, 1e6, 1.19024, f)
     assert np.array_equal(p2, c2) and np.array_equal(q2, s2)
     assert np.isclose(c2[0, 0], 1.19024) and s2[0, 5] == 0
+
+
+def test_sparse_index_closed_forms():
+    """build_sparse_index (qwen2.cpp:192-220): dense when the span fits
+    sink + window; else sink, every stride-th from sink below span - window,
+    then the window; stride < 2 acts as 2."""
+    assert list(O.sparse_index(10, 4, 8, 4)) == list(range(10))
+    k = O.sparse_index(100, 4, 8, 5)
+    assert list(k) == [0, 1, 2, 3] + list(range(4, 92, 5)) + list(range(92, 100))
+    assert list(O.sparse_index(50, 0, 10, 1)) == list(range(0, 40, 2)) + list(range(40, 50))
+    k = O.sparse_index(1000, 4, 512, 4)
+    assert k.size == 4 + (488 - 4 + 3) // 4 + 512 and np.all(np.diff(k) > 0)
+
+
+@pytest.mark.parametrize("fmt", [O.F32, O.F16])
+def test_sparse_head_against_reference_and_dense(fmt):
+    """orc_attention_head_sparse against the reference's own static sparse
+    kernels (attention_head_static_sparse_avx2 / _fp16_avx2, whose exp is a
+    vectorised approximation: 1e-5), equal to the dense oracle when the span
+    fits sink + window, and equal to the dense oracle over a cache holding
+    only the kept rows (same arithmetic on the same rows)."""
+    rng = np.random.default_rng(17)
+    hd, span = 64, 700
+    k = rng.standard_normal((span, hd)).astype(np.float32)
+    v = rng.standard_normal((span, hd)).astype(np.float32)
+    q = (rng.standard_normal(hd) * 2).astype(np.float32)
+    fc = O.FlatCache(fmt, k, v)
+    scale = float(np.float32(1.0 / np.sqrt(np.float32(hd))))
+    for sink, window, stride in ((4, 512, 4), (0, 64, 3), (7, 100, 33), (4, 512, 1)):
+        got = O.attention_head_sparse(fmt, q, fc.k, fc.v, None, None, hd, span, hd, scale, sink,
+                                      window, stride)
+        if O.ref_available():
+            want = O.ref_attention_head_sparse(fmt, q, fc.k, fc.v, hd, span, hd, scale, sink,
+                                               window, stride)
+            assert np.allclose(got, want, rtol=1e-5, atol=1e-5)
+        kept = O.sparse_index(span, sink, window, stride)
+        sub = O.attention_head(fmt, q, fc.k[kept], fc.v[kept], None, None, hd, kept.size, hd, scale)
+        assert np.array_equal(got, sub)
+    dense = O.attention_head(fmt, q, fc.k, fc.v, None, None, hd, 300, hd, scale)
+    assert np.array_equal(O.attention_head_sparse(fmt, q, fc.k, fc.v, None, None, hd, 300, hd,
+                                                  scale, 4, 296, 4), dense)
