@@ -22,7 +22,7 @@
 //
 // Per page, per 16-row group, per wave (lane = group g 0..3, column c 0..15):
 //   S^T[token][row] = K (16 x D) . Q^T: one v_mfma_f32_16x16x32_f16 per 32-dim
-//     block (prefill of int8 pools: two, with Q split into f16 hi + lo);
+//     block, Q rounded to f16 once;
 //     int8 codes are exact in f16 and the block's per-token scale multiplies
 //     the block's fp32 partial score. Lane (g, c) then holds row c,
 //     tokens 4g..4g+3.
@@ -133,7 +133,7 @@ struct Ring {
 // Waves per SIMD the block-prefill kernel is compiled for: the register
 // budget that keeps every live value in the 256 architectural VGPRs while
 // leaving room for a second wave to hide latency.
-template <int FMT, int D, int NRG, bool QSPLIT>
+template <int FMT, int D, int NRG>
 constexpr int waves_per_eu() {
   return D == 64 ? (NRG <= 2 ? 3 : 2) : (NRG <= 2 ? 2 : 1);
 }
@@ -250,14 +250,13 @@ __device__ __forceinline__ float4_t scales4(const uint32_t* s, int b) {
 #define MFMA16x16x16(a, b, c) __builtin_amdgcn_mfma_f32_16x16x16f16((a), (b), (c), 0, 0, 0)
 #define MFMA16x16x32(a, b, c) __builtin_amdgcn_mfma_f32_16x16x32_f16((a), (b), (c), 0, 0, 0)
 
-template <int FMT, bool SF32, int D, int NRG, bool QSPLIT>
+template <int FMT, bool SF32, int D, int NRG>
 struct Unit {
   static constexpr int NP = D / 32;
   static constexpr int NT = D / 16;
   using Regs = PageRegs<FMT, SF32, D>;
 
-  half8_t qhi[NRG][NP];
-  half8_t qlo[NRG][NP];
+  half8_t q[NRG][NP];  // Q^T operands (prefill; decode reads them from LDS)
   int lim[NRG];
   // Static sparse subset (attention_head_static_sparse_avx2 / _fp16_avx2,
   // attention_avx2.cpp:263-490; the kept set of build_sparse_index,
@@ -310,8 +309,8 @@ struct Unit {
   float4_t l4[NRG];  // row sums (all four entries equal), via the ones MFMA
   float4_t o[NRG][NT];
 
-  __device__ __forceinline__ half8_t qop(int rg, int pp, int part) const {
-    return part ? qlo[rg][pp] : qhi[rg][pp];
+  __device__ __forceinline__ half8_t qop(int rg, int pp) const {
+    return q[rg][pp];
   }
 
   // S^T = K.Q^T of one page for every row group (fp32, K scales applied).
@@ -325,15 +324,13 @@ struct Unit {
       if (FMT == kF16) {
 #pragma unroll
         for (int rg = 0; rg < NRG; ++rg) {
-          sacc[rg] = MFMA16x16x32(ka, qf(rg, pp, 0), sacc[rg]);
-          if (QSPLIT) sacc[rg] = MFMA16x16x32(ka, qf(rg, pp, 1), sacc[rg]);
+          sacc[rg] = MFMA16x16x32(ka, qf(rg, pp), sacc[rg]);
         }
       } else {
         const float4_t ks = scales4<SF32>(r.ks, pp);
 #pragma unroll
         for (int rg = 0; rg < NRG; ++rg) {
-          float4_t b = MFMA16x16x32(ka, qf(rg, pp, 0), (float4_t{0, 0, 0, 0}));
-          if (QSPLIT) b = MFMA16x16x32(ka, qf(rg, pp, 1), b);
+          float4_t b = MFMA16x16x32(ka, qf(rg, pp), (float4_t{0, 0, 0, 0}));
 #pragma unroll
           for (int e = 0; e < 4; ++e) sacc[rg][e] = fmaf(b[e], ks[e], sacc[rg][e]);
         }
@@ -415,13 +412,12 @@ struct Unit {
   template <bool SPARSE>
   __device__ __forceinline__ void consume(const Regs& r, int pi, int grp, bool masked) {
     consume_with<SPARSE>(r, pi, grp, masked,
-                         [&](int rg, int pp, int part) __attribute__((always_inline)) { return qop(rg, pp, part); });
+                         [&](int rg, int pp) __attribute__((always_inline)) { return qop(rg, pp); });
   }
 
   // One page: scores relative to base, online softmax, value accumulation.
   // `masked` pages hold positions beyond the unit's smallest visible limit.
-  // qf(rg, pp, part) yields the Q^T operand of row group rg, 32-dim block pp
-  // (part 1: the f16 low part, used when QSPLIT).
+  // qf(rg, pp) yields the Q^T operand of row group rg, 32-dim block pp.
   // SPARSE: the static sparse subset may apply (see set_sparse).
   template <bool SPARSE, class QF>
   __device__ __forceinline__ void consume_with(const Regs& r, int pi, int grp, bool masked,
@@ -435,15 +431,13 @@ struct Unit {
       if (FMT == kF16) {
 #pragma unroll
         for (int rg = 0; rg < NRG; ++rg) {
-          sacc[rg] = MFMA16x16x32(ka, qf(rg, pp, 0), sacc[rg]);
-          if (QSPLIT) sacc[rg] = MFMA16x16x32(ka, qf(rg, pp, 1), sacc[rg]);
+          sacc[rg] = MFMA16x16x32(ka, qf(rg, pp), sacc[rg]);
         }
       } else {
         const float4_t ks = scales4<SF32>(r.ks, pp);
 #pragma unroll
         for (int rg = 0; rg < NRG; ++rg) {
-          float4_t b = MFMA16x16x32(ka, qf(rg, pp, 0), (float4_t{0, 0, 0, 0}));
-          if (QSPLIT) b = MFMA16x16x32(ka, qf(rg, pp, 1), b);
+          float4_t b = MFMA16x16x32(ka, qf(rg, pp), (float4_t{0, 0, 0, 0}));
 #pragma unroll
           for (int e = 0; e < 4; ++e) sacc[rg][e] = fmaf(b[e], ks[e], sacc[rg][e]);
         }
@@ -517,23 +511,21 @@ struct Unit {
 };
 
 // ---------------------------------------------------------------------------
-// Decode kernel: one persistent workgroup of W waves per CU, each covering a
-// contiguous share of the plan's page sequence (its work items in order).
-//
-// The HBM rate a CU reaches grows with the number of waves issuing loads far
-// more than with the pages each wave has in flight, so the kernel runs as
-// many waves as the registers allow: the Q^T operands of the share's units
-// sit in LDS (f16, read per page), not in registers, which fits three waves
-// per SIMD (W = 12) for up to 32 rows per unit.
+// Decode kernel: persistent workgroups of W waves (DecodeCfg: 4 waves, two
+// workgroups per CU for up to 32 rows per unit), each covering a contiguous
+// share of the plan's page sequence (its work items in order).
 //
 // Within a unit the waves take pages round-robin (wave w: pages w, w+W,
-// ...). Each wave streams its pages through a private LDS ring of NB slots
-// (NB-1 page blocks in flight while it consumes one) and crosses unit
+// ...; with a static sparse subset that skips pages, the unit's kept pages
+// instead). Each wave streams its pages through a private LDS ring of NB
+// slots (NB-1 page blocks in flight while it consumes one) and crosses unit
 // boundaries without draining: the next unit's first pages are already in
-// flight while the current unit is merged. A unit ends for a wave when its
-// next page belongs to a later unit (or the share is exhausted); the W waves
-// then merge their states for that unit in wave order, so every wave passes
-// the same barriers. The page split is fixed by the plan, so results are
+// flight while the current unit is merged. The Q^T operands of the share's
+// units sit in an LDS table (f16, read per page), so no vector-memory wait
+// for Q stalls the ring. A unit ends for a wave when its next page belongs
+// to a later unit (or the share is exhausted); the W waves then merge their
+// states for that unit in wave order, so every wave passes the same
+// barriers. The page split is fixed by the plan, so results are
 // bit-reproducible.
 // ---------------------------------------------------------------------------
 constexpr int kLdsBytes = 160 * 1024;  // LDS of one CU (gfx950)
@@ -549,8 +541,8 @@ constexpr int kLdsBytes = 160 * 1024;  // LDS of one CU (gfx950)
 #endif
 
 // Launch shape of a decode variant: W waves per workgroup at WPE waves per
-// SIMD (one workgroup per CU), NB ring slots per wave, and the Q^T operands
-// of up to MAXU units resident in LDS.
+// SIMD (PER_CU = 4*WPE/W workgroups per CU), NB ring slots per wave, and the
+// Q^T operands of up to MAXU units resident in LDS.
 template <int FMT, bool SF32, int D, int NRG>
 struct DecodeCfg {
   static constexpr int SLOT = Ring<FMT, SF32, D>::SLOT;
@@ -651,7 +643,7 @@ __global__ __launch_bounds__(64 * W) __attribute__((amdgpu_waves_per_eu(WPE, WPE
 void paged_decode_kernel(AttnParams p) {
   using CFG = DecodeCfg<FMT, SF32, D, NRG>;
   using SH = DecodeShared<FMT, SF32, D, NRG>;
-  using U = Unit<FMT, SF32, D, NRG, false>;
+  using U = Unit<FMT, SF32, D, NRG>;
   using Regs = typename U::Regs;
   using RG = Ring<FMT, SF32, D>;
   static_assert(CFG::W == W && CFG::WPE == WPE, "launch shape");
@@ -983,7 +975,7 @@ void paged_decode_kernel(AttnParams p) {
     const int pi = cw.page_begin + (g - cbase);
     const half8_t* qt = sh.q + (ck - qfirst) * QUNIT + lane;
     u.template consume_with<true>(r, pi, grp, pi >= unmasked,
-                   [&](int rg, int pp, int) __attribute__((always_inline)) { return qt[(rg * NP + pp) * 64]; });
+                   [&](int rg, int pp) __attribute__((always_inline)) { return qt[(rg * NP + pp) * 64]; });
     head = head + 1 == NB ? 0 : head + 1;
     --count;
     fifo.pop();
@@ -1011,12 +1003,12 @@ struct PrefillShared {
   alignas(16) char ring[NB * TILE];
 };
 
-template <int FMT, bool SF32, int D, bool QSPLIT, int WPE, bool SP>
+template <int FMT, bool SF32, int D, int WPE, bool SP>
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(WPE, WPE)))
 void paged_prefill_kernel(AttnParams p) {
   constexpr int NRG = 2;  // 32 rows per wave
   using SH = PrefillShared<FMT, SF32, D, WPE>;
-  using U = Unit<FMT, SF32, D, NRG, QSPLIT>;
+  using U = Unit<FMT, SF32, D, NRG>;
   using Regs = typename U::Regs;
   using RG = Ring<FMT, SF32, D>;
   constexpr int NB = SH::NB;
@@ -1054,11 +1046,7 @@ void paged_prefill_kernel(AttnParams p) {
       const float c = p.scale_log2;
       const float x[8] = {a.x * c, a.y * c, a.z * c, a.w * c, b.x * c, b.y * c, b.z * c, b.w * c};
 #pragma unroll
-      for (int j = 0; j < 8; ++j) {
-        const _Float16 hi = (_Float16)x[j];
-        u.qhi[rg][pp][j] = hi;
-        u.qlo[rg][pp][j] = QSPLIT ? (_Float16)(x[j] - (float)hi) : (_Float16)0.0f;
-      }
+      for (int j = 0; j < 8; ++j) u.q[rg][pp][j] = (_Float16)x[j];
     }
     u.lim[rg] = valid ? w.ctx + w.row_begin + r / w.rows_per_query : -1;
     u.base[rg] = 0.0f;
@@ -1117,7 +1105,7 @@ void paged_prefill_kernel(AttnParams p) {
           read_page<FMT, SF32, D>(ra, tile + j * RG::SLOT, lane, grp);
           read_page<FMT, SF32, D>(rb, tile + (j + 1) * RG::SLOT, lane, grp);
           u.consume2(ra, rb, pi, pi + 1, grp, pi >= unmasked, pi + 1 >= unmasked,
-                     [&](int rg, int pp, int part) __attribute__((always_inline)) { return u.qop(rg, pp, part); });
+                     [&](int rg, int pp) __attribute__((always_inline)) { return u.qop(rg, pp); });
         } else if (pg < npages) {
           Regs r;
           read_page<FMT, SF32, D>(r, tile + j * RG::SLOT, lane, grp);
@@ -1321,40 +1309,36 @@ int decode_blocks_per_cu(int format, int scale_f32, int head_dim, int row_groups
   return scale_f32 ? decode_blocks_d<kI8, true, 128>(row_groups) : decode_blocks_d<kI8, false, 128>(row_groups);
 }
 
-template <int FMT, bool SF32, int D, bool QSPLIT>
+template <int FMT, bool SF32, int D>
 hipError_t launch_prefill_d(int n_units, const AttnParams& p, hipStream_t stream) {
 #ifdef TGE_PREFILL_WPE
   constexpr int wpe = TGE_PREFILL_WPE;
 #else
-  constexpr int wpe = waves_per_eu<FMT, D, 2, QSPLIT>();
+  constexpr int wpe = waves_per_eu<FMT, D, 2>();
 #endif
   if (p.sp_stride > 0) {
-    hipLaunchKernelGGL((paged_prefill_kernel<FMT, SF32, D, QSPLIT, wpe, true>), dim3((unsigned)n_units),
+    hipLaunchKernelGGL((paged_prefill_kernel<FMT, SF32, D, wpe, true>), dim3((unsigned)n_units),
                        dim3(256), 0, stream, p);
   } else {
-    hipLaunchKernelGGL((paged_prefill_kernel<FMT, SF32, D, QSPLIT, wpe, false>), dim3((unsigned)n_units),
+    hipLaunchKernelGGL((paged_prefill_kernel<FMT, SF32, D, wpe, false>), dim3((unsigned)n_units),
                        dim3(256), 0, stream, p);
   }
   return hipGetLastError();
 }
 
-hipError_t launch_prefill(int format, int scale_f32, int head_dim, bool qsplit, int n_units,
+hipError_t launch_prefill(int format, int scale_f32, int head_dim, int n_units,
                           const AttnParams& p, hipStream_t stream) {
   if (n_units <= 0) return hipSuccess;
   if (format == kF16) {
+    if (head_dim == 64) return launch_prefill_d<kF16, false, 64>(n_units, p, stream);
+    if (head_dim == 128) return launch_prefill_d<kF16, false, 128>(n_units, p, stream);
+  } else if (format == kI8) {
     if (head_dim == 64)
-      return qsplit ? launch_prefill_d<kF16, false, 64, true>(n_units, p, stream)
-                    : launch_prefill_d<kF16, false, 64, false>(n_units, p, stream);
+      return scale_f32 ? launch_prefill_d<kI8, true, 64>(n_units, p, stream)
+                       : launch_prefill_d<kI8, false, 64>(n_units, p, stream);
     if (head_dim == 128)
-      return qsplit ? launch_prefill_d<kF16, false, 128, true>(n_units, p, stream)
-                    : launch_prefill_d<kF16, false, 128, false>(n_units, p, stream);
-  } else if (format == kI8 && qsplit) {
-    if (head_dim == 64)
-      return scale_f32 ? launch_prefill_d<kI8, true, 64, true>(n_units, p, stream)
-                       : launch_prefill_d<kI8, false, 64, true>(n_units, p, stream);
-    if (head_dim == 128)
-      return scale_f32 ? launch_prefill_d<kI8, true, 128, true>(n_units, p, stream)
-                       : launch_prefill_d<kI8, false, 128, true>(n_units, p, stream);
+      return scale_f32 ? launch_prefill_d<kI8, true, 128>(n_units, p, stream)
+                       : launch_prefill_d<kI8, false, 128>(n_units, p, stream);
   }
   return hipErrorInvalidValue;
 }

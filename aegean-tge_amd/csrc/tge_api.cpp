@@ -781,7 +781,7 @@ tge::AttnParams attn_params(const tge_batch* b, const tge_kv_pool* p, int layer,
 }
 
 int run_attention(const tge_batch* b, const tge_kv_pool* p, int layer, const float* q,
-                  float* out, void* stream, const AttnPlan& pl, bool qsplit, bool decode) {
+                  float* out, void* stream, const AttnPlan& pl, bool decode) {
   hipStream_t st = static_cast<hipStream_t>(stream);
   const tge::AttnParams a = attn_params(b, p, layer, q, out, pl);
   std::array<hipEvent_t, 3>* ev = nullptr;
@@ -807,7 +807,7 @@ int run_attention(const tge_batch* b, const tge_kv_pool* p, int layer, const flo
                                pl.row_groups, pl.groups, a, st));
   } else {
     TGE_HIP(tge::launch_prefill(p->desc.format, p->desc.scale_format == TGE_SCALE_F32,
-                                b->head_dim, qsplit, (int)pl.work.size(), a, st));
+                                b->head_dim, (int)pl.work.size(), a, st));
   }
   if (ev) TGE_HIP(hipEventRecord((*ev)[1], st));
   if (!pl.reduce.empty()) {
@@ -914,7 +914,7 @@ int tge_decode_attention(const tge_batch* b, const tge_kv_pool* p, int layer,
   if (!q || !out) return fail(TGE_ERR_INVALID, "decode_attention: null q/out");
   if (!b->decode.built)
     return fail(TGE_ERR_INVALID, "decode_attention: n_new * group exceeds 64 rows");
-  return run_attention(b, p, layer, q, out, stream, b->decode, true, true);
+  return run_attention(b, p, layer, q, out, stream, b->decode, true);
 }
 
 int tge_prefill_attention(const tge_batch* b, const tge_kv_pool* p, int layer,
@@ -930,8 +930,7 @@ int tge_prefill_attention(const tge_batch* b, const tge_kv_pool* p, int layer,
     s = upload_plan(mb->prefill, b->head_dim, static_cast<hipStream_t>(stream));
     if (s != TGE_OK) return s;
   }
-  return run_attention(b, p, layer, q, out, stream, b->prefill, p->desc.format == TGE_KV_I8,
-                       false);
+  return run_attention(b, p, layer, q, out, stream, b->prefill, false);
 }
 
 int tge_batch_attention(const tge_batch* b, const tge_kv_pool* p, int layer, const float* q,
@@ -963,10 +962,9 @@ int tge_batch_attention(const tge_batch* b, const tge_kv_pool* p, int layer, con
   }
   // Long chunks first: the prefill tiles are MFMA-bound, the persistent
   // decode workgroups HBM-bound; both write disjoint rows of `out`.
-  s = run_attention(b, p, layer, q, out, stream, b->mix_prefill, p->desc.format == TGE_KV_I8,
-                    false);
+  s = run_attention(b, p, layer, q, out, stream, b->mix_prefill, false);
   if (s != TGE_OK) return s;
-  return run_attention(b, p, layer, q, out, stream, b->mix_decode, true, true);
+  return run_attention(b, p, layer, q, out, stream, b->mix_decode, true);
 }
 
 int tge_kv_gather(const tge_batch* b, const tge_kv_pool* p, int layer, int session,

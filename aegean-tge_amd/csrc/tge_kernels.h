@@ -85,7 +85,7 @@ hipError_t launch_kv_gather(int format, const GatherParams& p, hipStream_t strea
 hipError_t launch_decode(int format, int scale_f32, int head_dim, int row_groups, int n_groups,
                          const AttnParams& p, hipStream_t stream);
 // Block prefill: one workgroup per work item (tiles of up to 128 rows).
-hipError_t launch_prefill(int format, int scale_f32, int head_dim, bool qsplit, int n_units,
+hipError_t launch_prefill(int format, int scale_f32, int head_dim, int n_units,
                           const AttnParams& p, hipStream_t stream);
 // Resident decode workgroups per CU.
 int decode_blocks_per_cu(int format, int scale_f32, int head_dim, int row_groups);

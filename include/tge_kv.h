@@ -225,9 +225,9 @@ int tge_decode_attention(const tge_batch* batch, const tge_kv_pool* pool,
 /*
  * Chunked-prefill block attention (attention_block_head_avx2,
  * attention_avx2.cpp:660-864): each new token attends causally to every
- * prior page and the chunk itself, on f16 MFMA (Q rounded to f16 for F16
- * pools; I8 pools keep Q as f16 hi + lo, the reference's per-token i8 path
- * qwen2.cpp:1535-1538 computes the same values). Tiles of up to 128
+ * prior page and the chunk itself, on f16 MFMA (Q rounded to f16 as in
+ * decode; I8 pools run the same kernel where the reference takes its
+ * per-token i8 path, qwen2.cpp:1535-1538). Tiles of up to 128
  * (query, head) rows of one KV head's query group; long prefixes are split
  * and merged like decode.
  */
