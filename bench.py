@@ -21,7 +21,10 @@ dispatch from the committed rocprofv3 counter summary for this workload. cpu_bas
 (oracle/_ref, built from the reference sources) under the reference's
 forward_batch schedule, on a bounded sample of the same workload.
 The other four configurations are measured briefly and reported under
-"configs" (they are parity cases, not the headline).
+"configs" (they are parity cases, not the headline), each with its own
+"cpu_baseline": the reference's AVX2 kernels under the schedule the
+reference runs for that configuration (decode of one sequence, a batched
+step, block prefill per chunk), timed for a few seconds at most.
 
 Usage: python bench.py [--gpus 1] [--steps 32] [--warmup 4] [--no-others]
        [--no-cpu] [--cpu-seconds 10]
@@ -577,6 +580,138 @@ def cpu_baseline_c5(synth, cfg, seconds):
     }
 
 
+def _ref_team(seconds):
+    import oracle as O
+    ref = O.ref()
+    if ref is None or seconds <= 0:
+        return None, None, 0
+    threads = min(16, os.cpu_count() or 1)
+    return O, ref, threads
+
+
+def _timed(fn, seconds, min_reps=3, max_reps=1000):
+    reps, total = 0, 0.0
+    while reps < min_reps or (total < seconds and reps < max_reps):
+        t0 = time.perf_counter()
+        fn()
+        total += time.perf_counter() - t0
+        reps += 1
+    return total / reps, reps, total
+
+
+def cpu_baseline_decode(synth, cfg, seconds):
+    """The reference's decode attention for one layer-step of c1-c3 on its
+    own AVX2 kernels (oracle/_ref): one sequence goes through
+    Qwen2::attention (qwen2.cpp:1319-1380: attention_group_avx2 over span
+    chunks + merge_gqa_chunks from 256 positions on), several sessions
+    through forward_batch (qwen2.cpp:1705-1747: attention_head_avx2 per row
+    and head). Every session sits at its context + half the decode steps
+    (the run's mean span); the reference's flat cache, its own f32 int8
+    scales. Attention only (the one-row store per session is a copy)."""
+    O, ref, threads = _ref_team(seconds)
+    if ref is None:
+        return None
+    sh = cfg.shape
+    rng = np.random.default_rng(cfg.seed + 9)
+    spans = [c + cfg.steps // 2 + 1 for c in cfg.contexts]
+    rows_kv = sum(spans)
+    i8 = cfg.fmt == synth.tge_kv.KV_I8
+    if i8:
+        kc = rng.integers(-127, 128, size=(rows_kv, sh.kv_dim), dtype=np.int8)
+        vc = rng.integers(-127, 128, size=(rows_kv, sh.kv_dim), dtype=np.int8)
+        ks = rng.uniform(0.005, 0.05, size=(rows_kv, sh.kv_dim // 32)).astype(np.float32)
+        vs = rng.uniform(0.005, 0.05, size=(rows_kv, sh.kv_dim // 32)).astype(np.float32)
+    else:
+        kc = rng.standard_normal((rows_kv, sh.kv_dim)).astype(np.float16).view(np.uint16)
+        vc = rng.standard_normal((rows_kv, sh.kv_dim)).astype(np.float16).view(np.uint16)
+        ks = vs = np.zeros(1, np.float32)
+    n = len(spans)
+    q = rng.standard_normal((n, sh.q_dim)).astype(np.float32)
+    out = np.empty((n, sh.q_dim), np.float32)
+    fp = lambda a: a.ctypes.data_as(C.c_void_p)
+    fmt = O.I8 if i8 else O.F16
+    team = ref.ref_team_create(threads)
+    try:
+        if n == 1:
+            group = sh.q_heads // sh.kv_heads
+            scratch = np.empty(sh.kv_heads * 16 * group * (sh.head_dim + 2)
+                               + sh.q_heads * spans[0] + sh.head_dim, np.float32)
+            fn = lambda: ref.ref_baseline_decode(team, fmt, fp(q), fp(kc), fp(vc), fp(ks), fp(vs),
+                                                 sh.q_heads, sh.kv_heads, sh.head_dim, spans[0],
+                                                 fp(scratch), fp(out))
+            schedule = "Qwen2::attention (qwen2.cpp:1319-1380)"
+        else:
+            bases = np.cumsum([0] + spans[:-1]).astype(np.int64) * sh.kv_dim
+            s_arr = np.array(spans, np.int32)
+            scores = np.empty(n * sh.q_heads * max(spans), np.float32)
+            fn = lambda: ref.ref_baseline_batch_heads(team, fmt, fp(q), fp(kc), fp(vc), fp(ks),
+                                                      fp(vs), fp(bases), fp(s_arr), n, sh.q_heads,
+                                                      sh.kv_heads, sh.head_dim, max(spans),
+                                                      fp(scores), fp(out))
+            schedule = "forward_batch (qwen2.cpp:1705-1747)"
+        per, reps, total = _timed(fn, seconds)
+    finally:
+        ref.ref_team_destroy(team)
+    elem = 1 if i8 else 2
+    alg = sum(2 * S * sh.kv_dim * elem + (2 * S * (sh.kv_dim // 32) * 4 if i8 else 0)
+              + 2 * sh.q_dim * 4 for S in spans)
+    return {
+        "value": alg / per / 1e9,
+        "unit": "GB/s",
+        "cores": threads,
+        "kind": "reference",
+        "us_per_layer_step": 1e6 * per,
+        "sample": (f"reference {'attention_group_avx2 + attention_head_avx2' if n == 1 else 'attention_head_avx2'} "
+                   f"(oracle/_ref) under {schedule}, {threads} threads, spans {spans}, "
+                   f"one layer-step's attention repeated {reps}x in {total:.1f} s"),
+    }
+
+
+def cpu_baseline_prefill(synth, cfg, seconds):
+    """The reference's block prefill (attention_batch's query-block path,
+    qwen2.cpp:1524-1571: attention_block_head_avx2, one task per query head)
+    for each causal chunk of the c4 prompt over a flat f16 cache, on its own
+    AVX2 kernel (oracle/_ref)."""
+    O, ref, threads = _ref_team(seconds)
+    if ref is None:
+        return None
+    sh = cfg.shape
+    rng = np.random.default_rng(cfg.seed + 9)
+    n, ch = cfg.prompt, cfg.prefill_chunk
+    kc = rng.standard_normal((n, sh.kv_dim)).astype(np.float16).view(np.uint16)
+    vc = rng.standard_normal((n, sh.kv_dim)).astype(np.float16).view(np.uint16)
+    q = rng.standard_normal((ch, sh.q_dim)).astype(np.float32)
+    out = np.empty((ch, sh.q_dim), np.float32)
+    scores = np.empty(sh.q_heads * ch * n, np.float32)
+    fp = lambda a: a.ctypes.data_as(C.c_void_p)
+    team = ref.ref_team_create(threads)
+    per_chunk, reps_used = [], []
+    try:
+        for c in range(n // ch):
+            ctx = (c + 1) * ch
+            fn = lambda: ref.ref_baseline_block_prefill(team, O.F16, fp(q), fp(kc), fp(vc), ch,
+                                                        c * ch, sh.q_heads, sh.kv_heads,
+                                                        sh.head_dim, ctx, fp(scores), fp(out))
+            per, reps, _ = _timed(fn, seconds / (n // ch), min_reps=1)
+            per_chunk.append(per)
+            reps_used.append(reps)
+    finally:
+        ref.ref_team_destroy(team)
+    flops = sum(synth.prefill_flops(sh, c * ch, ch) for c in range(n // ch))
+    return {
+        "value": flops / sum(per_chunk) / 1e12,
+        "unit": "TFLOP/s",
+        "cores": threads,
+        "kind": "reference",
+        "us_per_layer_chunk": [1e6 * t for t in per_chunk],
+        "prompt_ms_est": 1e3 * sum(per_chunk) * sh.layers,
+        "sample": (f"reference attention_block_head_avx2 (oracle/_ref) under attention_batch's "
+                   f"query-block schedule (qwen2.cpp:1540-1571), {threads} threads, each of the "
+                   f"{n // ch} chunks of one layer timed {reps_used}x; prompt time scaled to "
+                   f"{sh.layers} layers"),
+    }
+
+
 def measured_traffic(workload):
     """HBM bytes per dispatch of the paged attention kernel on this workload,
     from the committed rocprofv3 counter summary (FETCH_SIZE and WRITE_SIZE
@@ -646,14 +781,17 @@ def main():
             continue
         cfg = cfgs[key]
         log(f"[bench] {key}: {cfg.note}")
+        cpu_s = min(2.0, args.cpu_seconds / 5) if args.cpu else 0.0
         if key == "c4":
             others[key] = run_prefill(tk, synth, cfg)
+            others[key]["cpu_baseline"] = cpu_baseline_prefill(synth, cfg, cpu_s)
         else:
             b = DecodeBench(tk, synth, cfg, cfg.steps + 4)
             r = b.run(cfg.steps, 4, 3)
             r["frac_attn"] = r["attn_gbs"] / HBM_PEAK_GBS
-            others[key] = r
             b.model.close()
+            r["cpu_baseline"] = cpu_baseline_decode(synth, cfg, cpu_s)
+            others[key] = r
         log(f"[bench] {key}: {json.dumps(others[key])}")
     if args.only and args.only != "c5":
         print(json.dumps({args.only: others[args.only]}))
