@@ -104,10 +104,11 @@ struct PageRegs {
   uint32_t vs[SW > 0 ? SW : 1];
 };
 
-// Buffer resource of one layer's block array. Loads address a page block with
-// a wave-uniform byte offset (SGPR) plus the lane's fixed chunk offset
-// (VGPR); offsets past the end of the array read zeros instead of faulting.
-__device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void* base, uint32_t bytes) {
+// Buffer resource of one page block (64-bit base, so a layer's array may
+// exceed 4 GiB). Loads add the lane's chunk offset (VGPR); offsets past the
+// block read zeros instead of faulting.
+[[maybe_unused]] __device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void* base,
+                                                                         uint32_t bytes) {
   return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), (short)0, (int)bytes,
                                            0x00020000);
 }
@@ -138,16 +139,19 @@ constexpr int waves_per_eu() {
   return D == 64 ? (NRG <= 2 ? 3 : 2) : (NRG <= 2 ? 2 : 1);
 }
 
-// Issue the direct-to-LDS loads of the page block at byte offset `boff` of
-// the layer's array into `slot`: the block's K part, V part and (int8) the
-// K and V scale parts, which follow each other in memory. The instruction
-// offset field stays 0 (it would move the LDS address too); every offset
-// goes into the lane's VGPR.
+// Issue the direct-to-LDS loads of the page block at `block` into `slot`:
+// the block's K part, V part and (int8) the K and V scale parts, which follow
+// each other in memory. The block gets its own buffer resource (wave-uniform,
+// built from the 64-bit address in scalar registers); the instruction offset
+// field stays 0 (it would move the LDS address too), so every offset goes
+// into the lane's VGPR.
 template <int FMT, bool SF32, int D>
-__device__ __forceinline__ void fetch_page(char* slot, __amdgpu_buffer_rsrc_t rs, uint32_t boff,
+__device__ __forceinline__ void fetch_page(char* slot, const char* block, uint32_t block_bytes,
                                            int lane) {
 #if defined(__HIP_DEVICE_COMPILE__)  // the LDS-load builtins exist for the device pass only
   using RG = Ring<FMT, SF32, D>;
+  const __amdgpu_buffer_rsrc_t rs = make_rsrc(block, block_bytes);
+  constexpr uint32_t boff = 0;
 #pragma unroll
   for (int i = 0; i < RG::PIECES; ++i) {
     __builtin_amdgcn_raw_ptr_buffer_load_lds(rs, (lds_void_t*)(slot + i * 1024), 16,
@@ -666,7 +670,6 @@ void paged_decode_kernel(AttnParams p) {
   const sconst_work* work = (const sconst_work*)p.work;
   const int q_stride = p.q_heads * D;
 
-  const __amdgpu_buffer_rsrc_t rs = make_rsrc(p.pool, p.array_bytes);
   char* ring = sh.ring + wave * NB * RG::SLOT;
 
   // ---- Q^T operands of units [qfirst, qfirst + MAXU) in LDS ----------------
@@ -791,8 +794,9 @@ void paged_decode_kernel(AttnParams p) {
   auto issue = [&](int slot) __attribute__((always_inline)) -> int {
     const int g = pend_g;
     if (g >= 0) {
-      const uint32_t off = (uint32_t)(pend_id * p.kv_heads + pend_head) * p.block_bytes;
-      fetch_page<FMT, SF32, D>(ring + slot * RG::SLOT, rs, off, lane);
+      const char* blk = static_cast<const char*>(p.pool) +
+                        ((size_t)pend_id * p.kv_heads + pend_head) * p.block_bytes;
+      fetch_page<FMT, SF32, D>(ring + slot * RG::SLOT, blk, p.block_bytes, lane);
     }
     return g;
   };
@@ -1025,8 +1029,6 @@ void paged_prefill_kernel(AttnParams p) {
   const int row0 = wave * 32;
   const bool has_rows = row0 < w.rows;
 
-  const __amdgpu_buffer_rsrc_t rs = make_rsrc(p.pool, p.array_bytes);
-
   // This wave's rows: Q^T operands (as in attend_unit) and visible limits.
   U u;
 #pragma unroll
@@ -1067,8 +1069,10 @@ void paged_prefill_kernel(AttnParams p) {
   auto fetch_tile = [&](int k) __attribute__((always_inline)) -> void {
     const int j = k * kWaves + wave;
     if (j < npages) {
-      fetch_page<FMT, SF32, D>(sh.ring + (k % NB) * SH::TILE + wave * RG::SLOT, rs,
-                               (uint32_t)(table[j] * p.kv_heads + w.kv_head) * p.block_bytes, lane);
+      const char* blk = static_cast<const char*>(p.pool) +
+                        ((size_t)table[j] * p.kv_heads + w.kv_head) * p.block_bytes;
+      fetch_page<FMT, SF32, D>(sh.ring + (k % NB) * SH::TILE + wave * RG::SLOT, blk,
+                               p.block_bytes, lane);
     }
   };
 #pragma unroll

@@ -210,13 +210,9 @@ int tge_kv_pool_create(const tge_kv_pool_desc* desc, tge_kv_pool** out) {
   p->desc = d;
   p->geom = tge::block_geom(d.format, d.head_dim, d.format == TGE_KV_I8 && d.scale_format == TGE_SCALE_F32);
   p->layer_blocks = (size_t)d.pages * d.kv_heads;
-  // Attention kernels address one layer's block array with 32-bit buffer
-  // offsets.
+  // Kernels address a page block by its 64-bit address (one buffer
+  // resource per block), so a layer's array has no 32-bit limit.
   const size_t layer_bytes = (size_t)p->geom.block_bytes * p->layer_blocks;
-  if (layer_bytes >= (size_t(1) << 31)) {
-    delete p;
-    return fail(TGE_ERR_CAPACITY, "kv_pool_create: one layer's page blocks must stay below 2 GiB");
-  }
   const size_t total = layer_bytes * d.layers;
   hipError_t e = hipMalloc(&p->blocks, total);
   if (e == hipSuccess) e = hipMemset(p->blocks, 0, total);
@@ -760,7 +756,6 @@ tge::AttnParams attn_params(const tge_batch* b, const tge_kv_pool* p, int layer,
   tge_kv_pool_layer(p, layer, &v);
   tge::AttnParams a{};
   a.pool = v.k;
-  a.array_bytes = (uint32_t)(p->geom.block_bytes * p->layer_blocks);
   a.block_bytes = (uint32_t)p->geom.block_bytes;
   a.sessions = reinterpret_cast<const tge::SessionRec*>(b->dev + b->off_sessions);
   a.work = reinterpret_cast<const tge::WorkRec*>(pl.dev);

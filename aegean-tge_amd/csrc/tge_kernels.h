@@ -47,7 +47,6 @@ struct GatherParams {
 
 struct AttnParams {
   const void* pool;       // layer base: the layer's page blocks
-  uint32_t array_bytes;   // bytes of the layer's block array, < 2^31
   uint32_t block_bytes;   // block stride
   const SessionRec* sessions;
   const WorkRec* work;

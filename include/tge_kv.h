@@ -46,9 +46,9 @@ enum tge_status {
   TGE_ERR_RUNTIME = -2,     /* misuse of model/table state (std::runtime_error) */
   TGE_ERR_UNAVAILABLE = -3, /* no usable gfx950 device, or forced off */
   TGE_ERR_DEVICE = -4,      /* a HIP runtime call failed */
-  TGE_ERR_CAPACITY = -5     /* out of device/host memory, or a layer array
-                               beyond 2 GiB (a full BlockTable is
-                               TGE_ERR_RUNTIME, as the reference throws) */
+  TGE_ERR_CAPACITY = -5     /* out of device/host memory (a full
+                               BlockTable is TGE_ERR_RUNTIME, as the
+                               reference throws) */
 };
 
 enum tge_kv_format {

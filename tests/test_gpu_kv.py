@@ -329,6 +329,50 @@ def test_prefill_chunks_match_oracle(gpu):
     pool.close()
 
 
+@pytest.mark.parametrize("fmt", [tk.KV_F16, tk.KV_I8])
+def test_pool_layer_beyond_4gib(gpu, fmt):
+    """One layer's block array past 4 GiB: the kernels address each page
+    block by its 64-bit address, so a session whose pages alternate between
+    the array's last 20,000 pages (byte offsets above 4 GiB) and its first
+    1,000 appends, block-prefills and decodes like any other."""
+    qh, kvh, hd = 14, 2, 128
+    n_pages = 300_000 if fmt == tk.KV_F16 else 600_000  # 8192 or 4352 B blocks
+    pool = tk.KvPool(1, n_pages, kvh, hd, fmt, tk.SCALE_F16)
+    block_bytes = 8192 if fmt == tk.KV_F16 else 4352
+    assert pool.bytes() > (1 << 32) + 20_000 * kvh * block_bytes
+    rng = np.random.default_rng(41)
+    hi = rng.choice(np.arange(n_pages - 20_000, n_pages), 6, replace=False)
+    lo = rng.choice(np.arange(0, 1_000), 6, replace=False)
+    pages = [int(x) for pair in zip(hi, lo) for x in pair]
+    assert min(hi) * kvh * block_bytes >= 1 << 32
+    n_fill, n_dec = 150, 1
+    total = n_fill + n_dec
+    k = rng.standard_normal((total, kvh * hd)).astype(np.float32)
+    v = rng.standard_normal((total, kvh * hd)).astype(np.float32)
+    q = rng.standard_normal((total, qh * hd)).astype(np.float32)
+    say(f"beyond-4GiB fmt={fmt} pages {pages}")
+    fc = O.FlatCache(O.F16 if fmt == tk.KV_F16 else O.I8, k, v)
+    if fmt == tk.KV_I8:
+        fc.with_scales(O.half_to_float(O.float_to_half(fc.ks)),
+                       O.half_to_float(O.float_to_half(fc.vs)))
+    for start, n, kind in ((0, n_fill, "prefill"), (n_fill, n_dec, "decode")):
+        b = tk.Batch().plan(pool, [tk.Session(start, n, pages)], qh)
+        dk = tk.DeviceArray.from_numpy(k[start:start + n])
+        dv = tk.DeviceArray.from_numpy(v[start:start + n])
+        dq = tk.DeviceArray.from_numpy(q[start:start + n])
+        dout = tk.DeviceArray((n, qh * hd), np.float32).zero()
+        b.append(pool, 0, dk, dv)
+        getattr(b, kind)(pool, 0, dq, dout)
+        tk.hip().sync()
+        want = fc.attend(q[start:start + n], qh, kvh, hd, start)
+        err = assert_attention_close(dout.numpy(), want, f"{kind} beyond 4 GiB")
+        say(f"  {kind}: max abs err {err:.2e}")
+        for a in (dk, dv, dq, dout):
+            a.close()
+        b.close()
+    pool.close()
+
+
 def test_prefill_i8_matches_oracle(gpu):
     case = PagedCase(14, 2, 64, tk.KV_I8, [40], 70, seed=12)
     case.fill()
