@@ -452,8 +452,14 @@ void build_decode(tge_batch* b, Residency res, AttnPlan& pl, int only) {
     for (int h = 0; h < b->kv_heads; ++h) segs.push_back(Seg{s, h, pages});
     total += (long)pages * b->kv_heads;
   }
-  // At least 16 pages per workgroup.
-  const long g_eff = std::max<long>(1, std::min<long>(res.groups, (total + 15) / 16));
+  // At least 8 pages per workgroup: on small steps (one to four sessions
+  // of 1k-8k positions) shorter chains win over fewer split merges down to
+  // 8 pages (c1-c3: 5-7 % per layer-step against 16; 4 is slower again).
+#ifndef TGE_DECODE_MIN_PAGES
+#define TGE_DECODE_MIN_PAGES 8
+#endif
+  const long g_eff = std::max<long>(
+      1, std::min<long>(res.groups, (total + TGE_DECODE_MIN_PAGES - 1) / TGE_DECODE_MIN_PAGES));
   std::vector<double> w((size_t)g_eff);
   double wrem = 0.0;
   for (long g = 0; g < g_eff; ++g) {
