@@ -387,3 +387,41 @@ def test_driver_sparse_config(gpu):
             md.m.set_sparse(4, 100, 1)
         assert e.value.status == tk.ERR_RUNTIME
         md.close()
+
+
+@pytest.mark.parametrize("fmt", [tk.KV_F16, tk.KV_I8])
+def test_native_cpp_driver(gpu, tmp_path, fmt):
+    """The C++20 driver used natively (tests/native/driver_check.cpp, built
+    by the package Makefile): hipMalloc'd buffers, a second sequence's pages
+    interleaved, a 37-token prefill chunk and three decode steps per layer
+    through tge::models::Qwen2KvPath, then its misuse exceptions
+    (qwen2.cpp:2036-2044). Outputs match the oracle's flat cache."""
+    import os
+    import subprocess
+    exe = os.path.join(os.path.dirname(tk.LIB_PATH), "bin", "driver_check")
+    if not os.path.exists(exe):
+        pytest.fail(f"{exe} is missing: build the package (make -C aegean-tge_amd)")
+    layers, qh, kvh, hd, n_pre, n_dec, context = 2, 14, 2, 64, 37, 3, 256
+    n = n_pre + n_dec
+    rng = np.random.default_rng(90 + fmt)
+    data = [[rng.standard_normal((n, d)).astype(np.float32) for d in (kvh * hd, kvh * hd, qh * hd)]
+            for _ in range(layers)]
+    src = tmp_path / "in.bin"
+    with open(src, "wb") as f:
+        f.write(np.array([layers, qh, kvh, hd, n_pre, n_dec, context, fmt], np.int32).tobytes())
+        for k, v, q in data:
+            f.write(k.tobytes() + v.tobytes() + q.tobytes())
+    dst = tmp_path / "out.bin"
+    say(f"native driver_check fmt={fmt}")
+    r = subprocess.run([exe, str(src), str(dst)], capture_output=True, text=True, timeout=120)
+    assert r.returncode == 0, r.stderr
+    assert "exceptions ok" in r.stdout
+    got = np.fromfile(dst, np.float32).reshape(layers, n, qh * hd)
+    for layer, (k, v, q) in enumerate(data):
+        fc = O.FlatCache(O.F16 if fmt == tk.KV_F16 else O.I8, k, v)
+        if fmt == tk.KV_I8:
+            fc.with_scales(O.half_to_float(O.float_to_half(fc.ks)),
+                           O.half_to_float(O.float_to_half(fc.vs)))
+        want = fc.attend(q, qh, kvh, hd, 0)
+        err = assert_attention_close(got[layer], want, f"native driver layer {layer}")
+        say(f"  layer {layer}: max abs err {err:.2e}")
