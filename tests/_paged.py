@@ -69,6 +69,8 @@ class PagedCase:
         b.append(self.pool, layer, dk, dv)
         if kind == "decode":
             b.decode(self.pool, layer, dq, dout)
+        elif kind == "mixed":
+            b.attention(self.pool, layer, dq, dout)
         else:
             b.prefill(self.pool, layer, dq, dout)
         tk.hip().sync()

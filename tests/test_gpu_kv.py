@@ -550,14 +550,15 @@ def test_static_sparse_attention(gpu, fmt, sparse, kind):
 def _random_case(i):
     """Seeded random shape for test_random_cases: GQA group 1-8, 1-8 KV
     heads, head_dim 64/128, f16 or int8 (f16 or f32 scales), 1-6 sessions
-    with empty, ragged and page-aligned contexts, decode or block prefill."""
+    with empty, ragged and page-aligned contexts; decode, block prefill or
+    a mixed step."""
     r = np.random.default_rng(1000 + i)
     kvh = int(r.choice([1, 2, 4, 8]))
     group = int(r.integers(1, 9))
     hd = int(r.choice([64, 128]))
     fmt = int(r.choice([tk.KV_F16, tk.KV_I8]))
     sf = int(r.choice([tk.SCALE_F16, tk.SCALE_F32])) if fmt == tk.KV_I8 else tk.SCALE_F16
-    kind = "decode" if i % 3 else "prefill"
+    kind = "mixed" if i >= 16 else "decode" if i % 3 else "prefill"
     n_s = int(r.integers(1, 7))
     ctx_max = 6000 if kind == "decode" else 1500
     contexts = []
@@ -567,16 +568,20 @@ def _random_case(i):
                         else int(r.integers(1, ctx_max)))
     if kind == "decode":
         n_new = [int(r.integers(1, 64 // group + 1)) for _ in range(n_s)]
+    elif kind == "mixed":  # each session decodes (rows fit a unit) or prefills
+        n_new = [int(r.integers(1, 64 // group + 1)) if r.integers(0, 2) else
+                 int(r.integers(64 // group + 1, 121)) for _ in range(n_s)]
     else:
         n_new = [int(r.integers(1, 81)) for _ in range(n_s)]
     return dict(qh=kvh * group, kvh=kvh, hd=hd, fmt=fmt, sf=sf, kind=kind, contexts=contexts,
                 n_new=n_new)
 
 
-@pytest.mark.parametrize("i", range(16))
+@pytest.mark.parametrize("i", range(24))
 def test_random_cases(gpu, i):
-    """Sixteen seeded random configurations (shapes, formats, ragged spans
-    including empty contexts, decode and block prefill) against the oracle."""
+    """Twenty-four seeded random configurations (shapes, formats, ragged
+    spans including empty contexts; decode, block prefill, and steps mixing
+    both through tge_batch_attention) against the oracle."""
     c = _random_case(i)
     say(f"random case {i}: {c}")
     case = PagedCase(c["qh"], c["kvh"], c["hd"], c["fmt"], c["contexts"], c["n_new"],
