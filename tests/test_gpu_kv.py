@@ -547,7 +547,7 @@ def test_static_sparse_attention(gpu, fmt, sparse, kind):
     case.close()
 
 
-def _random_case(i):
+def _random_case(i, kind=None):
     """Seeded random shape for test_random_cases: GQA group 1-8, 1-8 KV
     heads, head_dim 64/128, f16 or int8 (f16 or f32 scales), 1-6 sessions
     with empty, ragged and page-aligned contexts; decode, block prefill or
@@ -558,7 +558,8 @@ def _random_case(i):
     hd = int(r.choice([64, 128]))
     fmt = int(r.choice([tk.KV_F16, tk.KV_I8]))
     sf = int(r.choice([tk.SCALE_F16, tk.SCALE_F32])) if fmt == tk.KV_I8 else tk.SCALE_F16
-    kind = "mixed" if i >= 16 else "decode" if i % 3 else "prefill"
+    if kind is None:
+        kind = "mixed" if i >= 16 else "decode" if i % 3 else "prefill"
     n_s = int(r.integers(1, 7))
     ctx_max = 6000 if kind == "decode" else 1500
     contexts = []
@@ -590,5 +591,37 @@ def test_random_cases(gpu, i):
     got, b = case.step(kind=c["kind"])
     err = assert_attention_close(got, case.oracle_out(), f"random case {i}")
     say(f"  max abs err {err:.2e}")
+    b.close()
+    case.close()
+
+
+@pytest.mark.parametrize("i", range(12))
+def test_random_sparse_cases(gpu, i):
+    """Twelve seeded random static sparse subsets (sink 0-40, window 1-600,
+    stride 2-70, so both the masking-only and the page-skipping decode paths
+    run) over random shapes and kinds, against the oracle's sparse head."""
+    c = _random_case(100 + i, ("decode", "decode", "prefill", "mixed")[i % 4])
+    r = np.random.default_rng(3000 + i)
+    sparse = (int(r.integers(0, 41)), int(r.integers(1, 601)),
+              int(r.choice([int(r.integers(2, 17)), int(r.integers(17, 71))])))
+    say(f"random sparse case {i}: {c} sparse {sparse}")
+    case = PagedCase(c["qh"], c["kvh"], c["hd"], c["fmt"], c["contexts"], c["n_new"],
+                     scale_format=c["sf"], seed=4000 + i)
+    case.fill()
+    case.sparse = sparse
+    b = tk.Batch().plan(case.pool, case.sessions(True), case.qh).set_sparse(*sparse)
+    kk = np.concatenate([k[cc:] for k, cc in zip(case.k, case.contexts)])
+    vv = np.concatenate([v[cc:] for v, cc in zip(case.v, case.contexts)])
+    dk, dv = tk.DeviceArray.from_numpy(kk), tk.DeviceArray.from_numpy(vv)
+    dq = tk.DeviceArray.from_numpy(case.q)
+    out = tk.DeviceArray(case.q.shape, np.float32).zero()
+    b.append(case.pool, 0, dk, dv)
+    {"decode": b.decode, "prefill": b.prefill, "mixed": b.attention}[c["kind"]](
+        case.pool, 0, dq, out)
+    tk.hip().sync()
+    err = assert_attention_close(out.numpy(), case.oracle_out(), f"random sparse case {i}")
+    say(f"  max abs err {err:.2e}")
+    for a in (dk, dv, dq, out):
+        a.close()
     b.close()
     case.close()
