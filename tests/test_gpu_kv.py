@@ -625,3 +625,26 @@ def test_random_sparse_cases(gpu, i):
         a.close()
     b.close()
     case.close()
+
+
+@pytest.mark.parametrize("i", range(10))
+def test_random_append_bitexact(gpu, i):
+    """Ten seeded random shapes (the random-case generator's heads, head_dim,
+    formats, scale formats, empty and ragged contexts, 1-120 new rows per
+    session crossing page boundaries): after the fill and one appended step,
+    every session's pool contents (codes, f16 bits, scales) equal the
+    oracle's store bit for bit, read both through the gather and by the
+    layout formula."""
+    c = _random_case(200 + i, "prefill")
+    r = np.random.default_rng(5000 + i)
+    c["contexts"] = [min(x, 1200) for x in c["contexts"]]
+    c["n_new"] = [int(r.integers(1, 121)) for _ in c["n_new"]]
+    say(f"random append case {i}: {c}")
+    case = PagedCase(c["qh"], c["kvh"], c["hd"], c["fmt"], c["contexts"], c["n_new"],
+                     scale_format=c["sf"], seed=6000 + i,
+                     outlier_frac=0.01 if c["fmt"] == tk.KV_I8 else 0)
+    case.fill()
+    _, b = case.step(kind="prefill")
+    b.close()
+    check_contents(case)
+    case.close()
