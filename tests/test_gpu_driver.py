@@ -425,3 +425,53 @@ def test_native_cpp_driver(gpu, tmp_path, fmt):
         want = fc.attend(q, qh, kvh, hd, 0)
         err = assert_attention_close(got[layer], want, f"native driver layer {layer}")
         say(f"  layer {layer}: max abs err {err:.2e}")
+
+
+@pytest.mark.parametrize("fmt", [tk.KV_F16, tk.KV_I8])
+def test_random_serving_flow(gpu, fmt):
+    """A seeded serving run through the driver (c5's pattern at small size,
+    7B-like group of 7): twelve forward_batch steps over a random subset of
+    six sequences with 1-4 new tokens each, and every fourth step one
+    sequence reset and refilled with a random-length prompt (its pages go
+    back to the table and are reused). Every step's rows match the oracle
+    and the lengths follow."""
+    say(f"random serving flow fmt={fmt}")
+    md = Model(1, 28, 4, 128, fmt, sequences=6, pages=600, context=2048, seed=70, fragment=71)
+    r = np.random.default_rng(72)
+    length = [0] * 6
+
+    def refill(s):
+        n = int(r.integers(1, 700))
+        md.m.reset(s)
+        _, k, v = md.rows(n)
+        md.m.begin_prefill(s, 0, n)
+        md.k.pop((0, s), None)
+        md.v.pop((0, s), None)
+        md.keep(s, 0, k, v)
+        md.run_layers(None, k, v, attend=False)
+        length[s] = n
+
+    for s in range(6):
+        refill(s)
+    for step in range(12):
+        if step % 4 == 3:
+            refill(int(r.integers(0, 6)))
+        seqs = sorted(int(x) for x in r.choice(6, int(r.integers(1, 7)), replace=False))
+        counts = [int(r.integers(1, 5)) for _ in seqs]
+        positions = [length[s] + i for s, n in zip(seqs, counts) for i in range(n)]
+        owners = [s for s, n in zip(seqs, counts) for _ in range(n)]
+        q, k, v = md.rows(len(positions))
+        md.m.begin_forward_batch(positions, owners)
+        row = 0
+        for s, n in zip(seqs, counts):
+            md.keep(s, length[s], [k[0][row:row + n]], [v[0][row:row + n]])
+            row += n
+        out = md.run_layers(q, k, v)[0]
+        want, row = [], 0
+        for s, n in zip(seqs, counts):
+            want.append(md.oracle(0, s, q[0][row:row + n], length[s]))
+            row += n
+            length[s] += n
+        assert_attention_close(out, np.concatenate(want), f"serving step {step}")
+        assert [md.m.length(s) for s in range(6)] == length
+    md.close()
