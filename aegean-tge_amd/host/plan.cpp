@@ -1,0 +1,380 @@
+// Host-side planning of one step: see plan.hpp.
+#include "plan.hpp"
+
+#include <algorithm>
+#include <cmath>
+#include <cstring>
+
+#include "tge_kv.h"
+
+namespace tge::plan {
+
+namespace {
+std::size_t align256(std::size_t x) { return (x + 255) & ~std::size_t(255); }
+}  // namespace
+
+int Staged::upload(MemOps& m, std::size_t bytes, void* stream,
+                   const std::function<void(char*)>& fill) {
+  bytes = std::max<std::size_t>(bytes, 256);
+  if (staged) {
+    const int s = m.wait_event(staged);
+    if (s != TGE_OK) return s;
+  }
+  if (bytes > host_bytes) {
+    if (host) m.host_free(host);
+    host = nullptr;
+    host_bytes = 0;
+    const int s = m.host_alloc(&host, bytes);
+    if (s != TGE_OK) {
+      host = nullptr;
+      return s;
+    }
+    host_bytes = bytes;
+  }
+  if (bytes > dev_bytes) {
+    if (dev) {
+      const int s = m.wait_stream(stream);  // queued kernels may still read it
+      if (s != TGE_OK) return s;
+      m.dev_free(dev);
+    }
+    dev = nullptr;
+    dev_bytes = 0;
+    const int s = m.dev_alloc(&dev, bytes);
+    if (s != TGE_OK) {
+      dev = nullptr;
+      return s;
+    }
+    dev_bytes = bytes;
+  }
+  fill(host);
+  int s = m.copy_to_device(dev, host, bytes, stream);
+  if (s == TGE_OK) s = m.record(&staged, stream);
+  return s;
+}
+
+void Staged::release(MemOps& m) {
+  if (dev) m.dev_free(dev);
+  if (host) m.host_free(host);
+  if (staged) m.event_free(staged);
+  dev = host = nullptr;
+  staged = nullptr;
+  dev_bytes = host_bytes = 0;
+}
+
+int Scratch::reserve(MemOps& m, std::size_t need, void* stream) {
+  if (need <= bytes) return TGE_OK;
+  if (dev) {
+    const int s = m.wait_stream(stream);
+    if (s != TGE_OK) return s;
+    m.dev_free(dev);
+  }
+  dev = nullptr;
+  bytes = 0;
+  const int s = m.dev_alloc(&dev, need);
+  if (s != TGE_OK) {
+    dev = nullptr;
+    return s;
+  }
+  bytes = need;
+  return TGE_OK;
+}
+
+void Scratch::release(MemOps& m) {
+  if (dev) m.dev_free(dev);
+  dev = nullptr;
+  bytes = 0;
+}
+
+int build_step(Step& step, int ns, const int* ctx, const int* n_new, const int* table_offsets,
+               const int* page_ids, int q_heads, int kv_heads, int head_dim, int pool_pages,
+               const char** message) {
+  auto bad = [&](const char* m) {
+    if (message) *message = m;
+    return TGE_ERR_INVALID;
+  };
+  if (ns <= 0 || !ctx || !n_new || !table_offsets || !page_ids)
+    return bad("batch_plan: empty or incomplete description");
+  if (q_heads <= 0 || kv_heads <= 0 || q_heads % kv_heads != 0)
+    return bad("batch_plan: q_heads must be a multiple of kv_heads");
+  const int group = q_heads / kv_heads;
+  if (group > kPrefillRows)
+    return bad("batch_plan: more than 128 query heads per KV head");
+  if (table_offsets[0] != 0) return bad("batch_plan: table_offsets[0] must be 0");
+  const int n_entries = table_offsets[ns];
+  if (n_entries < 0) return bad("batch_plan: negative table size");
+
+  // Validate first: a failed plan leaves the step untouched.
+  int max_rows = 0;
+  for (int s = 0; s < ns; ++s) {
+    const int c = ctx[s], nn = n_new[s];
+    const int lo = table_offsets[s], hi = table_offsets[s + 1];
+    if (c < 0 || nn < 1) return bad("batch_plan: ctx must be >= 0 and n_new >= 1");
+    if (hi < lo || hi > n_entries) return bad("batch_plan: table_offsets must not decrease");
+    const long need = ((long)c + nn + 15) / 16;
+    if (hi - lo < need) return bad("batch_plan: block table shorter than the context");
+    for (long i = 0; i < need; ++i) {
+      const int id = page_ids[lo + i];
+      if (id < 0 || id >= pool_pages) return bad("batch_plan: page id outside the pool");
+    }
+    if ((long)nn * group > (1L << 30)) return bad("batch_plan: too many rows");
+    max_rows = std::max(max_rows, nn * group);
+  }
+
+  step.sessions.assign((std::size_t)ns, {});
+  step.rows.clear();
+  step.tables.assign(page_ids, page_ids + n_entries);
+  int q_row = 0;
+  for (int s = 0; s < ns; ++s) {
+    const int c = ctx[s], nn = n_new[s], lo = table_offsets[s];
+    step.sessions[(std::size_t)s] = SessionRec{c, nn, q_row, lo};
+    for (int j = 0; j < nn; ++j) {
+      const int pos = c + j;
+      step.rows.push_back(RowRec{page_ids[lo + pos / 16], pos % 16, pos});
+    }
+    q_row += nn;
+  }
+  step.kv_heads = kv_heads;
+  step.head_dim = head_dim;
+  step.q_heads = q_heads;
+  step.group = group;
+  step.pages = pool_pages;
+  step.max_rows = max_rows;
+  return TGE_OK;
+}
+
+bool decode_session(const Step& s, const SessionRec& r) { return r.n_new * s.group <= kMaxRows; }
+
+bool take_session(const Step& s, const SessionRec& r, int only) {
+  return only == 0 || (only == 1) == decode_session(s, r);
+}
+
+// Relative speed of the k-th workgroup that lands on a CU. Workgroups are
+// dispatched one per CU before a CU gets a second, and on a shared SIMD the
+// older wave wins issue, so equal page shares finish far apart (measured:
+// ~25 % slower for the second). Shares are weighted by rank^k.
+#ifndef TGE_DECODE_RANK_WEIGHT
+#define TGE_DECODE_RANK_WEIGHT 0.76
+#endif
+// Fixed cost of one unit of a share (start-up and merge), in pages.
+#ifndef TGE_DECODE_UNIT_COST
+#define TGE_DECODE_UNIT_COST 22
+#endif
+// At least 8 pages per workgroup: on small steps (one to four sessions
+// of 1k-8k positions) shorter chains win over fewer split merges down to
+// 8 pages (c1-c3: 5-7 % per layer-step against 16; 4 is slower again).
+#ifndef TGE_DECODE_MIN_PAGES
+#define TGE_DECODE_MIN_PAGES 8
+#endif
+
+void build_decode(const Step& b, Residency res, AttnLists& pl, int only) {
+  pl.work.clear();
+  pl.reduce.clear();
+  pl.wg_first.clear();
+  pl.parts = pl.max_splits = 0;
+  int max_rows = 0;
+  for (const auto& sr : b.sessions)
+    if (take_session(b, sr, only)) max_rows = std::max(max_rows, sr.n_new * b.group);
+  pl.row_groups = std::max(1, std::min(4, (max_rows + 15) / 16));
+
+  struct Seg {
+    int session, head, pages;
+  };
+  std::vector<Seg> segs;
+  long total = 0;
+  for (int s = 0; s < (int)b.sessions.size(); ++s) {
+    const SessionRec& sr = b.sessions[(std::size_t)s];
+    if (!take_session(b, sr, only)) continue;
+    const int pages = (sr.ctx + sr.n_new + 15) / 16;
+    for (int h = 0; h < b.kv_heads; ++h) segs.push_back(Seg{s, h, pages});
+    total += (long)pages * b.kv_heads;
+  }
+  const long g_eff = std::max<long>(
+      1, std::min<long>(res.groups, (total + TGE_DECODE_MIN_PAGES - 1) / TGE_DECODE_MIN_PAGES));
+  std::vector<double> w((std::size_t)g_eff);
+  double wrem = 0.0;
+  for (long g = 0; g < g_eff; ++g) {
+    w[(std::size_t)g] = std::pow(TGE_DECODE_RANK_WEIGHT, (double)(g / std::max(1, res.cus)));
+    wrem += w[(std::size_t)g];
+  }
+
+  // Cut the segments, end to end, into one share per workgroup. A share's
+  // cost is its pages plus TGE_DECODE_UNIT_COST per piece (the fixed cost
+  // of starting and merging a unit); each share gets the remaining cost in
+  // proportion to its rank weight, the last one takes what is left.
+  const double unit_cost = TGE_DECODE_UNIT_COST;
+  std::vector<int> seg_of;  // segment of each work item
+  long pages_rem = total, segs_rem = (long)segs.size();
+  std::size_t si = 0;
+  int pos = 0;
+  pl.wg_first.push_back(0);
+  for (long g = 0; g < g_eff && si < segs.size(); ++g) {
+    const bool last_wg = g + 1 == g_eff;
+    double target =
+        ((double)pages_rem + unit_cost * (double)(segs_rem + (g_eff - g))) * w[(std::size_t)g] / wrem;
+    wrem -= w[(std::size_t)g];
+    bool started = false;
+    while (si < segs.size()) {
+      const Seg& sg = segs[si];
+      const int left = sg.pages - pos;
+      int take = left;
+      if (!last_wg) {
+        const double room = target - unit_cost;
+        if (started && room < 1.0) break;
+        take = (int)std::min<double>(left, std::max(1.0, std::floor(room)));
+      }
+      const SessionRec& sr = b.sessions[(std::size_t)sg.session];
+      WorkRec it{};
+      it.session = sg.session;
+      it.kv_head = sg.head;
+      it.page_begin = pos;
+      it.page_end = pos + take;
+      it.part = -1;
+      it.row_begin = 0;
+      it.rows = sr.n_new * b.group;
+      it.rows_per_query = b.group;
+      it.head_base = sg.head * b.group;
+      it.ctx = sr.ctx;
+      it.q_row = sr.q_row;
+      it.table_off = sr.table_off;
+      pl.work.push_back(it);
+      seg_of.push_back((int)si);
+      started = true;
+      target -= take + unit_cost;
+      pos += take;
+      pages_rem -= take;
+      if (pos == sg.pages) {
+        ++si;
+        pos = 0;
+        --segs_rem;
+      }
+      if (!last_wg && target < unit_cost + 1.0) break;
+    }
+    pl.wg_first.push_back((int)pl.work.size());
+  }
+
+  // Segments cut into several items are merged by the split reduction.
+  for (std::size_t i = 0; i < pl.work.size();) {
+    std::size_t j = i + 1;
+    while (j < pl.work.size() && seg_of[j] == seg_of[i]) ++j;
+    const int n = (int)(j - i);
+    pl.max_splits = std::max(pl.max_splits, n);
+    if (n > 1) {
+      const WorkRec& w0 = pl.work[i];
+      ReduceRec r{};
+      r.session = w0.session;
+      r.row_begin = w0.row_begin;
+      r.rows = w0.rows;
+      r.rows_per_query = w0.rows_per_query;
+      r.head_base = w0.head_base;
+      r.first_part = pl.parts;
+      r.n_parts = n;
+      for (std::size_t k = i; k < j; ++k) pl.work[k].part = pl.parts++;
+      pl.reduce.push_back(r);
+    }
+    i = j;
+  }
+  pl.groups = (int)pl.wg_first.size() - 1;
+}
+
+namespace {
+
+// Splits [0, pages) into n nearly equal ranges and appends one unit each.
+void add_units(std::vector<WorkRec>& work, std::vector<ReduceRec>& red, int& parts,
+               int& max_splits, WorkRec base, int pages, int pps) {
+  const int n = std::max(1, (pages + pps - 1) / pps);
+  max_splits = std::max(max_splits, n);
+  if (n == 1) {
+    base.page_begin = 0;
+    base.page_end = pages;
+    base.part = -1;
+    work.push_back(base);
+    return;
+  }
+  const int chunk = (pages + n - 1) / n;
+  ReduceRec r{};
+  r.session = base.session;
+  r.row_begin = base.row_begin;
+  r.rows = base.rows;
+  r.rows_per_query = base.rows_per_query;
+  r.head_base = base.head_base;
+  r.first_part = parts;
+  r.n_parts = 0;
+  for (int b = 0; b < pages; b += chunk) {
+    WorkRec w = base;
+    w.page_begin = b;
+    w.page_end = std::min(pages, b + chunk);
+    w.part = parts++;
+    work.push_back(w);
+    ++r.n_parts;
+  }
+  red.push_back(r);
+}
+
+}  // namespace
+
+#ifndef TGE_PREFILL_MIN_SPLIT
+#define TGE_PREFILL_MIN_SPLIT 32
+#endif
+
+void build_prefill(const Step& b, int cus, AttnLists& pl, int only) {
+  pl.work.clear();
+  pl.reduce.clear();
+  pl.wg_first.clear();
+  pl.groups = 0;
+  pl.parts = pl.max_splits = 0;
+  pl.row_groups = kPrefillRows / 16;
+  const int tq = std::max(1, kPrefillRows / b.group);
+  // Page-split size: enough items for about two rounds of two workgroups
+  // on each compute unit, at least 32 pages (eight tiles of four).
+  long pages_total = 0;
+  for (const auto& sr : b.sessions) {
+    if (!take_session(b, sr, only)) continue;
+    for (int a = 0; a < sr.n_new; a += tq)
+      pages_total += (long)((sr.ctx + std::min(sr.n_new, a + tq) + 15) / 16) * b.kv_heads;
+  }
+  const long target_units = 2L * std::max(1, cus) * 2;
+  const int pps = (int)std::max<long>(TGE_PREFILL_MIN_SPLIT,
+                                      ((pages_total + target_units - 1) / target_units + 3) / 4 * 4);
+  for (int s = 0; s < (int)b.sessions.size(); ++s) {
+    const SessionRec& sr = b.sessions[(std::size_t)s];
+    if (!take_session(b, sr, only)) continue;
+    for (int h = 0; h < b.kv_heads; ++h) {
+      for (int a = 0; a < sr.n_new; a += tq) {
+        WorkRec w{};
+        w.session = s;
+        w.kv_head = h;
+        w.ctx = sr.ctx;
+        w.q_row = sr.q_row;
+        w.table_off = sr.table_off;
+        w.row_begin = a;
+        w.rows = std::min(tq, sr.n_new - a) * b.group;
+        w.rows_per_query = b.group;
+        w.head_base = h * b.group;
+        const int pages = (sr.ctx + a + std::min(tq, sr.n_new - a) + 15) / 16;
+        add_units(pl.work, pl.reduce, pl.parts, pl.max_splits, w, pages, pps);
+      }
+    }
+  }
+  // Longest items first (partial slots are fixed per item, so order is free).
+  std::stable_sort(pl.work.begin(), pl.work.end(), [](const WorkRec& x, const WorkRec& y) {
+    return x.page_end - x.page_begin > y.page_end - y.page_begin;
+  });
+  pl.groups = (int)pl.work.size();
+}
+
+std::size_t image_layout(const AttnLists& pl, std::size_t* off_reduce, std::size_t* off_first) {
+  const std::size_t wbytes = pl.work.size() * sizeof(WorkRec);
+  *off_reduce = align256(wbytes);
+  *off_first = align256(*off_reduce + pl.reduce.size() * sizeof(ReduceRec));
+  return *off_first + pl.wg_first.size() * sizeof(int);
+}
+
+void write_image(const AttnLists& pl, std::size_t off_reduce, std::size_t off_first, char* h) {
+  if (!pl.work.empty()) std::memcpy(h, pl.work.data(), pl.work.size() * sizeof(WorkRec));
+  if (!pl.reduce.empty())
+    std::memcpy(h + off_reduce, pl.reduce.data(), pl.reduce.size() * sizeof(ReduceRec));
+  if (!pl.wg_first.empty())
+    std::memcpy(h + off_first, pl.wg_first.data(), pl.wg_first.size() * sizeof(int));
+}
+
+}  // namespace tge::plan

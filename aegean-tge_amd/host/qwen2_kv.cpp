@@ -5,6 +5,7 @@
 #include "../csrc/tge_error.h"
 
 #include <algorithm>
+#include <functional>
 #include <memory>
 #include <stdexcept>
 #include <string>
@@ -33,6 +34,10 @@ Qwen2KvPath::Qwen2KvPath(const Qwen2KvConfig& config) : config_(config) {
   }
   if (config_.q_heads % config_.kv_heads != 0) {
     throw std::invalid_argument("Qwen2KvPath: q_heads must be a multiple of kv_heads");
+  }
+  if (config_.q_heads / config_.kv_heads > 128) {
+    // a block-prefill tile holds one query's whole head group (128 rows)
+    throw std::invalid_argument("Qwen2KvPath: more than 128 query heads per KV head");
   }
   if (config_.format == TGE_KV_I8 && (config_.kv_heads * config_.head_dim) % 32 != 0) {
     // qwen2.cpp:406-409: the i8 cache needs kv_dim to be a multiple of 32.
@@ -89,8 +94,7 @@ static int shared_in(const BlockTable& table, const std::vector<int>& list, int 
 
 void Qwen2KvPath::begin(const std::vector<Group>& groups, void* stream) {
   begun_ = false;
-  // Validate everything before touching the table, so a failed call leaves
-  // the model unchanged.
+  // Validate everything before touching the table.
   std::vector<int> need_pages(static_cast<std::size_t>(config_.sequences), 0);
   int extra = 0;
   for (const Group& g : groups) {
@@ -108,38 +112,70 @@ void Qwen2KvPath::begin(const std::vector<Group>& groups, void* stream) {
   }
   if (extra > table_->free_count()) throw std::runtime_error("BlockTable: table full");
 
+  // Tentative page lists: a written page still held by another sequence is
+  // replaced by a private copy (copy-on-write), and new pages are appended.
+  // Nothing is committed until the plan is uploaded and the copies are
+  // queued; on any failure the allocations are returned in reverse order,
+  // which restores the free list exactly, and the model is unchanged.
+  std::vector<std::vector<int>> lists;
+  std::vector<int> fresh;                 // allocated pages, in order
+  std::vector<std::pair<int, int>> cow;   // (shared page, its private copy)
   std::vector<int> ctx, n_new, offsets{0}, ids;
   int max_count = 0;
-  for (const Group& g : groups) {
-    auto& list = pages_[static_cast<std::size_t>(g.sequence)];
-    const int need = (g.start + g.count + kBlockTokens - 1) / kBlockTokens;
-    // Copy-on-write: a written page still held by another sequence is
-    // replaced by a private copy (all layers) before this step's append.
-    for (int k = g.start / kBlockTokens; k < need && k < static_cast<int>(list.size()); ++k) {
-      const int old = list[static_cast<std::size_t>(k)];
-      if (table_->refcount(old) > 1) {
-        const int fresh = table_->allocate();
-        check(tge_kv_copy_page(pool_, old, fresh, stream), "begin");
-        table_->release(old);
-        list[static_cast<std::size_t>(k)] = fresh;
+  try {
+    for (const Group& g : groups) {
+      std::vector<int> list = pages_[static_cast<std::size_t>(g.sequence)];
+      const int need = (g.start + g.count + kBlockTokens - 1) / kBlockTokens;
+      for (int k = g.start / kBlockTokens; k < need && k < static_cast<int>(list.size()); ++k) {
+        const int old = list[static_cast<std::size_t>(k)];
+        if (table_->refcount(old) > 1) {
+          const int copy = table_->allocate();
+          fresh.push_back(copy);
+          cow.emplace_back(old, copy);
+          list[static_cast<std::size_t>(k)] = copy;
+        }
       }
+      while (static_cast<int>(list.size()) < need) {
+        fresh.push_back(table_->allocate());
+        list.push_back(fresh.back());
+      }
+      ctx.push_back(g.start);
+      n_new.push_back(g.count);
+      ids.insert(ids.end(), list.begin(), list.end());
+      offsets.push_back(static_cast<int>(ids.size()));
+      max_count = std::max(max_count, g.count);
+      lists.push_back(std::move(list));
     }
-    while (static_cast<int>(list.size()) < need) list.push_back(table_->allocate());
-    length_[static_cast<std::size_t>(g.sequence)] = g.start + g.count;
-    ctx.push_back(g.start);
-    n_new.push_back(g.count);
-    ids.insert(ids.end(), list.begin(), list.end());
-    offsets.push_back(static_cast<int>(ids.size()));
-    max_count = std::max(max_count, g.count);
+    tge_batch_desc d{};
+    d.n_sessions = static_cast<int>(groups.size());
+    d.ctx = ctx.data();
+    d.n_new = n_new.data();
+    d.table_offsets = offsets.data();
+    d.page_ids = ids.data();
+    d.q_heads = config_.q_heads;
+    check(tge_batch_plan(batch_, pool_, &d, stream), "begin");
+    for (const auto& c : cow) check(tge_kv_copy_page(pool_, c.first, c.second, stream), "begin");
+  } catch (...) {
+    for (auto it = fresh.rbegin(); it != fresh.rend(); ++it) table_->release(*it);
+    throw;
   }
-  tge_batch_desc d{};
-  d.n_sessions = static_cast<int>(groups.size());
-  d.ctx = ctx.data();
-  d.n_new = n_new.data();
-  d.table_offsets = offsets.data();
-  d.page_ids = ids.data();
-  d.q_heads = config_.q_heads;
-  check(tge_batch_plan(batch_, pool_, &d, stream), "begin");
+
+  // Commit.
+  for (const auto& c : cow) table_->release(c.first);  // still held elsewhere
+  for (std::size_t i = 0; i < groups.size(); ++i) {
+    const Group& g = groups[i];
+    const std::size_t s = static_cast<std::size_t>(g.sequence);
+    pages_[s] = std::move(lists[i]);
+    length_[s] = g.start + g.count;
+    // A recorded page whose recorded rows this step rewrites in place no
+    // longer holds its recorded prefix.
+    const int need = (g.start + g.count + kBlockTokens - 1) / kBlockTokens;
+    for (int k = g.start / kBlockTokens; k < need; ++k) {
+      const int page = pages_[s][static_cast<std::size_t>(k)];
+      const auto it = prefix_.find(page);
+      if (it != prefix_.end() && k * kBlockTokens + it->second.count > g.start) drop_prefix(page);
+    }
+  }
   const int group = config_.q_heads / config_.kv_heads;
   // some session's rows exceed a decode unit: its attention runs on the
   // block-prefill kernel (tge_batch_attention picks per session)
@@ -249,32 +285,118 @@ void Qwen2KvPath::set_sparse_config(const SparseConfig& config) {
         "set_sparse_config");
 }
 
+void Qwen2KvPath::record_prefix(int block, int prev, const int* tokens, int count) {
+  auto it = prefix_.find(block);
+  if (it != prefix_.end() && it->second.prev != prev) {
+    auto& sib = children_[it->second.prev];
+    sib.erase(std::remove(sib.begin(), sib.end(), block), sib.end());
+    it = prefix_.end();
+    prefix_.erase(block);
+  }
+  if (it == prefix_.end()) {
+    it = prefix_.emplace(block, PrefixPage{}).first;
+    it->second.prev = prev;
+    children_[prev].push_back(block);
+  }
+  it->second.count = std::max(it->second.count, count);
+  std::copy(tokens, tokens + count, it->second.tokens);
+}
+
+void Qwen2KvPath::drop_prefix(int block) {
+  std::vector<int> todo{block};
+  while (!todo.empty()) {
+    const int b = todo.back();
+    todo.pop_back();
+    const auto it = prefix_.find(b);
+    if (it == prefix_.end()) continue;
+    auto& sib = children_[it->second.prev];
+    sib.erase(std::remove(sib.begin(), sib.end(), b), sib.end());
+    prefix_.erase(it);
+    if (table_->live(b)) table_->forget_prefix(b);
+    const auto ch = children_.find(b);
+    if (ch != children_.end()) {
+      todo.insert(todo.end(), ch->second.begin(), ch->second.end());
+      children_.erase(ch);
+    }
+  }
+}
+
+int Qwen2KvPath::match_prefix(const int* tokens, int count, std::vector<int>* chain) const {
+  // Longest chain of records spelling tokens[0, count). Several recorded
+  // pages may hold the same tokens after the same page (sequences that
+  // prefilled the same text separately) and continue differently, so every
+  // matching page is followed; a page always sits at the same position of
+  // the sequences holding it, so the best continuation after a page is
+  // memoised per page.
+  struct Best {
+    int len;   // tokens matched from the page's children on
+    int next;  // child taken (-1: none)
+  };
+  std::unordered_map<int, Best> memo;
+  auto run_of = [&](int block, int pos) {
+    const PrefixPage& r = prefix_.at(block);
+    const int lim = std::min(std::min(kBlockTokens, count - pos), r.count);
+    int run = 0;
+    while (run < lim && r.tokens[run] == tokens[pos + run]) ++run;
+    return run;
+  };
+  std::function<Best(int, int)> solve = [&](int prev, int pos) -> Best {
+    const auto m = memo.find(prev);
+    if (m != memo.end()) return m->second;
+    Best best{0, -1};
+    const auto ch = children_.find(prev);
+    if (ch != children_.end() && pos < count) {
+      for (int b : ch->second) {
+        const int run = run_of(b, pos);
+        if (run == 0) continue;
+        int len = run;
+        if (run == kBlockTokens && pos + kBlockTokens < count) len += solve(b, pos + run).len;
+        if (len > best.len) best = Best{len, b};
+      }
+    }
+    memo.emplace(prev, best);
+    return best;
+  };
+  const int total = solve(-1, 0).len;
+  if (chain) {
+    int prev = -1, pos = 0;
+    while (pos < total) {
+      const int b = memo.at(prev).next;
+      chain->push_back(b);
+      pos += run_of(b, pos);
+      prev = b;
+    }
+  }
+  return total;
+}
+
 int Qwen2KvPath::remember_prefix(int sequence, const int* tokens, int count) {
   check_sequence(sequence, "remember_prefix");
   if (count < 0 || (count > 0 && tokens == nullptr)) {
     throw std::runtime_error("remember_prefix: invalid tokens");
   }
   const auto& list = pages_[static_cast<std::size_t>(sequence)];
-  const int full = std::min(count, length_[static_cast<std::size_t>(sequence)]) / kBlockTokens;
+  const int n = std::min(count, length_[static_cast<std::size_t>(sequence)]);
   std::uint64_t h = BlockTable::hash_tokens(nullptr, 0);
-  for (int k = 0; k < full; ++k) {
-    h = BlockTable::hash_extend(h, tokens + k * kBlockTokens, kBlockTokens);
-    table_->remember_prefix(h, list[static_cast<std::size_t>(k)]);
+  int prev = -1;
+  for (int k = 0; k * kBlockTokens < n; ++k) {
+    const int m = std::min(kBlockTokens, n - k * kBlockTokens);
+    const int block = list[static_cast<std::size_t>(k)];
+    record_prefix(block, prev, tokens + k * kBlockTokens, m);
+    if (m == kBlockTokens) {
+      h = BlockTable::hash_extend(h, tokens + k * kBlockTokens, kBlockTokens);
+      table_->remember_prefix(h, block);
+    }
+    prev = block;
   }
-  return full;
+  return n;
 }
 
 int Qwen2KvPath::shared_prefix_len(const int* tokens, int count) const {
   if (count < 0 || (count > 0 && tokens == nullptr)) {
     throw std::runtime_error("shared_prefix_len: invalid tokens");
   }
-  std::uint64_t h = BlockTable::hash_tokens(nullptr, 0);
-  int k = 0;
-  for (; (k + 1) * kBlockTokens <= count; ++k) {
-    h = BlockTable::hash_extend(h, tokens + k * kBlockTokens, kBlockTokens);
-    if (table_->find_prefix(h) < 0) break;
-  }
-  return k * kBlockTokens;
+  return match_prefix(tokens, count, nullptr);
 }
 
 int Qwen2KvPath::attach_prefix(int sequence, const int* tokens, int count) {
@@ -286,18 +408,13 @@ int Qwen2KvPath::attach_prefix(int sequence, const int* tokens, int count) {
   if (!list.empty() || length_[static_cast<std::size_t>(sequence)] != 0) {
     throw std::runtime_error("attach_prefix: the sequence is not empty");
   }
-  std::uint64_t h = BlockTable::hash_tokens(nullptr, 0);
-  const int limit = std::min(count, config_.context);
-  for (int k = 0; (k + 1) * kBlockTokens <= limit; ++k) {
-    h = BlockTable::hash_extend(h, tokens + k * kBlockTokens, kBlockTokens);
-    const int block = table_->find_prefix(h);
-    if (block < 0) break;
-    table_->share(block);
-    list.push_back(block);
-  }
-  length_[static_cast<std::size_t>(sequence)] = static_cast<int>(list.size()) * kBlockTokens;
+  std::vector<int> chain;
+  const int matched = match_prefix(tokens, std::min(count, config_.context), &chain);
+  for (int block : chain) table_->share(block);
+  list = std::move(chain);
+  length_[static_cast<std::size_t>(sequence)] = matched;
   begun_ = false;
-  return length_[static_cast<std::size_t>(sequence)];
+  return matched;
 }
 
 void Qwen2KvPath::reset_cache(int sequence) {
@@ -306,7 +423,10 @@ void Qwen2KvPath::reset_cache(int sequence) {
     throw std::runtime_error("reset_cache: sequence outside the model");
   }
   auto& list = pages_[static_cast<std::size_t>(sequence)];
-  for (int id : list) table_->release(id);
+  for (int id : list) {
+    table_->release(id);
+    if (!table_->live(id)) drop_prefix(id);  // back on the free list
+  }
   list.clear();
   length_[static_cast<std::size_t>(sequence)] = 0;
   begun_ = false;

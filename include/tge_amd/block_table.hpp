@@ -12,6 +12,7 @@
 //     page drops the hash it was remembered under from the lookup (the
 //     page -> hash record itself is kept, as in the reference, :64-67);
 //   - every misuse throws std::runtime_error.
+// Two additions of this build (live, forget_prefix) serve the KV driver.
 // Single-threaded, like the reference.
 #pragma once
 
@@ -104,6 +105,20 @@ class BlockTable {
   int find_prefix(std::uint64_t hash) const {
     const auto it = owner_.find(hash);
     return it == owner_.end() ? -1 : it->second;
+  }
+
+  // Not in the reference table: whether a block is allocated, and dropping
+  // the prefix hash a block was remembered under (for a page whose rows are
+  // rewritten in place, so the hash no longer describes its contents).
+  bool live(int block) const {
+    return block >= 0 && block < capacity() && refs_[static_cast<std::size_t>(block)] > 0;
+  }
+  void forget_prefix(int block) {
+    const auto it = hash_of_.find(block);
+    if (it == hash_of_.end()) return;
+    const auto own = owner_.find(it->second);
+    if (own != owner_.end() && own->second == block) owner_.erase(own);
+    hash_of_.erase(it);
   }
 
  private:

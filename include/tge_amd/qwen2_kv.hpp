@@ -18,6 +18,7 @@
 #pragma once
 
 #include <memory>
+#include <unordered_map>
 #include <vector>
 
 #include "tge_amd/block_table.hpp"
@@ -91,16 +92,20 @@ class Qwen2KvPath {
   void set_sparse_config(const SparseConfig& config);
   const SparseConfig& sparse_config() const { return sparse_; }
 
-  // Shared prefixes over pages. Page k of a sequence is keyed by the hash of
-  // its tokens [0, 16(k+1)), so one hit covers every page before it.
-  // remember_prefix keys the sequence's full cached pages among the first
-  // `count` tokens (the populate step, qwen2.cpp:2388-2465); returns the
-  // pages keyed. shared_prefix_len is the token length of the longest keyed
-  // page chain `tokens` starts with (qwen2.cpp:1948-1971, whole pages).
-  // attach_prefix gives an empty sequence that chain by reference count
-  // (BlockTable::share; qwen2.cpp:1973-2026 copies rows instead) and
-  // returns its cached length. A step that writes into a page another
-  // sequence also holds copies the page first (copy-on-write).
+  // Shared prefixes over pages, matched token by token. remember_prefix
+  // records, for each cached page among the sequence's first `count`
+  // tokens, the tokens it holds (up to 16; the last page may be partial)
+  // and the page before it, so a chain of records spells out a prefix
+  // exactly (the populate step, qwen2.cpp:2388-2465); full pages are also
+  // keyed in the BlockTable under the hash of tokens [0, 16(k+1)). Returns
+  // the tokens recorded. shared_prefix_len is the longest run of tokens,
+  // from the first, that some recorded chain holds (qwen2.cpp:1948-1971):
+  // every token is compared, never a hash alone. attach_prefix gives an
+  // empty sequence that run by reference count (BlockTable::share;
+  // qwen2.cpp:1973-2026 copies rows instead), the last page possibly only
+  // in part, and returns its cached length. A step that writes into a page
+  // another sequence also holds copies the page first (copy-on-write); a
+  // step that rewrites recorded rows of a page in place drops its record.
   int remember_prefix(int sequence, const int* tokens, int count);
   int shared_prefix_len(const int* tokens, int count) const;
   int attach_prefix(int sequence, const int* tokens, int count);
@@ -128,8 +133,22 @@ class Qwen2KvPath {
     int start;
     int count;
   };
+  // One recorded page of a shared prefix: the tokens its first `count`
+  // rows hold and the recorded page before it (-1 for a chain's first).
+  struct PrefixPage {
+    int prev = -1;
+    int count = 0;
+    int tokens[kBlockTokens] = {};
+  };
   void check_sequence(int sequence, const char* who) const;
   void begin(const std::vector<Group>& groups, void* stream);
+  // Pages of the longest recorded chain matching `tokens`; returns the
+  // matched token count.
+  int match_prefix(const int* tokens, int count, std::vector<int>* chain) const;
+  void record_prefix(int block, int prev, const int* tokens, int count);
+  // Drops a page's record and, since their chains pass through it, the
+  // records of every page recorded after it.
+  void drop_prefix(int block);
 
   Qwen2KvConfig config_;
   std::unique_ptr<BlockTable> table_;
@@ -141,6 +160,8 @@ class Qwen2KvPath {
   bool prefill_ = false;
   bool begun_ = false;
   SparseConfig sparse_;
+  std::unordered_map<int, PrefixPage> prefix_;          // page -> record
+  std::unordered_map<int, std::vector<int>> children_;  // record's prev -> pages
 };
 
 }  // namespace tge::models

@@ -154,18 +154,23 @@ typedef struct {
   const int* n_new;         /* host [n_sessions], >= 1 */
   const int* table_offsets; /* host [n_sessions+1] */
   const int* page_ids;      /* host [table_offsets[n_sessions]] */
-  int q_heads;              /* multiple of the pool's kv_heads */
+  int q_heads;              /* multiple of the pool's kv_heads, at most 128
+                               query heads per KV head */
 } tge_batch_desc;
 
 int tge_batch_create(tge_batch** out);
 void tge_batch_destroy(tge_batch* batch);
 
 /* Validates the description against `pool`, builds the work lists and
- * uploads tables and plan (one host-to-device copy on `stream`). */
+ * uploads tables and plan (one host-to-device copy on `stream`). A failure
+ * leaves the batch unplanned; TGE_ERR_CAPACITY when device or pinned host
+ * memory runs out (a later, smaller plan allocates again). */
 int tge_batch_plan(tge_batch* batch, const tge_kv_pool* pool,
                    const tge_batch_desc* desc, void* stream);
 
-/* Plan statistics: total new-token rows, decode work items, splits. */
+/* Plan statistics: total new-token rows, decode work items and the largest
+ * number of splits of one (session, KV head); a plan whose rows exceed a
+ * decode unit reports 0 work items and 0 splits. */
 int tge_batch_info(const tge_batch* batch, int* rows, int* work_items,
                    int* max_splits);
 
@@ -382,21 +387,26 @@ int tge_qwen2_kv_set_sparse(tge_qwen2_kv* model, int enabled, int sink,
                             int window, int stride);
 
 /* Shared prefixes over pages (the BlockTable recipe of prefix sharing,
- * replacing the reference's four-slot snapshot table, qwen2.cpp:40-72).
- * A full page of a sequence is keyed by the hash of every token up to its
- * end (hash_tokens of tokens[0, 16(k+1)) for page k), so a hit on page k
- * implies the same tokens at the same positions for pages 0..k.
+ * replacing the reference's four-slot snapshot table, qwen2.cpp:40-72),
+ * matched token by token.
  *
- * remember_prefix: key the sequence's full, cached pages among the first
- * `count` tokens (the populate step, qwen2.cpp:2388-2465, without its
- * four-slot and 256-token caps).
- * shared_prefix_len: tokens of the longest remembered page chain that
- * `tokens` starts with (qwen2.cpp:1948-1971; whole pages here).
- * attach_prefix: an empty sequence takes that chain by reference count
- * (no copy; qwen2.cpp:1973-2026 copies rows) and is cached up to the
- * returned length; the caller prefills from there. A later step that
- * writes into a page another sequence still holds copies it first
- * (copy-on-write), so sharers never see each other's writes. */
+ * remember_prefix: record, for each cached page among the sequence's first
+ * `count` tokens, the tokens it holds (the last page may be partial) and
+ * the page before it (the populate step, qwen2.cpp:2388-2465, without its
+ * four-slot and 256-token caps); full pages are also keyed in the block
+ * table under hash_tokens of tokens[0, 16(k+1)). Returns the tokens
+ * recorded.
+ * shared_prefix_len: the longest run of tokens, from the first, that a
+ * recorded chain of pages holds (qwen2.cpp:1948-1971). Every token is
+ * compared; a hash alone never decides a match.
+ * attach_prefix: an empty sequence takes that run by reference count (no
+ * copy; qwen2.cpp:1973-2026 copies rows), its last page possibly in part,
+ * and is cached up to the returned length; the caller prefills from there.
+ * A later step that writes into a page another sequence still holds copies
+ * it first (copy-on-write), so sharers never see each other's writes; a
+ * step that rewrites recorded rows of a page in place drops the record of
+ * that page and of the pages recorded after it, and a page's record goes
+ * when its last holder releases it. */
 int tge_qwen2_kv_remember_prefix(tge_qwen2_kv* model, int sequence,
                                  const int* tokens, int count);
 int tge_qwen2_kv_shared_prefix_len(const tge_qwen2_kv* model, const int* tokens,

@@ -214,12 +214,15 @@ def pool_rows(md, layer, seq, count):
 
 
 def test_prefix_sharing_and_copy_on_write(gpu):
-    """Pages remembered under their token-prefix hashes are attached to a new
-    sequence by reference count (BlockTable share, block_table.hpp:52-111),
-    replacing the reference's copied prefix rows (qwen2.cpp:1948-2026). The
-    attached sequence appends after them; attention over the shared pages
-    equals attention over a privately filled copy bit for bit; a write into
-    a shared page copies it first, so the other holder's rows never change."""
+    """Shared prefixes matched token by token (shared_prefix_len,
+    qwen2.cpp:1948-1971): recorded pages are attached to a new sequence by
+    reference count (BlockTable share, block_table.hpp:52-111), the last
+    one possibly in part, replacing the reference's copied prefix rows
+    (qwen2.cpp:1973-2026). The attached sequence appends after them (its
+    first write copies the partly matched page); attention over the shared
+    pages equals attention over a privately filled copy bit for bit; a write
+    into a shared page copies it first, so the other holder's rows never
+    change."""
     say("driver prefix sharing")
     md = Model(2, 14, 2, 64, tk.KV_F16, sequences=4, pages=64, context=512, seed=6)
     tab = md.m.table()
@@ -228,42 +231,44 @@ def test_prefix_sharing_and_copy_on_write(gpu):
     md.m.begin_prefill(0, 0, 50)
     md.keep(0, 0, k0, v0)
     md.run_layers(None, k0, v0, attend=False)
-    assert md.m.remember_prefix(0, toks) == 3  # pages 0..2 are full (48 tokens)
-    assert md.m.shared_prefix_len(toks + [1, 2]) == 48
-    assert md.m.shared_prefix_len(toks[:40] + [7] * 10) == 32
-    assert md.m.shared_prefix_len(toks[:47]) == 32  # only whole pages are keyed
+    assert md.m.remember_prefix(0, toks) == 50  # every cached token, page 3 in part
+    assert md.m.shared_prefix_len(toks + [1, 2]) == 50
+    assert md.m.shared_prefix_len(toks[:40] + [7] * 10) == 40
+    assert md.m.shared_prefix_len(toks[:47]) == 47  # inside page 2
     assert md.m.shared_prefix_len([999] + toks) == 0
     p0 = md.m.pages(0)
 
-    # sequence 1 takes the 48-token chain, then prefills 20 tokens of its own
-    assert md.m.attach_prefix(1, toks + [5] * 20) == 48
-    assert md.m.pages(1) == p0[:3] and md.m.length(1) == 48
+    # sequence 1 takes a 47-token run (page 2 in part), then prefills 20 of its own
+    assert md.m.attach_prefix(1, toks[:47] + [5] * 20) == 47
+    assert md.m.pages(1) == p0[:3] and md.m.length(1) == 47
     assert [tab.refcount(p) for p in p0] == [2, 2, 2, 1]
     _, k1, v1 = md.rows(20)
-    md.m.begin_prefill(1, 48, 20)
+    md.m.begin_prefill(1, 47, 20)
     for l in range(md.layers):
-        md.k[(l, 1)] = np.concatenate([md.k[(l, 0)][:48], k1[l]])
-        md.v[(l, 1)] = np.concatenate([md.v[(l, 0)][:48], v1[l]])
+        md.k[(l, 1)] = np.concatenate([md.k[(l, 0)][:47], k1[l]])
+        md.v[(l, 1)] = np.concatenate([md.v[(l, 0)][:47], v1[l]])
     md.run_layers(None, k1, v1, attend=False)
-    assert md.m.pages(1)[:3] == p0[:3] and len(md.m.pages(1)) == 5
-    # sequence 2 holds the same 68 rows in private pages
+    p1 = md.m.pages(1)
+    assert p1[:2] == p0[:2] and p1[2] not in p0 and len(p1) == 5
+    assert [tab.refcount(p) for p in p0] == [2, 2, 1, 1]
+    # sequence 2 holds the same 67 rows in private pages
     k2 = [md.k[(l, 1)].copy() for l in range(md.layers)]
     v2 = [md.v[(l, 1)].copy() for l in range(md.layers)]
-    md.m.begin_prefill(2, 0, 68)
+    md.m.begin_prefill(2, 0, 67)
     md.keep(2, 0, k2, v2)
     md.run_layers(None, k2, v2, attend=False)
     assert not set(md.m.pages(2)) & set(p0)
 
     q, k, v = md.rows(1)
-    md.m.begin_forward(1, 68)
-    md.keep(1, 68, k, v)
+    md.m.begin_forward(1, 67)
+    md.keep(1, 67, k, v)
     out1 = md.run_layers(q, k, v)
-    md.m.begin_forward(2, 68)
-    md.keep(2, 68, k, v)
+    md.m.begin_forward(2, 67)
+    md.keep(2, 67, k, v)
     out2 = md.run_layers(q, k, v)
     for l in range(md.layers):
         assert np.array_equal(out1[l], out2[l]), f"shared vs private pages differ, layer {l}"
-        assert_attention_close(out1[l], md.oracle(l, 1, q[l], 68), f"shared prefix layer {l}")
+        assert_attention_close(out1[l], md.oracle(l, 1, q[l], 67), f"shared prefix layer {l}")
 
     # copy-on-write: sequence 1 verifies drafts at 20..21, inside shared page 1
     q, k, v = md.rows(2)
@@ -273,8 +278,8 @@ def test_prefix_sharing_and_copy_on_write(gpu):
     for l in range(md.layers):
         assert_attention_close(out[l], md.oracle(l, 1, q[l], 20), f"after copy layer {l}")
     p1 = md.m.pages(1)
-    assert p1[0] == p0[0] and p1[2] == p0[2] and p1[1] not in p0
-    assert [tab.refcount(p) for p in p0] == [2, 1, 2, 1]
+    assert p1[0] == p0[0] and p1[1] not in p0
+    assert [tab.refcount(p) for p in p0] == [2, 1, 1, 1]
     for l in range(md.layers):
         gk, gv = pool_rows(md, l, 0, 50)
         assert np.array_equal(gk, O.float_to_half(md.k[(l, 0)])), f"sequence 0 K changed, layer {l}"
@@ -287,10 +292,10 @@ def test_prefix_sharing_and_copy_on_write(gpu):
     with pytest.raises(tk.TgeError) as e:
         md.m.attach_prefix(1, toks)
     assert e.value.status == tk.ERR_RUNTIME
-    # releases: keyed pages stay found while some sequence holds them
+    # releases: recorded pages stay found while some sequence holds them
     md.m.reset(0)
-    assert [tab.refcount(p) for p in (p0[0], p0[2])] == [1, 1]
-    assert md.m.shared_prefix_len(toks) == 16  # page 1's key went with its last holder
+    assert tab.refcount(p0[0]) == 1
+    assert md.m.shared_prefix_len(toks) == 16  # page 1's record went with its last holder
     md.m.reset(1)
     assert md.m.shared_prefix_len(toks) == 0
     md.close()
