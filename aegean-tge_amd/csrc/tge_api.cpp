@@ -668,6 +668,147 @@ int tge_batch_attention(const tge_batch* b, const tge_kv_pool* p, int layer, con
   return run_attention(b, p, layer, q, out, stream, b->mix_decode, true);
 }
 
+}  // extern "C"
+
+// ---------------------------------------------------------------------------
+// Decode attention that allocates nothing (tge_decode_attention_static): the
+// step's plan image and its split-K partials live in `scratch`, one array
+// per device that the library holds until the process ends. In host code
+// `scratch` names a host-side stand-in, never device memory: every host use
+// goes through the device address hipGetSymbolAddress returns for the
+// current device (static_scratch below).
+// ---------------------------------------------------------------------------
+namespace {
+
+constexpr size_t kStaticImageBytes = size_t(4) << 20;    // sessions | tables | work lists
+constexpr size_t kStaticScratchBytes = size_t(32) << 20;  // image, then partials
+constexpr int kStaticDevices = 64;
+
+__device__ __align__(256) char scratch[kStaticScratchBytes];
+
+struct StaticScratch {
+  std::once_flag once;
+  char* ptr = nullptr;  // device address of `scratch` on this device
+  std::string error;
+};
+StaticScratch g_static[kStaticDevices];
+
+// The device address of this device's `scratch`, looked up once per device
+// with that device current.
+int static_scratch(char** out) {
+  int dev = 0;
+  TGE_HIP(hipGetDevice(&dev));
+  if (dev < 0 || dev >= kStaticDevices)
+    return fail(TGE_ERR_DEVICE, "decode_attention_static: device index beyond the table");
+  StaticScratch& s = g_static[dev];
+  std::call_once(s.once, [&s] {
+    void* p = nullptr;
+    const hipError_t e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    if (e == hipSuccess && p) {
+      s.ptr = static_cast<char*>(p);
+    } else {
+      s.error = std::string("hipGetSymbolAddress(scratch): ") + hipGetErrorString(e);
+    }
+  });
+  if (!s.ptr) return fail(TGE_ERR_DEVICE, s.error);
+  *out = s.ptr;
+  return TGE_OK;
+}
+
+}  // namespace
+
+extern "C" {
+
+int tge_decode_attention_static(const tge_batch_desc* d, const tge_kv_pool* p, int layer,
+                                const float* q, float* out, void* stream) {
+  if (!d || !p || !q || !out) return fail(TGE_ERR_INVALID, "decode_attention_static: null argument");
+  if (layer < 0 || layer >= p->desc.layers)
+    return fail(TGE_ERR_INVALID, "decode_attention_static: layer out of range");
+  int s = backend_ready();
+  if (s != TGE_OK) return fail(s, "decode_attention_static: backend unavailable");
+  // Host-side plan in per-thread buffers that keep their capacity.
+  thread_local tge::plan::Step step;
+  thread_local tge::plan::AttnLists lists;
+  thread_local std::vector<char> image;
+  const int hd = p->desc.head_dim;
+  const char* msg = nullptr;
+  s = tge::plan::build_step(step, d->n_sessions, d->ctx, d->n_new, d->table_offsets, d->page_ids,
+                            d->q_heads, p->desc.kv_heads, hd, p->desc.pages, &msg);
+  if (s != TGE_OK) return fail(s, std::string(msg ? msg : "invalid description"));
+  if (step.max_rows > tge::kMaxRows)
+    return fail(TGE_ERR_INVALID, "decode_attention_static: n_new * group exceeds 64 rows");
+  const int f = p->desc.format, sf32 = p->desc.scale_format == TGE_SCALE_F32;
+  const int rg = std::max(1, std::min(4, (step.max_rows + 15) / 16));
+  tge::plan::build_decode(step, resident_groups(f, sf32, hd, rg), lists, 0);
+
+  // scratch: [ sessions | tables | work | reduce | wg_first ] in the first
+  // kStaticImageBytes, then part_o [parts][rows_cap][hd] and part_ml
+  // [parts][rows_cap][2].
+  const size_t o_tab = align_up(step.sessions.size() * sizeof(tge::SessionRec));
+  const size_t o_work = align_up(o_tab + step.tables.size() * sizeof(int));
+  size_t l_red = 0, l_first = 0;
+  const size_t l_total = tge::plan::image_layout(lists, &l_red, &l_first);
+  const size_t total = o_work + l_total;
+  const size_t rows_cap = 16 * (size_t)lists.row_groups;
+  const size_t parts = (size_t)std::max(lists.parts, 1);
+  const size_t part_floats = parts * rows_cap * hd;
+  const size_t part_bytes = (part_floats + parts * rows_cap * 2) * sizeof(float);
+  if (total > kStaticImageBytes)
+    return fail(TGE_ERR_CAPACITY, "decode_attention_static: the step's plan (" +
+                                      std::to_string(total) + " B) exceeds the static limit of " +
+                                      std::to_string(kStaticImageBytes) + " B");
+  if (part_bytes > kStaticScratchBytes - kStaticImageBytes)
+    return fail(TGE_ERR_CAPACITY, "decode_attention_static: the step's split-K partials (" +
+                                      std::to_string(part_bytes) +
+                                      " B) exceed the static limit of " +
+                                      std::to_string(kStaticScratchBytes - kStaticImageBytes) +
+                                      " B");
+  char* base = nullptr;
+  s = static_scratch(&base);
+  if (s != TGE_OK) return s;
+
+  if (image.size() < total) image.resize(total);
+  std::memcpy(image.data(), step.sessions.data(), step.sessions.size() * sizeof(tge::SessionRec));
+  if (!step.tables.empty())
+    std::memcpy(image.data() + o_tab, step.tables.data(), step.tables.size() * sizeof(int));
+  tge::plan::write_image(lists, l_red, l_first, image.data() + o_work);
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  // From pageable memory: the copy is ordered after the stream's earlier
+  // work, and the host buffer may be reused once the call returns.
+  TGE_HIP(hipMemcpyAsync(base, image.data(), total, hipMemcpyHostToDevice, st));
+
+  tge_kv_layer_view v{};
+  tge_kv_pool_layer(p, layer, &v);
+  tge::AttnParams a{};
+  a.pool = v.k;
+  a.block_bytes = (uint32_t)p->geom.block_bytes;
+  a.sessions = reinterpret_cast<const tge::SessionRec*>(base);
+  a.work = reinterpret_cast<const tge::WorkRec*>(base + o_work);
+  a.wg_first = reinterpret_cast<const int*>(base + o_work + l_first);
+  a.tables = reinterpret_cast<const int*>(base + o_tab);
+  a.q = q;
+  a.out = out;
+  a.part_o = reinterpret_cast<float*>(base + kStaticImageBytes);
+  a.part_ml = a.part_o + part_floats;
+  a.rows_cap = (int)rows_cap;
+  a.kv_heads = step.kv_heads;
+  a.q_heads = step.q_heads;
+  a.scale_log2 = (float)(1.4426950408889634 / std::sqrt((double)hd));
+  TGE_HIP(tge::launch_decode(f, sf32, hd, lists.row_groups, lists.groups, a, st));
+  if (!lists.reduce.empty()) {
+    tge::ReduceParams r{};
+    r.sessions = a.sessions;
+    r.items = reinterpret_cast<const tge::ReduceRec*>(base + o_work + l_red);
+    r.part_o = a.part_o;
+    r.part_ml = a.part_ml;
+    r.out = out;
+    r.rows_cap = a.rows_cap;
+    r.q_heads = step.q_heads;
+    TGE_HIP(tge::launch_reduce(hd, (int)lists.reduce.size(), lists.max_splits, r, st));
+  }
+  return TGE_OK;
+}
+
 int tge_kv_gather(const tge_batch* b, const tge_kv_pool* p, int layer, int session,
                   int count, void* k_rows, void* v_rows, void* k_scales, void* v_scales,
                   void* stream) {

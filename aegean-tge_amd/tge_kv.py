@@ -113,6 +113,7 @@ SIGNATURES = [
     ("tge_batch_kernel_times", _I, [_VP, _PI, C.POINTER(C.c_float), C.POINTER(C.c_float)]),
     ("tge_kv_append", _I, [_VP, _VP, _I, _VP, _VP, _VP]),
     ("tge_decode_attention", _I, [_VP, _VP, _I, _VP, _VP, _VP]),
+    ("tge_decode_attention_static", _I, [C.POINTER(BatchDesc), _VP, _I, _VP, _VP, _VP]),
     ("tge_prefill_attention", _I, [_VP, _VP, _I, _VP, _VP, _VP]),
     ("tge_kv_gather", _I, [_VP, _VP, _I, _I, _I, _VP, _VP, _VP, _VP, _VP]),
     ("tge_block_table_create", _I, [_I, _I, C.POINTER(_VP)]),
@@ -429,6 +430,29 @@ def batch_info(handle):
     r, w, s = C.c_int(), C.c_int(), C.c_int()
     check(lib().tge_batch_info(handle, C.byref(r), C.byref(w), C.byref(s)), "batch_info")
     return r.value, w.value, s.value
+
+
+def batch_desc(sessions, q_heads):
+    """A tge_batch_desc over `sessions` (Session records) and the int arrays
+    it points to (keep them alive while the descriptor is used)."""
+    ctx = [s.ctx for s in sessions]
+    n_new = [s.n_new for s in sessions]
+    offs = [0]
+    ids = []
+    for s in sessions:
+        ids.extend(int(p) for p in s.pages)
+        offs.append(len(ids))
+    keep = (_ints(ctx), _ints(n_new), _ints(offs), _ints(ids))
+    return BatchDesc(len(sessions), keep[0], keep[1], keep[2], keep[3], q_heads), keep
+
+
+def decode_attention_static(pool, sessions, q_heads, layer, q, out, stream=None):
+    """tge_decode_attention_static: plan and decode one step with no
+    allocation (plan and partials in the library's static device array)."""
+    d, keep = batch_desc(sessions, q_heads)
+    check(lib().tge_decode_attention_static(C.byref(d), pool.h, layer, q.ptr, out.ptr, stream),
+          "decode_attention_static")
+    del keep
 
 
 class Batch:

@@ -228,6 +228,25 @@ int tge_decode_attention(const tge_batch* batch, const tge_kv_pool* pool,
                          int layer, const float* q, float* out, void* stream);
 
 /*
+ * tge_decode_attention for callers that cannot allocate memory (code under
+ * HIP graph capture, tight serving loops, harnesses that forbid hipMalloc).
+ * No counterpart in the reference. It plans the step from `desc` on the
+ * host (the decode plan of tge_batch_plan; dense attention, no sparse
+ * subset) and runs the same kernels, so its output equals that of
+ * tge_batch_plan + tge_decode_attention on the same description bit for
+ * bit. The plan image and the split-K partials live in a static device
+ * array of 32 MiB per GPU, held until the process ends: at most 4 MiB of
+ * plan (sessions, block tables, work lists) and 28 MiB of partials; a
+ * larger step returns TGE_ERR_CAPACITY before anything runs. It calls no
+ * device or pinned-host allocation. Every call on one GPU shares that
+ * array, so calls that overlap on one GPU (different streams, or threads)
+ * race; calls on one stream are ordered. q, out and the pool are as in
+ * tge_decode_attention; the K/V rows of the step must already be appended.
+ */
+int tge_decode_attention_static(const tge_batch_desc* desc, const tge_kv_pool* pool,
+                                int layer, const float* q, float* out, void* stream);
+
+/*
  * Chunked-prefill block attention (attention_block_head_avx2,
  * attention_avx2.cpp:660-864): each new token attends causally to every
  * prior page and the chunk itself, on f16 MFMA (Q rounded to f16 as in

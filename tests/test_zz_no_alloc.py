@@ -1,0 +1,82 @@
+"""tge_decode_attention_static (the entry point that allocates nothing)
+against tge_batch_plan + tge_decode_attention, through the C ABI, on the GPU.
+
+Two calls in a row, the second on a smaller step, must each equal the
+allocating entry point bit for bit (same plan, same kernels), and match the
+oracle within the attention tolerance. A step whose plan exceeds the static
+array is refused with TGE_ERR_CAPACITY before anything runs, and a later
+call still works.
+"""
+import sys
+
+import numpy as np
+import pytest
+
+import tge_kv as tk
+from _paged import PagedCase
+from _util import assert_attention_close, bits
+
+pytestmark = pytest.mark.gpu
+
+
+def say(*a):
+    print(*a, flush=True)
+    sys.stdout.flush()
+
+
+def run_both(case):
+    """(static output, allocating output) of the case's decode step."""
+    got_alloc, b = case.step()  # appends the step's rows, then decodes
+    dq = tk.DeviceArray.from_numpy(case.q)
+    out = tk.DeviceArray(case.q.shape, np.float32)
+    tk.hip().memset(out.ptr, 0xFF, out.nbytes)  # NaN bits: every row must be written
+    tk.decode_attention_static(case.pool, case.sessions(True), case.qh, 0, dq, out)
+    tk.hip().sync()
+    got_static = out.numpy()
+    info = b.info()
+    for a in (dq, out):
+        a.close()
+    b.close()
+    return got_static, got_alloc, info
+
+
+def test_static_decode_equals_allocating_decode(gpu):
+    # first call: c5-shaped (int8, f16 scales, 4-query verify) with split-K
+    say("static decode: first call (c5 shape, 6 sessions up to 9000 positions)")
+    big = PagedCase(28, 4, 128, tk.KV_I8, [9000, 40, 3000, 1, 1500, 700], 4, seed=71,
+                    outlier_frac=0.01)
+    big.fill()
+    s1, a1, info1 = run_both(big)
+    assert info1[2] > 1, f"expected split-K partials in the first call: {info1}"
+    assert np.array_equal(bits(s1), bits(a1)), "static and allocating decode differ (call 1)"
+    assert_attention_close(s1, big.oracle_out(), "static decode call 1")
+    # second call, smaller: the array keeps the first call's contents
+    say("static decode: second, smaller call (c1 shape)")
+    small = PagedCase(14, 2, 64, tk.KV_F16, [300, 17], 1, seed=72)
+    small.fill()
+    s2, a2, _ = run_both(small)
+    assert np.array_equal(bits(s2), bits(a2)), "static and allocating decode differ (call 2)"
+    assert_attention_close(s2, small.oracle_out(), "static decode call 2")
+    small.close()
+    big.close()
+
+
+def test_static_decode_rejects_oversized_plans(gpu):
+    say("static decode: oversized plan")
+    pool = tk.KvPool(1, 4, 2, 64, tk.KV_F16)
+    q = tk.DeviceArray((1, 14 * 64), np.float32).zero()
+    out = tk.DeviceArray((1, 14 * 64), np.float32).zero()
+    # a 17.6M-position session: its block table alone (4.4 MB) exceeds the
+    # 4 MiB plan area (page ids may repeat; nothing is launched)
+    ctx = 1_100_000 * 16 - 1
+    with pytest.raises(tk.TgeError) as e:
+        tk.decode_attention_static(pool, [tk.Session(ctx, 1, [0] * 1_100_000)], 14, 0, q, out)
+    assert e.value.status == tk.ERR_CAPACITY, e.value
+    assert "static limit" in tk.lib().tge_last_error().decode()
+    # still usable afterwards
+    tk.decode_attention_static(pool, [tk.Session(20, 1, [1, 2])], 14, 0, q, out)
+    tk.hip().sync()
+    assert np.all(np.isfinite(out.numpy()))
+    for a in (q, out):
+        a.close()
+    pool.close()
