@@ -178,30 +178,35 @@ __device__ __forceinline__ void fetch_page(char* slot, const char* block, uint32
 }
 
 // Read a landed page back into registers (the lane's own chunk and its
-// group's scales).
-template <int FMT, bool SF32, int D>
-__device__ __forceinline__ void read_page(PageRegs<FMT, SF32, D>& r, const char* slot, int lane,
+// group's scales): the K half (K codes and scales) and the V half, so a
+// consumer can hold only the half it is using.
+template <int FMT, bool SF32, int D, bool V>
+__device__ __forceinline__ void read_half(PageRegs<FMT, SF32, D>& r, const char* slot, int lane,
                                           int grp) {
   using RG = Ring<FMT, SF32, D>;
   using R = PageRegs<FMT, SF32, D>;
+  uint32_t* c = V ? r.v : r.k;
+  uint32_t* sc = V ? r.vs : r.ks;
 #pragma unroll
   for (int i = 0; i < RG::PIECES; ++i) {
-    const u32x4_t k = *reinterpret_cast<const u32x4_t*>(slot + i * 1024 + 16 * lane);
-    const u32x4_t v = *reinterpret_cast<const u32x4_t*>(slot + RG::KV_BYTES + i * 1024 + 16 * lane);
-    r.k[4 * i] = k.x; r.k[4 * i + 1] = k.y; r.k[4 * i + 2] = k.z; r.k[4 * i + 3] = k.w;
-    r.v[4 * i] = v.x; r.v[4 * i + 1] = v.y; r.v[4 * i + 2] = v.z; r.v[4 * i + 3] = v.w;
+    const u32x4_t x = *reinterpret_cast<const u32x4_t*>(slot + (V ? RG::KV_BYTES : 0) + i * 1024 + 16 * lane);
+    c[4 * i] = x.x; c[4 * i + 1] = x.y; c[4 * i + 2] = x.z; c[4 * i + 3] = x.w;
   }
   if constexpr (FMT == kI8) {
-    const char* sk = slot + 2 * RG::KV_BYTES + grp * R::SW * 4;
-    const char* sv = sk + RG::SC_BYTES;
+    const char* ss = slot + 2 * RG::KV_BYTES + grp * R::SW * 4 + (V ? RG::SC_BYTES : 0);
 #pragma unroll
     for (int i = 0; i < R::SW / 4; ++i) {
-      const u32x4_t a = *reinterpret_cast<const u32x4_t*>(sk + 16 * i);
-      const u32x4_t b = *reinterpret_cast<const u32x4_t*>(sv + 16 * i);
-      r.ks[4 * i] = a.x; r.ks[4 * i + 1] = a.y; r.ks[4 * i + 2] = a.z; r.ks[4 * i + 3] = a.w;
-      r.vs[4 * i] = b.x; r.vs[4 * i + 1] = b.y; r.vs[4 * i + 2] = b.z; r.vs[4 * i + 3] = b.w;
+      const u32x4_t a = *reinterpret_cast<const u32x4_t*>(ss + 16 * i);
+      sc[4 * i] = a.x; sc[4 * i + 1] = a.y; sc[4 * i + 2] = a.z; sc[4 * i + 3] = a.w;
     }
   }
+}
+
+template <int FMT, bool SF32, int D>
+__device__ __forceinline__ void read_page(PageRegs<FMT, SF32, D>& r, const char* slot, int lane,
+                                          int grp) {
+  read_half<FMT, SF32, D, false>(r, slot, lane, grp);
+  read_half<FMT, SF32, D, true>(r, slot, lane, grp);
 }
 
 // s_waitcnt vmcnt(n) (other counters untouched), n <= 63.
@@ -426,6 +431,32 @@ struct Unit {
   template <bool SPARSE, class QF>
   __device__ __forceinline__ void consume_with(const Regs& r, int pi, int grp, bool masked,
                                                const QF& qf) {
+    half4_t pw[NRG];
+    score_phase<SPARSE>(r, pi, grp, masked, qf, pw);
+    value_phase(r, pw);
+  }
+
+  // The same for a page still in its LDS slot: the K half is read for the
+  // scores and the V half only after the softmax, so the two halves are
+  // never held at once (fewer live registers per wave).
+  // `after_k` runs once the K half's reads are issued.
+  template <bool SPARSE, class QF, class HOOK>
+  __device__ __forceinline__ void consume_slot(const char* slot, int lane, int pi, int grp,
+                                               bool masked, const QF& qf, const HOOK& after_k) {
+    Regs r;
+    read_half<FMT, SF32, D, false>(r, slot, lane, grp);
+    after_k();
+    half4_t pw[NRG];
+    score_phase<SPARSE>(r, pi, grp, masked, qf, pw);
+    read_half<FMT, SF32, D, true>(r, slot, lane, grp);
+    value_phase(r, pw);
+  }
+
+  // Scores of one page (K half of r), online softmax; the f16 weights of
+  // the page's 16 positions per row go to pw.
+  template <bool SPARSE, class QF>
+  __device__ __forceinline__ void score_phase(const Regs& r, int pi, int grp, bool masked,
+                                              const QF& qf, half4_t (&pw)[NRG]) {
     float4_t sacc[NRG];
 #pragma unroll
     for (int rg = 0; rg < NRG; ++rg) sacc[rg] = float4_t{0, 0, 0, 0};
@@ -450,7 +481,6 @@ struct Unit {
 
     const bool sp = SPARSE && sparse_page(pi);
     const int ph = sp ? sparse_phase(pi * 16 + 4 * grp) : 0;
-    half4_t pw[NRG];
 #pragma unroll
     for (int rg = 0; rg < NRG; ++rg) {
       sacc[rg] -= base[rg];  // exact: base is an integer
@@ -484,7 +514,10 @@ struct Unit {
       const half4_t ones = {(_Float16)1.0f, (_Float16)1.0f, (_Float16)1.0f, (_Float16)1.0f};
       l4[rg] = MFMA16x16x16(ones, pw[rg], l4[rg]);
     }
+  }
 
+  // Value accumulation of one page (V half of r) with the weights pw.
+  __device__ __forceinline__ void value_phase(const Regs& r, const half4_t (&pw)[NRG]) {
 #pragma unroll
     for (int pp = 0; pp < NP; ++pp) {
       half4_t va[2];
@@ -537,8 +570,19 @@ constexpr int kLdsBytes = 160 * 1024;  // LDS of one CU (gfx950)
 #ifndef TGE_DECODE_WAVES
 #define TGE_DECODE_WAVES 4
 #endif
+// Waves per SIMD of the dense decode kernel. A plain LDS-DMA ring over the
+// c5 block pattern streams ~5.95 TB/s with three (twelve waves per CU)
+// against ~5.4 with two, and the dense kernel fits the 168 registers three
+// allow; but the whole kernel measured the same at three (132.4 against
+// 131.5 us per c5 launch: the extra speed goes to cross-XCD imbalance that
+// changes from launch to launch) while cutting a third more split partials.
+// The static sparse variant stays at two in any case (its extra per-row
+// state would spill at three).
 #ifndef TGE_DECODE_WPE
 #define TGE_DECODE_WPE 2
+#endif
+#ifndef TGE_DECODE_WPE_SPARSE
+#define TGE_DECODE_WPE_SPARSE 2
 #endif
 #ifndef TGE_DECODE_MAX_SLOTS
 #define TGE_DECODE_MAX_SLOTS 4
@@ -547,8 +591,9 @@ constexpr int kLdsBytes = 160 * 1024;  // LDS of one CU (gfx950)
 // Launch shape of a decode variant: W waves per workgroup at WPE waves per
 // SIMD (PER_CU = 4*WPE/W workgroups per CU), NB ring slots per wave, and the
 // Q^T operands of up to MAXU units resident in LDS.
-template <int FMT, bool SF32, int D, int NRG>
+template <int FMT, bool SF32, int D, int NRG, bool SP = false>
 struct DecodeCfg {
+  static constexpr int WANT = SP ? TGE_DECODE_WPE_SPARSE : TGE_DECODE_WPE;
   static constexpr int SLOT = Ring<FMT, SF32, D>::SLOT;
   static constexpr int ROWS = 16 * NRG;
   static constexpr int QBYTES = NRG * (D / 32) * 64 * 16;  // one unit's Q^T operands (f16)
@@ -562,9 +607,9 @@ struct DecodeCfg {
   // configured shape, or eight waves at two per SIMD when its rings do not
   // fit (f16 pages at head_dim 128).
   static constexpr bool kBig = NRG > 2;
-  static constexpr bool kFits = nb_fit(TGE_DECODE_WAVES, TGE_DECODE_WPE) >= 2;
+  static constexpr bool kFits = nb_fit(TGE_DECODE_WAVES, WANT) >= 2;
   static constexpr int W = kBig ? 4 : (kFits ? TGE_DECODE_WAVES : 8);
-  static constexpr int WPE = kBig ? 1 : (kFits ? TGE_DECODE_WPE : 2);
+  static constexpr int WPE = kBig ? 1 : (kFits ? WANT : 2);
   static constexpr int PER_CU = 4 * WPE / W > 1 ? 4 * WPE / W : 1;  // workgroups per CU
   static constexpr int LDS = kLdsBytes / PER_CU - 256;             // one workgroup's share
   static constexpr int NB = nb_fit(W, WPE) > TGE_DECODE_MAX_SLOTS ? TGE_DECODE_MAX_SLOTS : nb_fit(W, WPE);
@@ -575,9 +620,9 @@ struct DecodeCfg {
   static_assert(8 * (D + 4) * 4 <= SLOT, "merge staging fits a slot");
 };
 
-template <int FMT, bool SF32, int D, int NRG>
+template <int FMT, bool SF32, int D, int NRG, bool SP>
 struct DecodeShared {
-  using C = DecodeCfg<FMT, SF32, D, NRG>;
+  using C = DecodeCfg<FMT, SF32, D, NRG, SP>;
   static constexpr int ROWS = 16 * NRG;
   static constexpr int MERGE_FLOATS = 2 * C::W * ROWS + 2 * ROWS + C::W;
   alignas(16) char ring[C::W * C::NB * C::SLOT];
@@ -642,11 +687,11 @@ struct PageFifo {
   __device__ __forceinline__ int front() const { return t[0]; }
 };
 
-template <int FMT, bool SF32, int D, int NRG, int W, int WPE>
+template <int FMT, bool SF32, int D, int NRG, int W, int WPE, bool SP>
 __global__ __launch_bounds__(64 * W) __attribute__((amdgpu_waves_per_eu(WPE, WPE)))
 void paged_decode_kernel(AttnParams p) {
-  using CFG = DecodeCfg<FMT, SF32, D, NRG>;
-  using SH = DecodeShared<FMT, SF32, D, NRG>;
+  using CFG = DecodeCfg<FMT, SF32, D, NRG, SP>;
+  using SH = DecodeShared<FMT, SF32, D, NRG, SP>;
   using U = Unit<FMT, SF32, D, NRG>;
   using Regs = typename U::Regs;
   using RG = Ring<FMT, SF32, D>;
@@ -702,6 +747,45 @@ void paged_decode_kernel(AttnParams p) {
       sh.q[idx] = h;
     }
   };
+  // The same at kernel start, with every load of the table issued before
+  // any is used (one memory round trip instead of one per pass); rows past
+  // a unit's end read its row 0 (always present) and store zeros.
+  auto fill_q_start = [&](int from) __attribute__((always_inline)) -> void {
+    constexpr int TOTAL = MAXU * QUNIT;
+    constexpr int PER = (TOTAL + 64 * W - 1) / (64 * W);
+    float4 qa[PER], qb[PER];
+    bool ok[PER];
+#pragma unroll
+    for (int k = 0; k < PER; ++k) {
+      const int idx = threadIdx.x + k * 64 * W;
+      const int l = idx & 63;
+      const int blk = __builtin_amdgcn_readfirstlane(idx >> 6);
+      const int pp = blk % NP;
+      const int rg = (blk / NP) % NRG;
+      const int it = from + blk / (NP * NRG);
+      const bool in = idx < TOTAL && it < last;
+      const WorkRec w = load_work(work + (in ? it : from));
+      const int r = rg * 16 + (l & 15);
+      ok[k] = in && r < w.rows;
+      const int rr = ok[k] ? r : 0;
+      const int qi = w.row_begin + rr / w.rows_per_query;
+      const int head = w.head_base + rr % w.rows_per_query;
+      const float* qp = p.q + (size_t)(w.q_row + qi) * q_stride + (size_t)head * D + 32 * pp + 4 * (l >> 4);
+      qa[k] = *reinterpret_cast<const float4*>(qp);
+      qb[k] = *reinterpret_cast<const float4*>(qp + 16);
+    }
+#pragma unroll
+    for (int k = 0; k < PER; ++k) {
+      const int idx = threadIdx.x + k * 64 * W;
+      if (idx < TOTAL) {
+        const float c = p.scale_log2;
+        const float4 a = qa[k], b = qb[k];
+        const half8_t h = {(_Float16)(a.x * c), (_Float16)(a.y * c), (_Float16)(a.z * c), (_Float16)(a.w * c),
+                           (_Float16)(b.x * c), (_Float16)(b.y * c), (_Float16)(b.z * c), (_Float16)(b.w * c)};
+        sh.q[idx] = ok[k] ? h : half8_t{};
+      }
+    }
+  };
 
   // ---- issue side: this wave's next page, its block, its fetch -------------
   // Cursor over the share's units: unit `ik` covers share pages
@@ -723,7 +807,7 @@ void paged_decode_kernel(AttnParams p) {
   // unit's smallest span). The waves split the kept ordinals round-robin
   // (wave w takes w, w+W, ...), so a periodic skip pattern never leaves
   // one wave all the work.
-  const bool skipping = p.sp_stride > 16;
+  const bool skipping = SP && p.sp_stride > 16;
   int ka0 = 0, kna = 0, kk0 = 0, knm = 0, kc0 = 0, knc = 0;  // A start/count, M first k/count, C
   auto kept_geometry = [&](const WorkRec& w) __attribute__((always_inline)) -> void {
     const int pb = w.page_begin, pe = w.page_end;
@@ -929,9 +1013,8 @@ void paged_decode_kernel(AttnParams p) {
   };
 
   // ---- the page loop -----------------------------------------------------------
-  fill_q(qfirst);
-  reset_unit();
-  __syncthreads();  // the Q table is written
+  // The first pages are requested before the Q table is filled, so the
+  // table's loads and the ring's first fetches share one memory round trip.
   request();
   PageFifo<NB> fifo;
   int head = 0, count = 0;
@@ -946,6 +1029,9 @@ void paged_decode_kernel(AttnParams p) {
       }
     }
   }
+  fill_q_start(qfirst);
+  reset_unit();
+  __syncthreads();  // the Q table is written
   // Close every unit that ends before this wave's next page (all of them
   // once the share is exhausted). Called with a free ring slot.
   auto close_units = [&]() __attribute__((always_inline)) -> void {
@@ -969,17 +1055,19 @@ void paged_decode_kernel(AttnParams p) {
       wait_vmcnt<0>();
     }
     const int g = fifo.front();
-    Regs r;
-    read_page<FMT, SF32, D>(r, ring + head * RG::SLOT, lane, grp);
-    // The next page id is read through the scalar cache only now, after the
-    // page's LDS reads have completed (they share the lgkm counter), so its
-    // latency hides behind this page's math instead of stalling the wave.
-    lgkm_wait_all();
-    if (gn >= 0) request();
     const int pi = cw.page_begin + (g - cbase);
     const half8_t* qt = sh.q + (ck - qfirst) * QUNIT + lane;
-    u.template consume_with<true>(r, pi, grp, pi >= unmasked,
-                   [&](int rg, int pp) __attribute__((always_inline)) { return qt[(rg * NP + pp) * 64]; });
+    u.template consume_slot<SP>(
+        ring + head * RG::SLOT, lane, pi, grp, pi >= unmasked,
+        [&](int rg, int pp) __attribute__((always_inline)) { return qt[(rg * NP + pp) * 64]; },
+        [&]() __attribute__((always_inline)) {
+          // The next page id is read through the scalar cache only now,
+          // after the K half's LDS reads have completed (they share the lgkm
+          // counter), so its latency hides behind this page's math instead
+          // of stalling the wave.
+          lgkm_wait_all();
+          if (gn >= 0) request();
+        });
     head = head + 1 == NB ? 0 : head + 1;
     --count;
     fifo.pop();
@@ -1246,9 +1334,14 @@ hipError_t launch_decode_d(int row_groups, int n_groups, const AttnParams& p, hi
   switch (row_groups) {
 #define TGE_DEC(n)                                                                          \
   case n: {                                                                                 \
-    using C = DecodeCfg<FMT, SF32, D, n>;                                                   \
-    hipLaunchKernelGGL((paged_decode_kernel<FMT, SF32, D, n, C::W, C::WPE>),           \
-                       dim3((unsigned)n_groups), dim3(64 * C::W), 0, stream, p);            \
+    using C = DecodeCfg<FMT, SF32, D, n, false>;                                            \
+    using CS = DecodeCfg<FMT, SF32, D, n, true>;                                            \
+    if (p.sp_stride > 0)                                                                    \
+      hipLaunchKernelGGL((paged_decode_kernel<FMT, SF32, D, n, CS::W, CS::WPE, true>),      \
+                         dim3((unsigned)n_groups), dim3(64 * CS::W), 0, stream, p);         \
+    else                                                                                    \
+      hipLaunchKernelGGL((paged_decode_kernel<FMT, SF32, D, n, C::W, C::WPE, false>),       \
+                         dim3((unsigned)n_groups), dim3(64 * C::W), 0, stream, p);          \
     break;                                                                                  \
   }
     TGE_DEC(1)
@@ -1263,15 +1356,20 @@ hipError_t launch_decode_d(int row_groups, int n_groups, const AttnParams& p, hi
 }
 
 template <int FMT, bool SF32, int D>
-int decode_blocks_d(int row_groups) {
+int decode_blocks_d(int row_groups, bool sparse) {
   int n = 0;
   hipError_t e = hipErrorInvalidValue;
   switch (row_groups) {
 #define TGE_DOCC(r)                                                                        \
   case r: {                                                                                \
-    using C = DecodeCfg<FMT, SF32, D, r>;                                                  \
-    e = hipOccupancyMaxActiveBlocksPerMultiprocessor(                                      \
-        &n, paged_decode_kernel<FMT, SF32, D, r, C::W, C::WPE>, 64 * C::W, 0);             \
+    using C = DecodeCfg<FMT, SF32, D, r, false>;                                           \
+    using CS = DecodeCfg<FMT, SF32, D, r, true>;                                           \
+    e = sparse ? hipOccupancyMaxActiveBlocksPerMultiprocessor(                             \
+                     &n, paged_decode_kernel<FMT, SF32, D, r, CS::W, CS::WPE, true>,       \
+                     64 * CS::W, 0)                                                        \
+               : hipOccupancyMaxActiveBlocksPerMultiprocessor(                             \
+                     &n, paged_decode_kernel<FMT, SF32, D, r, C::W, C::WPE, false>,        \
+                     64 * C::W, 0);                                                        \
     break;                                                                                 \
   }
     TGE_DOCC(1)
@@ -1303,14 +1401,16 @@ hipError_t launch_decode(int format, int scale_f32, int head_dim, int row_groups
   return hipErrorInvalidValue;
 }
 
-int decode_blocks_per_cu(int format, int scale_f32, int head_dim, int row_groups) {
+int decode_blocks_per_cu(int format, int scale_f32, int head_dim, int row_groups, bool sparse) {
   if (format == kF16) {
-    return head_dim == 64 ? decode_blocks_d<kF16, false, 64>(row_groups)
-                          : decode_blocks_d<kF16, false, 128>(row_groups);
+    return head_dim == 64 ? decode_blocks_d<kF16, false, 64>(row_groups, sparse)
+                          : decode_blocks_d<kF16, false, 128>(row_groups, sparse);
   }
   if (head_dim == 64)
-    return scale_f32 ? decode_blocks_d<kI8, true, 64>(row_groups) : decode_blocks_d<kI8, false, 64>(row_groups);
-  return scale_f32 ? decode_blocks_d<kI8, true, 128>(row_groups) : decode_blocks_d<kI8, false, 128>(row_groups);
+    return scale_f32 ? decode_blocks_d<kI8, true, 64>(row_groups, sparse)
+                     : decode_blocks_d<kI8, false, 64>(row_groups, sparse);
+  return scale_f32 ? decode_blocks_d<kI8, true, 128>(row_groups, sparse)
+                   : decode_blocks_d<kI8, false, 128>(row_groups, sparse);
 }
 
 template <int FMT, bool SF32, int D>

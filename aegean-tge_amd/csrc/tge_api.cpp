@@ -127,6 +127,7 @@ HipMem g_mem;
 struct AttnPlan {
   tge::plan::AttnLists lists;
   bool built = false;
+  bool sparse = false;  // decode lists balanced for the static sparse kernel
   tge::plan::Staged image;  // work | reduce | wg_first
   size_t off_reduce = 0;
   size_t off_first = 0;
@@ -330,19 +331,38 @@ int device_cus() {
 
 // Resident workgroups of a decode variant on this device (cached): the
 // compute units times what the occupancy query allows per unit.
-tge::plan::Residency resident_groups(int format, int scale_f32, int head_dim, int row_groups) {
+tge::plan::Residency resident_groups(int format, int scale_f32, int head_dim, int row_groups,
+                                     bool sparse) {
   static std::mutex mu;
   static std::vector<std::pair<int, tge::plan::Residency>> cache;  // key -> residency
-  const int key = ((format * 2 + scale_f32) * 256 + head_dim) * 8 + row_groups;
+  const int key = (((format * 2 + scale_f32) * 256 + head_dim) * 8 + row_groups) * 2 + sparse;
   std::lock_guard<std::mutex> lock(mu);
   for (const auto& kv : cache)
     if (kv.first == key) return kv.second;
   const int cus = device_cus();
-  int per_cu = tge::decode_blocks_per_cu(format, scale_f32, head_dim, row_groups);
+  int per_cu = tge::decode_blocks_per_cu(format, scale_f32, head_dim, row_groups, sparse);
   if (per_cu <= 0) per_cu = 1;
   const tge::plan::Residency r{per_cu * cus, cus};
   cache.emplace_back(key, r);
   return r;
+}
+
+// Builds and uploads a decode plan over the sessions `only` selects
+// (0 all, 1 those a decode unit holds), balanced for the decode kernel the
+// batch's current sparse setting launches.
+int build_decode_plan(tge_batch* b, const tge_kv_pool* p, AttnPlan& pl, int only, hipStream_t st) {
+  int max_rows = 0;
+  for (const auto& sr : b->step.sessions)
+    if (tge::plan::take_session(b->step, sr, only))
+      max_rows = std::max(max_rows, sr.n_new * b->step.group);
+  const int rg = std::max(1, std::min(4, (max_rows + 15) / 16));
+  const bool sparse = b->sp_stride > 0;
+  tge::plan::build_decode(b->step,
+                          resident_groups(p->desc.format, p->desc.scale_format == TGE_SCALE_F32,
+                                          b->step.head_dim, rg, sparse),
+                          pl.lists, only);
+  pl.sparse = sparse;
+  return upload_plan(pl, b->step.head_dim, st);
 }
 
 }  // namespace
@@ -379,11 +399,7 @@ int tge_batch_plan(tge_batch* b, const tge_kv_pool* pool, const tge_batch_desc* 
   // Decode lists are built eagerly when the rows fit a decode unit (the
   // common case: one upload per step serves every layer).
   if (st.max_rows <= tge::kMaxRows) {
-    const int rg = std::max(1, std::min(4, (st.max_rows + 15) / 16));
-    tge::plan::build_decode(
-        st, resident_groups(pool->desc.format, pool->desc.scale_format == TGE_SCALE_F32, hd, rg),
-        b->decode.lists, 0);
-    s = upload_plan(b->decode, hd, hs);
+    s = build_decode_plan(b, pool, b->decode, 0, hs);
     if (s != TGE_OK) return s;
   }
   b->planned = true;
@@ -615,6 +631,12 @@ int tge_decode_attention(const tge_batch* b, const tge_kv_pool* p, int layer,
   if (!q || !out) return fail(TGE_ERR_INVALID, "decode_attention: null q/out");
   if (!b->decode.built)
     return fail(TGE_ERR_INVALID, "decode_attention: n_new * group exceeds 64 rows");
+  if (b->decode.sparse != (b->sp_stride > 0)) {
+    // the sparse setting changed after planning: rebalance for its kernel
+    s = build_decode_plan(const_cast<tge_batch*>(b), p, const_cast<tge_batch*>(b)->decode, 0,
+                          static_cast<hipStream_t>(stream));
+    if (s != TGE_OK) return s;
+  }
   return run_attention(b, p, layer, q, out, stream, b->decode, true);
 }
 
@@ -645,16 +667,9 @@ int tge_batch_attention(const tge_batch* b, const tge_kv_pool* p, int layer, con
   if (n_pf == 0) return tge_decode_attention(b, p, layer, q, out, stream);
   if (n_dec == 0) return tge_prefill_attention(b, p, layer, q, out, stream);
   hipStream_t st = static_cast<hipStream_t>(stream);
-  if (!mb->mix_built) {
+  if (!mb->mix_built || mb->mix_decode.sparse != (b->sp_stride > 0)) {
     // Built on first use after each plan, reused by every layer.
-    int max_rows = 0;
-    for (const auto& sr : b->step.sessions)
-      if (tge::plan::decode_session(b->step, sr)) max_rows = std::max(max_rows, sr.n_new * b->step.group);
-    const int rg = std::max(1, std::min(4, (max_rows + 15) / 16));
-    tge::plan::build_decode(mb->step, resident_groups(p->desc.format, p->desc.scale_format == TGE_SCALE_F32,
-                                     b->step.head_dim, rg),
-                 mb->mix_decode.lists, 1);
-    s = upload_plan(mb->mix_decode, b->step.head_dim, st);
+    s = build_decode_plan(mb, p, mb->mix_decode, 1, st);
     if (s != TGE_OK) return s;
     tge::plan::build_prefill(mb->step, device_cus(), mb->mix_prefill.lists, 2);
     s = upload_plan(mb->mix_prefill, b->step.head_dim, st);
@@ -739,7 +754,7 @@ int tge_decode_attention_static(const tge_batch_desc* d, const tge_kv_pool* p, i
     return fail(TGE_ERR_INVALID, "decode_attention_static: n_new * group exceeds 64 rows");
   const int f = p->desc.format, sf32 = p->desc.scale_format == TGE_SCALE_F32;
   const int rg = std::max(1, std::min(4, (step.max_rows + 15) / 16));
-  tge::plan::build_decode(step, resident_groups(f, sf32, hd, rg), lists, 0);
+  tge::plan::build_decode(step, resident_groups(f, sf32, hd, rg, false), lists, 0);
 
   // scratch: [ sessions | tables | work | reduce | wg_first ] in the first
   // kStaticImageBytes, then part_o [parts][rows_cap][hd] and part_ml

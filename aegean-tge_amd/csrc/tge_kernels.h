@@ -86,8 +86,9 @@ hipError_t launch_decode(int format, int scale_f32, int head_dim, int row_groups
 // Block prefill: one workgroup per work item (tiles of up to 128 rows).
 hipError_t launch_prefill(int format, int scale_f32, int head_dim, int n_units,
                           const AttnParams& p, hipStream_t stream);
-// Resident decode workgroups per CU.
-int decode_blocks_per_cu(int format, int scale_f32, int head_dim, int row_groups);
+// Resident decode workgroups per CU (of the static sparse variant when
+// `sparse`).
+int decode_blocks_per_cu(int format, int scale_f32, int head_dim, int row_groups, bool sparse);
 hipError_t launch_reduce(int head_dim, int n_items, int max_parts, const ReduceParams& p,
                          hipStream_t stream);
 

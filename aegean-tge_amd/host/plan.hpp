@@ -91,7 +91,8 @@ struct AttnLists {
   int max_splits = 0;
 };
 
-// Resident workgroups of the decode launch and the device's compute units.
+// Resident workgroups of the decode launch and the device's compute units;
+// workgroup g is the (g / cus)-th to land on its compute unit.
 struct Residency {
   int groups;
   int cus;

@@ -17,7 +17,10 @@ roofline = the paged attention kernel alone (the dominant kernel; the split
 merge kernel is timed beside it): the last step's decode attention replayed
 over all layers, each kernel bracketed by HIP events that the library records
 on the launch stream (tge_batch_set_profiling). traffic = HBM bytes per
-dispatch from the committed rocprofv3 counter summary for this workload. cpu_baseline = the reference's own AVX2 attention kernel
+dispatch: the committed rocprofv3 counter summary for this workload gives
+traffic per algorithmic byte, scaled to this run's spans (the source is
+stated in the line). measured_copy_peak = device-to-device copy GB/s on this
+GPU, beside the 8 TB/s spec peak. cpu_baseline = the reference's own AVX2 attention kernel
 (oracle/_ref, built from the reference sources) under the reference's
 forward_batch schedule, on a bounded sample of the same workload.
 The other four configurations are measured briefly and reported under
@@ -54,6 +57,48 @@ METRIC = ("paged-KV decode attention: achieved HBM GB/s (% of peak), "
 
 def log(*a):
     print(*a, file=sys.stderr, flush=True)
+
+
+# CPU threads one GPU's job may use on the GPU box (its CPU share), whatever
+# the host reports.
+CPU_SHARE = 16
+
+
+def host_cores():
+    """(logical, physical) cores this process may run on: the affinity set,
+    and the distinct (package, core) pairs among it."""
+    cpus = sorted(os.sched_getaffinity(0)) if hasattr(os, "sched_getaffinity") else \
+        list(range(os.cpu_count() or 1))
+    phys = set()
+    for c in cpus:
+        base = f"/sys/devices/system/cpu/cpu{c}/topology"
+        try:
+            with open(f"{base}/physical_package_id") as f:
+                pkg = f.read().strip()
+            with open(f"{base}/core_id") as f:
+                core = f.read().strip()
+            phys.add((pkg, core))
+        except OSError:
+            phys.add(("?", str(c)))
+    return len(cpus), max(1, len(phys))
+
+
+def decode_threads():
+    """The reference's decode rule: one worker per physical core
+    (resolve_decode_threads, dispatch.cpp:77-94), within the CPU share."""
+    return min(CPU_SHARE, host_cores()[1])
+
+
+def prefill_threads():
+    """The reference's default pool: every logical core
+    (default_thread_count, thread_pool.cpp:337-340), within the CPU share."""
+    return min(CPU_SHARE, host_cores()[0])
+
+
+def cores_fields(threads, rule):
+    logical, physical = host_cores()
+    return {"cores": threads, "host_logical_cores": logical, "host_physical_cores": physical,
+            "thread_rule": rule}
 
 
 def parse():
@@ -523,7 +568,7 @@ def cpu_baseline_c5(synth, cfg, seconds):
     if ref is None:
         return None
     sh = cfg.shape
-    threads = min(16, os.cpu_count() or 1)
+    threads = decode_threads()
     rng = np.random.default_rng(cfg.seed + 5)
     sample = sorted(rng.choice(len(cfg.contexts), 16, replace=False))
     n_q = cfg.n_new
@@ -568,7 +613,8 @@ def cpu_baseline_c5(synth, cfg, seconds):
     return {
         "value": alg / per / 1e9,
         "unit": "GB/s",
-        "cores": threads,
+        **cores_fields(threads, "decode: one thread per physical core (dispatch.cpp:77-94), "
+                                f"at most the GPU's CPU share of {CPU_SHARE}"),
         "kind": "reference",
         "sample": (f"reference attention_head_avx2 (oracle/_ref, built from the reference "
                    f"sources) under the forward_batch schedule (qwen2.cpp:1705-1747), "
@@ -580,12 +626,11 @@ def cpu_baseline_c5(synth, cfg, seconds):
     }
 
 
-def _ref_team(seconds):
+def _ref_team(seconds, threads):
     import oracle as O
     ref = O.ref()
     if ref is None or seconds <= 0:
         return None, None, 0
-    threads = min(16, os.cpu_count() or 1)
     return O, ref, threads
 
 
@@ -608,7 +653,7 @@ def cpu_baseline_decode(synth, cfg, seconds):
     and head). Every session sits at its context + half the decode steps
     (the run's mean span); the reference's flat cache, its own f32 int8
     scales. Attention only (the one-row store per session is a copy)."""
-    O, ref, threads = _ref_team(seconds)
+    O, ref, threads = _ref_team(seconds, decode_threads())
     if ref is None:
         return None
     sh = cfg.shape
@@ -658,7 +703,8 @@ def cpu_baseline_decode(synth, cfg, seconds):
     return {
         "value": alg / per / 1e9,
         "unit": "GB/s",
-        "cores": threads,
+        **cores_fields(threads, "decode: one thread per physical core (dispatch.cpp:77-94), "
+                                f"at most the GPU's CPU share of {CPU_SHARE}"),
         "kind": "reference",
         "us_per_layer_step": 1e6 * per,
         "sample": (f"reference {'attention_group_avx2 + attention_head_avx2' if n == 1 else 'attention_head_avx2'} "
@@ -672,7 +718,7 @@ def cpu_baseline_prefill(synth, cfg, seconds):
     qwen2.cpp:1524-1571: attention_block_head_avx2, one task per query head)
     for each causal chunk of the c4 prompt over a flat f16 cache, on its own
     AVX2 kernel (oracle/_ref)."""
-    O, ref, threads = _ref_team(seconds)
+    O, ref, threads = _ref_team(seconds, prefill_threads())
     if ref is None:
         return None
     sh = cfg.shape
@@ -701,7 +747,8 @@ def cpu_baseline_prefill(synth, cfg, seconds):
     return {
         "value": flops / sum(per_chunk) / 1e12,
         "unit": "TFLOP/s",
-        "cores": threads,
+        **cores_fields(threads, "prefill: every logical core (thread_pool.cpp:337-340), "
+                                f"at most the GPU's CPU share of {CPU_SHARE}"),
         "kind": "reference",
         "us_per_layer_chunk": [1e6 * t for t in per_chunk],
         "prompt_ms_est": 1e3 * sum(per_chunk) * sh.layers,
@@ -712,19 +759,49 @@ def cpu_baseline_prefill(synth, cfg, seconds):
     }
 
 
-def measured_traffic(workload):
-    """HBM bytes per dispatch of the paged attention kernel on this workload,
-    from the committed rocprofv3 counter summary (FETCH_SIZE and WRITE_SIZE
-    per dispatch, each scaled by what the counter reads for a copy of known
-    size), or None when no summary covers the workload."""
+def measured_traffic(workload, algorithmic_bytes):
+    """HBM bytes per dispatch of the paged attention kernel at this run's
+    algorithmic bytes, and where the figure comes from: the committed
+    rocprofv3 counter summary of this workload (FETCH_SIZE and WRITE_SIZE per
+    dispatch, each scaled by what the counter reads for a copy of known
+    size) gives traffic per algorithmic byte, which scales to this run's
+    spans. (None, None) when no summary covers the workload."""
     path = os.path.join(ROOT, "profiles", "paged_decode_kernel_c5_traffic.json")
     if not os.path.exists(path):
-        return None
+        return None, None
     with open(path) as f:
         t = json.load(f)
-    if t.get("workload") != workload:
-        return None
-    return t.get("traffic_bytes_per_dispatch")
+    if t.get("workload") != workload or not t.get("traffic_over_algorithmic"):
+        return None, None
+    ratio = float(t["traffic_over_algorithmic"])
+    source = (f"rocprofv3 FETCH_SIZE + WRITE_SIZE per dispatch of this workload "
+              f"(profiles/paged_decode_kernel_c5_traffic.json: {t['traffic_bytes_per_dispatch']} B "
+              f"at {t['algorithmic_bytes_per_dispatch']} algorithmic B, ratio {ratio:.4f}) "
+              f"times this run's algorithmic bytes")
+    return int(round(ratio * algorithmic_bytes)), source
+
+
+def copy_peak(nbytes=1 << 30, reps=5):
+    """Read + write GB/s of device-to-device copies of 1 GiB on this GPU
+    (the runtime's copy kernel; best of `reps`): the measured peak the
+    roofline fraction is also quoted against."""
+    import tge_kv as tk
+    hip = tk.hip()
+    src, dst = hip.malloc(nbytes), hip.malloc(nbytes)
+    hip.memset(src, 1, nbytes)
+    hip.sync()
+    e0, e1 = hip.event(), hip.event()
+    best = None
+    for _ in range(reps + 1):
+        hip.record(e0)
+        hip.ok(hip.h.hipMemcpyAsync(C.c_void_p(dst), C.c_void_p(src), nbytes, hip.D2D, None),
+               "hipMemcpyAsync D2D")
+        hip.record(e1)
+        ms = hip.elapsed_ms(e0, e1)
+        best = ms if best is None else min(best, ms)
+    hip.free(src)
+    hip.free(dst)
+    return 2 * nbytes / (best * 1e-3) / 1e9
 
 
 def calibrate_copy(nbytes=1 << 30, reps=3):
@@ -796,6 +873,21 @@ def main():
     if args.only and args.only != "c5":
         print(json.dumps({args.only: others[args.only]}))
         return
+    copy_gbs = copy_peak()
+    log(f"[bench] device-to-device copy: {copy_gbs:.0f} GB/s read + write")
+    if args.others and not args.only and not args.fragment_c5:
+        # c5 on a fragmented pool (free list shuffled before the sessions
+        # allocate, so no session's pages are adjacent), a shorter run
+        fcfg = synth.configs()["c5"]
+        fcfg.fragmented = True
+        log(f"[bench] c5 fragmented: {fcfg.note} (fragmented pool)")
+        fb = DecodeBench(tk, synth, fcfg, 2 + 12)
+        fr = fb.run(12, 2, 2)
+        fb.model.close()
+        fr["pool"] = "fragmented (free list shuffled before the sessions allocate)"
+        fr["frac_attn_kernel"] = fr["attn_kernel_gbs"] / HBM_PEAK_GBS
+        others["c5_fragmented"] = fr
+        log(f"[bench] c5 fragmented: {json.dumps(fr)}")
     cfg = cfgs["c5"]
     if args.fragment_c5:
         cfg.fragmented = True
@@ -809,6 +901,7 @@ def main():
     if args.cpu:
         cpu = cpu_baseline_c5(synth, cfg, args.cpu_seconds)
         log(f"[bench] cpu baseline: {json.dumps(cpu)}")
+    traffic, traffic_source = measured_traffic(WORKLOAD_C5, r["attn_bytes_per_launch"])
     line = {
         "metric": METRIC,
         "value": round(r["gbs"], 2),
@@ -847,9 +940,12 @@ def main():
             "peak": HBM_PEAK_GBS,
             "unit": "GB/s",
             "frac": round(r["attn_kernel_gbs"] / HBM_PEAK_GBS, 4),
-            "traffic": measured_traffic(WORKLOAD_C5),
+            "traffic": traffic,
+            "traffic_source": traffic_source,
             "kernel_us": round(r["attn_kernel_us"], 3),
             "algorithmic_bytes": r["attn_bytes_per_launch"],
+            "measured_copy_peak": round(copy_gbs, 1),
+            "frac_of_measured_copy_peak": round(r["attn_kernel_gbs"] / copy_gbs, 4),
         },
         "cpu_baseline": cpu,
         "configs": others,
