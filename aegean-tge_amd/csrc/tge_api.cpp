@@ -140,10 +140,27 @@ struct AttnPlan {
   }
 };
 
+// A small decode step in one launch (paged_step_kernel): its records, the
+// split partials and the per-segment arrival counters (zero between
+// launches: each launch's last piece of a segment resets its counter).
+struct StepPlan {
+  tge::plan::StepLists lists;
+  bool built = false;
+  tge::plan::Staged image;
+  tge::plan::Scratch part_o, part_ml, counters;
+  ~StepPlan() {
+    image.release(g_mem);
+    part_o.release(g_mem);
+    part_ml.release(g_mem);
+    counters.release(g_mem);
+  }
+};
+
 }  // namespace
 
 struct tge_batch {
   tge::plan::Step step;  // host copy of the plan
+  StepPlan small;        // one-launch decode steps (tge_decode_step)
   bool planned = false;
   AttnPlan decode, prefill;
   // Mixed steps (tge_batch_attention): the decode kernel over the sessions
@@ -367,6 +384,38 @@ int build_decode_plan(tge_batch* b, const tge_kv_pool* p, AttnPlan& pl, int only
 
 }  // namespace
 
+namespace {
+
+// The one-launch lists of a small decode step, uploaded with their partial
+// and counter buffers (counters zeroed when allocated).
+int upload_step_plan(tge_batch* b, const tge_kv_pool* pool, hipStream_t st) {
+  StepPlan& sp = b->small;
+  sp.built = false;
+  if (!tge::plan::build_step_lists(b->step, pool->desc.format == TGE_KV_I8,
+                                   pool->desc.scale_format == TGE_SCALE_F32, sp.lists))
+    return TGE_OK;
+  const auto& L = sp.lists;
+  const size_t bytes = L.recs.size() * sizeof(tge::StepRec);
+  int s = sp.image.upload(g_mem, bytes, st, [&](char* h) {
+    std::memcpy(h, L.recs.data(), bytes);
+  });
+  if (s != TGE_OK) return s;
+  const size_t rows_cap = 16 * (size_t)L.row_groups;
+  const size_t parts = (size_t)std::max(L.parts, 1);
+  s = sp.part_o.reserve(g_mem, parts * rows_cap * b->step.head_dim * sizeof(float), st);
+  if (s == TGE_OK) s = sp.part_ml.reserve(g_mem, parts * rows_cap * 2 * sizeof(float), st);
+  if (s != TGE_OK) return s;
+  const size_t had = sp.counters.bytes;
+  s = sp.counters.reserve(g_mem, (size_t)std::max(L.segments, 1) * sizeof(int), st);
+  if (s != TGE_OK) return s;
+  if (sp.counters.bytes != had)
+    TGE_HIP(hipMemsetAsync(sp.counters.dev, 0, sp.counters.bytes, st));
+  sp.built = true;
+  return TGE_OK;
+}
+
+}  // namespace
+
 int tge_batch_plan(tge_batch* b, const tge_kv_pool* pool, const tge_batch_desc* d,
                    void* stream) {
   if (!b || !pool || !d) return fail(TGE_ERR_INVALID, "batch_plan: null argument");
@@ -402,6 +451,8 @@ int tge_batch_plan(tge_batch* b, const tge_kv_pool* pool, const tge_batch_desc* 
     s = build_decode_plan(b, pool, b->decode, 0, hs);
     if (s != TGE_OK) return s;
   }
+  s = upload_step_plan(b, pool, hs);
+  if (s != TGE_OK) return s;
   b->planned = true;
   return TGE_OK;
 }
@@ -414,6 +465,14 @@ int tge_batch_info(const tge_batch* b, int* rows, int* work_items, int* max_spli
   if (rows) *rows = (int)b->step.rows.size();
   if (work_items) *work_items = dec ? (int)b->decode.lists.work.size() : 0;
   if (max_splits) *max_splits = dec ? b->decode.lists.max_splits : 0;
+  return TGE_OK;
+}
+
+int tge_batch_step_info(const tge_batch* b, int* workgroups, int* max_pieces) {
+  if (!b || !b->planned) return fail(TGE_ERR_INVALID, "batch_step_info: batch not planned");
+  const bool one = b->small.built;
+  if (workgroups) *workgroups = one ? (int)b->small.lists.recs.size() : 0;
+  if (max_pieces) *max_pieces = one ? b->small.lists.max_pieces : 0;
   return TGE_OK;
 }
 
@@ -638,6 +697,48 @@ int tge_decode_attention(const tge_batch* b, const tge_kv_pool* p, int layer,
     if (s != TGE_OK) return s;
   }
   return run_attention(b, p, layer, q, out, stream, b->decode, true);
+}
+
+int tge_decode_step(const tge_batch* b, tge_kv_pool* p, int layer, const float* q,
+                    const float* k, const float* v, float* out, void* stream) {
+  int s = check_use(b, p, layer, "decode_step");
+  if (s != TGE_OK) return s;
+  if (!q || !k || !v || !out) return fail(TGE_ERR_INVALID, "decode_step: null q/k/v/out");
+  if (!b->decode.built)
+    return fail(TGE_ERR_INVALID, "decode_step: n_new * group exceeds 64 rows");
+  if (!b->small.built || b->sp_stride > 0) {
+    // a large step (or a static sparse one): the append, then the decode
+    // kernel and its split merge
+    s = tge_kv_append(b, p, layer, k, v, stream);
+    if (s != TGE_OK) return s;
+    return tge_decode_attention(b, p, layer, q, out, stream);
+  }
+  const StepPlan& sp = b->small;
+  tge_kv_layer_view view{};
+  tge_kv_pool_layer(p, layer, &view);
+  tge::StepParams a{};
+  a.app.k = k;
+  a.app.v = v;
+  a.app.pool = view.k;
+  a.app.geom = p->geom;
+  a.app.kv_heads = b->step.kv_heads;
+  a.app.head_dim = b->step.head_dim;
+  a.app.scale_f32 = p->desc.scale_format == TGE_SCALE_F32;
+  a.app.q_heads = b->step.q_heads;
+  a.recs = reinterpret_cast<const tge::StepRec*>(sp.image.dev);
+  a.tables = reinterpret_cast<const int*>(b->image.dev + b->off_tables);
+  a.q = q;
+  a.out = out;
+  a.part_o = reinterpret_cast<float*>(sp.part_o.dev);
+  a.part_ml = reinterpret_cast<float*>(sp.part_ml.dev);
+  a.counters = reinterpret_cast<int*>(sp.counters.dev);
+  a.rows_cap = 16 * sp.lists.row_groups;
+  a.group = b->step.group;
+  a.scale_log2 = (float)(1.4426950408889634 / std::sqrt((double)b->step.head_dim));
+  TGE_HIP(tge::launch_step(p->desc.format, p->desc.scale_format == TGE_SCALE_F32,
+                           b->step.head_dim, sp.lists.row_groups, (int)sp.lists.recs.size(), a,
+                           static_cast<hipStream_t>(stream)));
+  return TGE_OK;
 }
 
 int tge_prefill_attention(const tge_batch* b, const tge_kv_pool* p, int layer,

@@ -76,7 +76,25 @@ struct ReduceParams {
   int q_heads;
 };
 
+// Small decode step (paged_step_kernel): append + attention + split merge.
+struct StepParams {
+  AppendParams app;       // pool, geometry, k/v rows, scale format (rows unused)
+  const StepRec* recs;    // one per workgroup
+  const int* tables;
+  const float* q;
+  float* out;
+  float* part_o;          // [parts][rows_cap][head_dim]
+  float* part_ml;         // [parts][rows_cap][2]
+  int* counters;          // [segments], zero between launches
+  int rows_cap;
+  int group;              // query heads per KV head
+  float scale_log2;
+};
+
 hipError_t launch_kv_append(int format, const AppendParams& p, hipStream_t stream);
+// One workgroup per StepRec; row_groups = ceil(max n_new * group / 16).
+hipError_t launch_step(int format, int scale_f32, int head_dim, int row_groups, int n_recs,
+                       const StepParams& p, hipStream_t stream);
 hipError_t launch_kv_append_rope(int format, const AppendParams& p, hipStream_t stream);
 hipError_t launch_kv_gather(int format, const GatherParams& p, hipStream_t stream);
 // Decode attention over a balanced plan (p.wg_first required): n_groups

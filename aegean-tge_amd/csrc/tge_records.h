@@ -53,6 +53,49 @@ struct ReduceRec {
   int pad;
 };
 
+// One workgroup of a small decode step (append, attention and split merge
+// in one launch): a piece of one (session, KV head) segment. The piece
+// holding the segment's new positions stores the new rows of its KV head
+// first; a segment cut into several pieces is merged by the last of its
+// pieces to finish, found through the segment's arrival counter.
+struct StepRec {
+  int session;
+  int kv_head;
+  int page_begin;  // logical page range [page_begin, page_end)
+  int page_end;
+  int part;        // partial slot of this piece, or -1 (the segment is one piece)
+  int seg;         // segment index: its arrival counter
+  int seg_parts;   // pieces of the segment
+  int seg_first;   // partial slot of the segment's first piece
+  int append;      // 1: store the session's new rows of this KV head first
+  int ctx;
+  int n_new;
+  int q_row;
+  int table_off;
+  int pad[3];
+};
+
+static_assert(sizeof(StepRec) == 16 * sizeof(int), "StepRec is read as 16 ints");
+
+// The one-kernel decode step: waves per workgroup, and the pages one wave
+// holds in registers at once (page images of 2*KW + 2*SW dwords per lane
+// beside the unit's accumulators; KW dwords of K per lane = 16 tokens x
+// head_dim elements / 64 lanes, SW dwords of scales). A piece of a context
+// is a whole number of such batches.
+constexpr int kStepWaves = 8;
+constexpr int kStepMaxParts = 64;  // pieces of one (session, KV head) context
+constexpr int step_batch_pages(bool i8, bool scale_f32, int head_dim, int row_groups) {
+  const int np = head_dim / 32;
+  const int kw = i8 ? 2 * np : 4 * np;
+  const int sw = i8 ? (scale_f32 ? 4 * np : 2 * np) : 0;
+  return row_groups >= 3 ? 1 : (2 * kw + 2 * sw <= 16 ? 4 : 2);
+}
+
+// Steps the one-kernel step takes: rows per unit that fit its registers.
+constexpr bool step_fits(bool i8, bool scale_f32, int head_dim, int rows) {
+  return rows <= kMaxRows && (head_dim <= 64 || rows <= (i8 && scale_f32 ? 32 : 48));
+}
+
 struct RowRec {  // one new token: destination page and slot, logical position
   int page;
   int slot;

@@ -373,6 +373,72 @@ void build_prefill(const Step& b, int cus, AttnLists& pl, int only) {
   pl.groups = (int)pl.work.size();
 }
 
+bool build_step_lists(const Step& b, bool i8, bool scale_f32, StepLists& out) {
+  out = StepLists{};
+  if (b.max_rows > kMaxRows || b.sessions.empty()) return false;
+  long blocks = 0;
+  int max_pages = 0;
+  for (const auto& sr : b.sessions) {
+    const int pages = (sr.ctx + sr.n_new + 15) / 16;
+    blocks += (long)pages * b.kv_heads;
+    max_pages = std::max(max_pages, pages);
+  }
+  if (blocks > kStepMaxBlocks) return false;
+  // 64 rows at head_dim 128 (48 with int8 K/V and fp32 scales) do not fit
+  // the step kernel's registers beside its page images (it would spill);
+  // those steps take the decode kernel
+  if (!step_fits(i8, scale_f32, b.head_dim, b.max_rows)) return false;
+  out.row_groups = std::max(1, std::min(4, (b.max_rows + 15) / 16));
+  // A piece is a whole number of batches (every wave of the workgroup loads
+  // one batch of pages at once), as few as keep every context within
+  // kStepMaxParts pieces.
+  const int batch = kStepWaves * step_batch_pages(i8, scale_f32, b.head_dim, out.row_groups);
+  const int heads = kStepMaxParts - 1;  // pieces before the appending one
+  const int piece = batch * std::max(1, (max_pages + batch * heads - 1) / (batch * heads));
+  out.piece_pages = piece;
+  for (int s = 0; s < (int)b.sessions.size(); ++s) {
+    const SessionRec& sr = b.sessions[(std::size_t)s];
+    const int pages = (sr.ctx + sr.n_new + 15) / 16;
+    // A context of more than one piece: the pages before the first new
+    // position in pieces of `piece` pages cut from the end (the first takes
+    // the remainder), then one piece of the pages the new positions fall in
+    // (at most 5: n_new <= 64), which stores the new rows first.
+    const int written = sr.ctx / 16;
+    const int head = pages <= piece ? 0 : (written + piece - 1) / piece;
+    const int n = head + 1;
+    out.max_pieces = std::max(out.max_pieces, n);
+    for (int h = 0; h < b.kv_heads; ++h) {
+      const int seg = out.segments++;
+      const int first = n > 1 ? out.parts : -1;
+      if (n > 1) out.parts += n;
+      for (int k = 0; k < n; ++k) {
+        StepRec r{};
+        if (k < head) {
+          const int end = written - (head - 1 - k) * piece;
+          r.page_begin = std::max(0, end - piece);
+          r.page_end = end;
+        } else {
+          r.page_begin = head > 0 ? written : 0;
+          r.page_end = pages;
+        }
+        r.session = s;
+        r.kv_head = h;
+        r.part = n > 1 ? first + k : -1;
+        r.seg = seg;
+        r.seg_parts = n;
+        r.seg_first = first;
+        r.append = k == n - 1;
+        r.ctx = sr.ctx;
+        r.n_new = sr.n_new;
+        r.q_row = sr.q_row;
+        r.table_off = sr.table_off;
+        out.recs.push_back(r);
+      }
+    }
+  }
+  return true;
+}
+
 std::size_t image_layout(const AttnLists& pl, std::size_t* off_reduce, std::size_t* off_first) {
   const std::size_t wbytes = pl.work.size() * sizeof(WorkRec);
   *off_reduce = align256(wbytes);

@@ -113,6 +113,28 @@ void build_decode(const Step& s, Residency res, AttnLists& out, int only);
 // the launch covers `cus` compute units about twice; longest items first.
 void build_prefill(const Step& s, int cus, AttnLists& out, int only);
 
+// A small decode step in one launch (paged_step_kernel): one workgroup per
+// piece of a (session, KV head) segment; pieces of a split segment own
+// consecutive partial slots and the segment's arrival counter.
+struct StepLists {
+  std::vector<StepRec> recs;
+  int row_groups = 1;
+  int piece_pages = 0;  // pages of every piece but a segment's first
+  int parts = 0;        // partial slots
+  int segments = 0;     // arrival counters
+  int max_pieces = 0;
+};
+
+// Builds the one-launch lists when every session's rows fit a decode unit
+// (at most 48 rows at head_dim above 64) and the step holds at most
+// kStepMaxBlocks page blocks; returns false (and leaves `out` empty)
+// otherwise. Pieces are whole batches of the kernel's page loads
+// (kStepWaves x step_batch_pages), at most kStepMaxParts per segment; the
+// segment's last piece holds every page with a new position and stores the
+// new rows.
+constexpr int kStepMaxBlocks = 4096;
+bool build_step_lists(const Step& s, bool i8, bool scale_f32, StepLists& out);
+
 // The plan image of `lists` (work | reduce | wg_first, each 256-aligned):
 // total bytes and the offsets of the reduce and wg_first parts.
 std::size_t image_layout(const AttnLists& lists, std::size_t* off_reduce, std::size_t* off_first);

@@ -251,6 +251,12 @@ void Qwen2KvPath::layer(int layer, const float* q, const float* k, const float* 
   if (layer < 0 || layer >= config_.layers) {
     throw std::invalid_argument("layer: layer out of range");
   }
+  if (!prefill_) {
+    // every session's rows fit a decode unit: store and attend in one call
+    // (one kernel for a small step)
+    check(tge_decode_step(batch_, pool_, layer, q, k, v, out, stream), "layer");
+    return;
+  }
   check(tge_kv_append(batch_, pool_, layer, k, v, stream), "layer");
   check(tge_batch_attention(batch_, pool_, layer, q, out, stream), "layer");
 }

@@ -113,6 +113,8 @@ SIGNATURES = [
     ("tge_batch_kernel_times", _I, [_VP, _PI, C.POINTER(C.c_float), C.POINTER(C.c_float)]),
     ("tge_kv_append", _I, [_VP, _VP, _I, _VP, _VP, _VP]),
     ("tge_decode_attention", _I, [_VP, _VP, _I, _VP, _VP, _VP]),
+    ("tge_decode_step", _I, [_VP, _VP, _I, _VP, _VP, _VP, _VP, _VP]),
+    ("tge_batch_step_info", _I, [_VP, _PI, _PI]),
     ("tge_decode_attention_static", _I, [C.POINTER(BatchDesc), _VP, _I, _VP, _VP, _VP]),
     ("tge_prefill_attention", _I, [_VP, _VP, _I, _VP, _VP, _VP]),
     ("tge_kv_gather", _I, [_VP, _VP, _I, _I, _I, _VP, _VP, _VP, _VP, _VP]),
@@ -509,6 +511,19 @@ class Batch:
     def decode(self, pool, layer, q, out, stream=None):
         check(lib().tge_decode_attention(self.h, pool.h, layer, q.ptr, out.ptr, stream),
               "decode_attention")
+
+    def step_info(self):
+        """tge_batch_step_info: (workgroups, max pieces) of the one-kernel
+        step, (0, 0) when the step runs the append and decode kernels."""
+        w, m = C.c_int(), C.c_int()
+        check(lib().tge_batch_step_info(self.h, C.byref(w), C.byref(m)), "batch_step_info")
+        return w.value, m.value
+
+    def decode_step(self, pool, layer, q, k, v, out, stream=None):
+        """tge_decode_step: append the step's K/V rows, then decode attention
+        (one kernel for a small step)."""
+        check(lib().tge_decode_step(self.h, pool.h, layer, q.ptr, k.ptr, v.ptr, out.ptr, stream),
+              "decode_step")
 
     def attention(self, pool, layer, q, out, stream=None):
         """tge_batch_attention: decode kernel for short sessions, prefill kernel for the rest."""

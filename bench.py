@@ -271,7 +271,20 @@ class DecodeBench:
             for layer in range(L):
                 tk.check(lib.tge_kv_append_rope(batch, pool, layer, C.byref(args), None))
         hip.record(e3)
+        # The whole layer step as the driver issues it (tge_decode_step: one
+        # kernel for a small step, else append + decode + merge), replayed
+        # (idempotent: the same rows stored at the same positions again).
+        e4, e5 = hip.event(), hip.event()
+        hip.record(e4)
+        for _ in range(replay):
+            for layer in range(L):
+                tk.check(lib.tge_decode_step(batch, pool, layer, self.q.ptr, self.k.ptr, self.v.ptr,
+                                             self.out.ptr, None))
+        hip.record(e5)
+        step_wg, step_pieces = C.c_int(), C.c_int()
+        tk.check(lib.tge_batch_step_info(batch, C.byref(step_wg), C.byref(step_pieces)))
         att_ms = hip.elapsed_ms(e0, e1) / (replay * L)
+        step_launch_ms = hip.elapsed_ms(e4, e5) / (replay * L)
         app_ms = hip.elapsed_ms(e1, e2) / (replay * L)
         rope_ms = hip.elapsed_ms(e2r, e3) / (replay * L)
         # Static sparse attention (sink 4, window 512) at stride 4 (every
@@ -306,6 +319,10 @@ class DecodeBench:
             "attn_gbs": att_b / (att_ms * 1e-3) / 1e9,
             "attn_kernel_gbs": att_b / (float(np.mean(k_us)) * 1e-6) / 1e9,
             "append_launch_us": app_ms * 1e3,
+            "step_launch_us": step_launch_ms * 1e3,
+            "step_path": (f"one kernel, {step_wg.value} workgroups, up to {step_pieces.value} "
+                          f"pieces per context" if step_wg.value else "append + decode + merge"),
+            "step_gbs": (att_b + app_b) / (step_launch_ms * 1e-3) / 1e9,
             "append_bytes_per_launch": app_b,
             "append_gbs": app_b / (app_ms * 1e-3) / 1e9,
             "append_rope_launch_us": rope_ms * 1e3,
@@ -929,6 +946,8 @@ def main():
             "merge_kernel_us": round(r["merge_kernel_us"], 3),
             "append_launch_us": round(r["append_launch_us"], 3),
             "append_rope_launch_us": round(r["append_rope_launch_us"], 3),
+            "step_launch_us": round(r["step_launch_us"], 3),
+            "step_path": r["step_path"],
             "sparse_attn_kernel_us": {k: round(v, 3) for k, v in r["sparse_attn_kernel_us"].items()},
             "decode_work_items": r["work_items"], "max_splits": r["max_splits"],
             "pool": "fragmented" if cfg.fragmented else "fresh (LIFO reuse after churn)",

@@ -228,6 +228,27 @@ int tge_decode_attention(const tge_batch* batch, const tge_kv_pool* pool,
                          int layer, const float* q, float* out, void* stream);
 
 /*
+ * tge_kv_append followed by tge_decode_attention, in one call: the
+ * store-then-attend order of forward / forward_batch (qwen2.cpp:2073-2095,
+ * 1681-1747). A small step (every session's rows fit a decode unit, at
+ * most 48 rows per session at head_dim 128, at most 4096 page blocks in the
+ * step, no static sparse subset) runs as one kernel: the workgroup that reads a segment's new positions stores the new
+ * rows of its KV head first (the same bits as tge_kv_append), and a context
+ * cut into several pieces is merged by the last piece to finish. Larger
+ * steps run the append, the decode kernel and its merge. Outputs equal
+ * those of the two calls within the attention tolerance (the same math,
+ * other page splits).
+ */
+int tge_decode_step(const tge_batch* batch, tge_kv_pool* pool, int layer, const float* q,
+                    const float* k, const float* v, float* out, void* stream);
+
+/* Workgroups of the one-kernel step tge_decode_step launches for the
+ * current plan, and the most pieces one (session, KV head) context is cut
+ * into; 0 and 0 when the step runs the append and decode kernels. No
+ * counterpart in the reference: for benchmarks and tests. */
+int tge_batch_step_info(const tge_batch* batch, int* workgroups, int* max_pieces);
+
+/*
  * tge_decode_attention for callers that cannot allocate memory (code under
  * HIP graph capture, tight serving loops, harnesses that forbid hipMalloc).
  * No counterpart in the reference. It plans the step from `desc` on the

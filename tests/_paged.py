@@ -66,6 +66,10 @@ class PagedCase:
         dk, dv = tk.DeviceArray.from_numpy(kk), tk.DeviceArray.from_numpy(vv)
         dq = tk.DeviceArray.from_numpy(self.q)
         dout = tk.DeviceArray((self.q.shape[0], self.qh * self.hd), np.float32).zero()
+        if kind == "step":  # append + attention in one call
+            b.decode_step(self.pool, layer, dq, dk, dv, dout)
+            tk.hip().sync()
+            return dout.numpy(), b
         b.append(self.pool, layer, dk, dv)
         if kind == "decode":
             b.decode(self.pool, layer, dq, dout)

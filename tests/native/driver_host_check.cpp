@@ -103,6 +103,10 @@ int tge_batch_attention(const tge_batch* b, const tge_kv_pool*, int, const float
                         void*) {
   return b->planned ? TGE_OK : TGE_ERR_INVALID;
 }
+int tge_decode_step(const tge_batch* b, tge_kv_pool*, int, const float*, const float*,
+                    const float*, float*, void*) {
+  return b->planned ? TGE_OK : TGE_ERR_INVALID;
+}
 int tge_batch_set_sparse(tge_batch*, int, int, int, int) { return TGE_OK; }
 }
 

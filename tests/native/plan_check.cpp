@@ -4,6 +4,8 @@
 //     page of every (session, KV head[, query tile]) exactly once, in order;
 //     split items own consecutive partial slots that one reduction record
 //     lists; workgroup ranges tile the work list; rows fit the units;
+//   - the one-launch step lists are taken exactly when a step qualifies and
+//     tile each (session, KV head) in order with one appending last piece;
 //   - invalid descriptions are rejected and leave the step untouched;
 //   - staged uploads and scratch buffers survive injected allocation
 //     failures: after a failure the recorded capacity is zero, and a later
@@ -171,6 +173,75 @@ void check_lists(const Step& st, const AttnLists& l, int only, bool prefill) {
   }
 }
 
+// The one-launch step lists: taken exactly when the step qualifies; each
+// (session, KV head) is one segment of at most kStepMaxParts pieces tiling
+// its pages in order; only the last piece appends and it holds every new
+// position (and, when there are several, nothing else); split pieces own
+// consecutive partial slots, each slot once.
+void check_step_lists(const Step& st, bool i8, bool sf32) {
+  StepLists sl;
+  const bool one = build_step_lists(st, i8, sf32, sl);
+  long blocks = 0;
+  for (const auto& r : st.sessions) blocks += (long)((r.ctx + r.n_new + 15) / 16) * st.kv_heads;
+  const int row_cap = st.head_dim <= 64 ? 64 : (i8 && sf32 ? 32 : 48);
+  const bool fits = st.max_rows <= row_cap && blocks <= kStepMaxBlocks && !st.sessions.empty();
+  REQUIRE(one == fits, "one-launch %d, qualifies %d (rows %d blocks %ld)", one, fits, st.max_rows,
+          blocks);
+  if (!one) {
+    REQUIRE(sl.recs.empty() && sl.parts == 0 && sl.segments == 0, "lists left behind");
+    return;
+  }
+  REQUIRE(16 * sl.row_groups >= st.max_rows && sl.row_groups <= 4, "row groups %d", sl.row_groups);
+  const int batch = kStepWaves * step_batch_pages(i8, sf32, st.head_dim, sl.row_groups);
+  REQUIRE(sl.piece_pages >= batch && sl.piece_pages % batch == 0, "piece %d batch %d",
+          sl.piece_pages, batch);
+  REQUIRE(sl.piece_pages == batch || sl.max_pieces > kStepMaxParts / 2, "pieces longer than needed");
+  std::vector<int> slot_used((std::size_t)sl.parts, 0);
+  std::size_t i = 0;
+  int seg = 0, max_pieces = 0;
+  for (int s = 0; s < (int)st.sessions.size(); ++s) {
+    const SessionRec& sr = st.sessions[(std::size_t)s];
+    const int pages = (sr.ctx + sr.n_new + 15) / 16;
+    for (int h = 0; h < st.kv_heads; ++h, ++seg) {
+      int at = 0, k = 0;
+      const int n = sl.recs[i].seg_parts;
+      REQUIRE(n >= 1 && n <= kStepMaxParts, "pieces %d", n);
+      max_pieces = std::max(max_pieces, n);
+      for (; k < n; ++k, ++i) {
+        REQUIRE(i < sl.recs.size(), "records end early");
+        const StepRec& r = sl.recs[i];
+        REQUIRE(r.session == s && r.kv_head == h && r.seg == seg && r.seg_parts == n,
+                "record %zu identity", i);
+        REQUIRE(r.ctx == sr.ctx && r.n_new == sr.n_new && r.q_row == sr.q_row &&
+                    r.table_off == sr.table_off, "record %zu session fields", i);
+        REQUIRE(r.page_begin == at && r.page_end > r.page_begin, "record %zu pages", i);
+        if (n > 1 && k == n - 1) {
+          REQUIRE(r.page_begin == sr.ctx / 16 && r.page_end - r.page_begin <= 5,
+                  "appending piece [%d, %d) of ctx %d", r.page_begin, r.page_end, sr.ctx);
+        } else if (n > 1) {
+          REQUIRE(r.page_end - r.page_begin == sl.piece_pages || k == 0, "piece length");
+          REQUIRE(r.page_end - r.page_begin <= sl.piece_pages, "first piece length");
+        } else {
+          REQUIRE(pages <= sl.piece_pages, "one piece of %d pages", pages);
+        }
+        at = r.page_end;
+        REQUIRE(r.append == (k == n - 1), "append flag");
+        if (r.append) REQUIRE(16 * r.page_begin <= sr.ctx, "new positions before the last piece");
+        if (n == 1) {
+          REQUIRE(r.part == -1 && r.seg_first == -1, "single piece with a slot");
+        } else {
+          REQUIRE(r.part == r.seg_first + k && r.part >= 0 && r.part < sl.parts, "slot %d", r.part);
+          REQUIRE(slot_used[(std::size_t)r.part]++ == 0, "slot %d twice", r.part);
+        }
+      }
+      REQUIRE(at == pages, "segment covers %d of %d pages", at, pages);
+    }
+  }
+  REQUIRE(i == sl.recs.size() && seg == sl.segments, "extra records");
+  REQUIRE(max_pieces == sl.max_pieces, "max pieces");
+  for (int u : slot_used) REQUIRE(u == 1, "unused slot");
+}
+
 void random_plans(int cases) {
   std::mt19937 rng(12345);
   for (int i = 0; i < cases; ++i) {
@@ -189,6 +260,21 @@ void random_plans(int cases) {
     int rows = 0;
     for (int k = 0; k < ns; ++k) rows += d.n_new[(std::size_t)k];
     REQUIRE((int)st.rows.size() == rows, "rows");
+    const bool i8 = rng() % 2, sf32 = rng() % 2;
+    check_step_lists(st, i8, sf32);
+    {
+      // the same sessions at head_dim 64, and a short slice of them (so
+      // that many steps qualify for one launch)
+      Step s64;
+      REQUIRE(build_step(s64, ns, d.ctx.data(), d.n_new.data(), d.offsets.data(), d.ids.data(),
+                         kvh * group, kvh, 64, pool, &msg) == TGE_OK, "head_dim 64");
+      check_step_lists(s64, i8, sf32);
+      const int few = std::min(ns, 1 + (int)(rng() % 4));
+      Step sf;
+      REQUIRE(build_step(sf, few, d.ctx.data(), d.n_new.data(), d.offsets.data(), d.ids.data(),
+                         kvh * group, kvh, (i & 1) ? 64 : 128, pool, &msg) == TGE_OK, "slice");
+      check_step_lists(sf, i8, sf32);
+    }
     const int cus = (rng() % 2) ? 256 : 1 + (int)(rng() % 300);
     const Residency res{cus * (1 + (int)(rng() % 2)), cus};
     for (int only = 0; only < 3; ++only) {

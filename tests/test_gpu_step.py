@@ -1,0 +1,131 @@
+"""GPU parity of tge_decode_step (append + decode attention in one call; a
+small step is one kernel that stores the new rows, attends and merges its
+split contexts in-kernel) against the oracle: pool contents bit for bit,
+attention within max-abs 2e-3 / rel 1e-3."""
+import sys
+
+import numpy as np
+import pytest
+
+import synth
+import tge_kv as tk
+from _paged import PagedCase
+from _util import assert_attention_close, bits
+from test_gpu_kv import check_contents
+
+pytestmark = pytest.mark.gpu
+
+
+def say(*a):
+    print(*a, flush=True)
+    sys.stdout.flush()
+
+
+STEP_CASES = {
+    # name: (q_heads, kv_heads, hd, fmt, sf, contexts, n_new, outliers)
+    "c1_shape": (14, 2, 64, tk.KV_F16, 0, [1024], 1, 0),
+    "c2_shape_i8": (14, 2, 64, tk.KV_I8, 0, [4096], 1, 0.01),
+    "c3_shape": (12, 2, 128, tk.KV_F16, 0, [512, 2048, 4096, 8192], 1, 0),
+    "verify_i8_f32_scales": (28, 4, 128, tk.KV_I8, 1, [700, 35, 1500], 4, 0.01),
+    "span_edges": (8, 2, 64, tk.KV_F16, 0, [0, 15, 16, 17, 31, 32, 255, 256, 257], 1, 0),
+    "verify_six_page_cross": (14, 2, 64, tk.KV_I8, 0, [13, 510, 1000], 6, 0),
+}
+
+
+@pytest.mark.parametrize("name", list(STEP_CASES))
+def test_step_matches_oracle(gpu, name):
+    qh, kvh, hd, fmt, sf, ctx, nn, out = STEP_CASES[name]
+    say(f"step case {name}")
+    case = PagedCase(qh, kvh, hd, fmt, ctx, nn, scale_format=sf, seed=31, outlier_frac=out)
+    case.fill()
+    got, b = case.step(kind="step")
+    assert b.step_info()[0] > 0, "the step ran the append + decode kernels"
+    err = assert_attention_close(got, case.oracle_out(), name)
+    say(f"  max abs err {err:.2e}")
+    b.close()
+    check_contents(case)
+    case.close()
+
+
+def test_step_split_counters_across_layers(gpu):
+    """A context cut into the most pieces, run on three layers in a row and
+    twice on one layer: every launch's last piece merges and resets its
+    segment counter, so each launch matches the oracle and a repeat is
+    bit-identical."""
+    case = PagedCase(12, 2, 128, tk.KV_F16, [8000, 300], 2, seed=44, layers=3)
+    for layer in range(3):
+        case.fill(layer)
+    outs = []
+    for layer in (0, 1, 2, 2):
+        got, b = case.step(layer=layer, kind="step")
+        # 500 context pages in pieces of 16, then the page of the new rows
+        assert b.step_info()[1] == 33
+        assert_attention_close(got, case.oracle_out(), f"layer {layer}")
+        outs.append(got)
+        b.close()
+    assert np.array_equal(bits(outs[2]), bits(outs[3]))
+    case.close()
+
+
+def test_step_pieces_of_several_batches(gpu):
+    """A context long enough that one batch per wave would need more than 64
+    pieces: pieces of two batches, every wave loading twice."""
+    case = PagedCase(8, 1, 64, tk.KV_F16, [48000], 1, seed=46)
+    case.fill()
+    got, b = case.step(kind="step")
+    wg, pieces = b.step_info()
+    assert wg == pieces and 32 < pieces <= 64, (wg, pieces)
+    assert_attention_close(got, case.oracle_out(), "two-batch pieces")
+    b.close()
+    check_contents(case)
+    case.close()
+
+
+def _random_step_case(i):
+    r = np.random.default_rng(7000 + i)
+    kvh = int(r.choice([1, 2, 4, 8]))
+    hd = int(r.choice([64, 128]))
+    group = int(r.integers(1, 9))
+    fmt = int(r.choice([tk.KV_F16, tk.KV_I8]))
+    sf = int(r.choice([tk.SCALE_F16, tk.SCALE_F32])) if fmt == tk.KV_I8 else tk.SCALE_F16
+    n_s = int(r.integers(1, 6))
+    # rows per unit the one-kernel step holds (step_fits)
+    cap = 64 if hd == 64 else (32 if fmt == tk.KV_I8 and sf == tk.SCALE_F32 else 48)
+    max_q = max(1, cap // group)
+    contexts = [int(r.choice([0, int(r.integers(1, 400)), int(r.integers(400, 3000))]))
+                for _ in range(n_s)]
+    n_new = [int(r.integers(1, min(6, max_q) + 1)) for _ in range(n_s)]
+    return dict(qh=kvh * group, kvh=kvh, hd=hd, fmt=fmt, sf=sf, contexts=contexts, n_new=n_new)
+
+
+@pytest.mark.parametrize("i", range(16))
+def test_random_steps(gpu, i):
+    """Sixteen seeded random small steps (heads, head_dim, formats, empty and
+    ragged contexts, 1-6 new rows per session) through tge_decode_step:
+    pool contents bit-exact, attention against the oracle."""
+    c = _random_step_case(i)
+    say(f"random step {i}: {c}")
+    case = PagedCase(c["qh"], c["kvh"], c["hd"], c["fmt"], c["contexts"], c["n_new"],
+                     scale_format=c["sf"], seed=8000 + i,
+                     outlier_frac=0.01 if c["fmt"] == tk.KV_I8 else 0)
+    case.fill()
+    got, b = case.step(kind="step")
+    assert b.step_info()[0] > 0
+    err = assert_attention_close(got, case.oracle_out(), f"random step {i}")
+    say(f"  max abs err {err:.2e}")
+    b.close()
+    check_contents(case)
+    case.close()
+
+
+def test_step_large_falls_back(gpu):
+    """A step above the one-launch size (more than 4096 page blocks) runs the
+    append, the persistent decode kernel and its merge: same results."""
+    case = PagedCase(28, 4, 128, tk.KV_I8, [9000, 9000], 4, seed=45, outlier_frac=0.01)
+    case.fill()
+    got, b = case.step(kind="step")
+    assert b.step_info() == (0, 0)
+    assert_attention_close(got, case.oracle_out(), "large step")
+    b.close()
+    check_contents(case)
+    case.close()
