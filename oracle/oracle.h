@@ -17,9 +17,14 @@
  *   orc_half_to_float        exhaustive 2^16 vs hardware F16C, vs oracle/_ref
  *   orc_float_to_half        exhaustive 2^32 vs an independent bit model, KATs
  *                            from test_attention.cpp:107-115, vs oracle/_ref
- *   orc_quantize_kv_block    closed forms (exact-ratio blocks, all-zero sign
- *                            rule, +-0.49999997 rounding), brute force vs a
- *                            float64 model of the fp32 op sequence
+ *   orc_quantize_kv_block    closed forms: exact-ratio blocks, the all-zero
+ *                            sign rule, +-0.49999997 rounding, blocks whose
+ *                            codes change if x*inv +- 0.5 is fused into one
+ *                            multiply-add, blocks whose codes change if they
+ *                            come from the f16-rounded scale (expected codes
+ *                            from exact float64 arithmetic); property checks
+ *                            on random blocks (nearest code within fp32
+ *                            slack, the maximum maps to +-127)
  *   orc_attention_head       vs oracle/_ref attention_head_scalar (bit-exact),
  *                            closed forms (span 1, equal keys, dominant key),
  *                            float64 truth

@@ -165,6 +165,31 @@ def test_append_i8_edge_blocks(gpu):
         pool.close()
 
 
+def test_append_i8_rounding_closed_forms(gpu):
+    # Blocks whose codes change if the quantizer fuses x*inv +- 0.5 into one
+    # multiply-add, and blocks whose codes change if they are derived from
+    # the f16-rounded scale (expected codes from exact arithmetic,
+    # tests/_quant_cases.py); K gets one kind, V the other.
+    from _quant_cases import contraction_blocks, f16_scale_blocks
+    kb, kc = contraction_blocks(32, seed=11)
+    vb, vc, vs16 = f16_scale_blocks(32, seed=12)
+    rows, kv_dim = 8, 128
+    k = kb.reshape(rows, kv_dim)
+    v = vb.reshape(rows, kv_dim)
+    for sf in (tk.SCALE_F16, tk.SCALE_F32):
+        say(f"append rounding closed forms, scale format {sf}")
+        pool = tk.KvPool(1, 2, 1, kv_dim, tk.KV_I8, sf)
+        b = tk.Batch().plan(pool, [tk.Session(0, rows, [1])], 1)
+        b.append(pool, 0, tk.DeviceArray.from_numpy(k), tk.DeviceArray.from_numpy(v))
+        tk.hip().sync()
+        gk, gv, _, gvs = b.gather(pool, 0, 0, rows)
+        assert np.array_equal(gk.reshape(-1, 32), kc)
+        assert np.array_equal(gv.reshape(-1, 32), vc)
+        if sf == tk.SCALE_F16:
+            assert np.array_equal(gvs.reshape(-1), vs16)
+        pool.close()
+
+
 # ---------------------------------------------------------------------------
 # attention
 # ---------------------------------------------------------------------------
@@ -295,6 +320,31 @@ def test_decode_many_units_per_workgroup(gpu):
         say(f"  plan {b.info()}")
         assert b.info()[1] > 4 * 64, "expected several units per workgroup"
         assert_attention_close(out, want, "many units")
+        outs.append(out)
+        b.close()
+    assert np.array_equal(bits(outs[0]), bits(outs[1]))
+    case.close()
+
+
+def test_decode_short_units_mixed_rows(gpu):
+    """Units shorter than a wave's page ring with mixed row counts: eighty
+    sessions of 0-50 cached positions with 1-6 new tokens (7-42 rows, one to
+    three 16-row groups), so a workgroup's share holds many one- to
+    four-page units whose pages cross unit boundaries in the ring, and the
+    Q table is reloaded mid-share. Matches the oracle and is
+    bit-reproducible."""
+    r = np.random.default_rng(77)
+    ctx = [int(x) for x in r.integers(0, 51, 80)]
+    nn = [int(x) for x in r.integers(1, 7, 80)]
+    nn[0] = 6  # at least one unit of three row groups
+    case = PagedCase(28, 4, 128, tk.KV_I8, ctx, nn, seed=43, outlier_frac=0.01)
+    case.fill()
+    want = case.oracle_out()
+    outs = []
+    for _ in range(2):
+        out, b = case.step()
+        say(f"  plan {b.info()}")
+        assert_attention_close(out, want, "row-split short units")
         outs.append(out)
         b.close()
     assert np.array_equal(bits(outs[0]), bits(outs[1]))

@@ -155,6 +155,39 @@ def test_quantize_half_rounding_is_add_then_truncate():
     assert round(float(below_half)) == 0
 
 
+def test_quantize_multiply_then_add_is_not_fused():
+    # Values whose exact product x*inv lies just below 0.5 - 2^-25: the
+    # reference rounds the product (to 0.5 - 2^-25), then the add ties to
+    # 1.0 (code +-1); one fused multiply-add rounds once to 1 - 2^-24 (code
+    # 0). A contracted oracle fails every block.
+    from _quant_cases import contraction_blocks
+    blocks, want = contraction_blocks(24, seed=3)
+    for b, w in zip(blocks, want):
+        codes, _ = quant(b)
+        assert np.array_equal(codes, w), (b[:3], codes[:9], w[:9])
+    # the row quantizer (the store path) agrees block for block
+    rows = blocks.reshape(6, 128)
+    codes, _ = O.quantize_rows(rows)
+    assert np.array_equal(codes.reshape(-1, 32), want)
+
+
+def test_quantize_codes_use_the_fp32_scale():
+    # the f16-scale format stores float_to_half(scale) but its
+    # codes come from the fp32 scale. Each value sits a margin above a
+    # half-integer multiple of the fp32 scale and below it for the (larger)
+    # f16-rounded scale, so codes derived from the stored f16 scale would be
+    # one smaller in magnitude on every non-maximum slot.
+    from _quant_cases import f16_scale_blocks
+    blocks, want, s16 = f16_scale_blocks(24, seed=4)
+    for b, w, h in zip(blocks, want, s16):
+        codes, s = quant(b)
+        assert np.array_equal(codes, w), (codes[:6], w[:6])
+        assert O.float_to_half(np.array([s], np.float32))[0] == h
+        inv16 = np.float32(1) / O.half_to_float(np.array([h], np.uint16))[0]
+        alt = np.trunc(b[1:] * inv16 + np.where(b[1:] >= 0, 0.5, -0.5).astype(np.float32))
+        assert np.all(np.abs(alt) == np.abs(w[1:].astype(np.float32)) - 1)
+
+
 def test_quantize_properties_random():
     rng = np.random.default_rng(7)
     for trial in range(400):
