@@ -812,13 +812,12 @@ __global__ __launch_bounds__(256) void split_reduce_kernel(ReduceParams p) {
   } else {
     if (!active) return;
   }
-  const SessionRec s = p.sessions[it.session];
   const int q_stride = p.q_heads * D;
   const int qi = it.row_begin + r / it.rows_per_query;
   const int head = it.head_base + r % it.rows_per_query;
   float4_t res = float4_t{0, 0, 0, 0};
   if (sum > 0.0f) res = div4(acc, sum);
-  *reinterpret_cast<float4_t*>(p.out + (size_t)(s.q_row + qi) * q_stride + (size_t)head * D + 4 * d4) = res;
+  *reinterpret_cast<float4_t*>(p.out + (size_t)(it.q_row + qi) * q_stride + (size_t)head * D + 4 * d4) = res;
 }
 
 }  // namespace
@@ -943,8 +942,8 @@ hipError_t launch_prefill(int format, int scale_f32, int head_dim, int n_units,
 
 template <int D>
 hipError_t launch_reduce_d(int n_items, int max_parts, const ReduceParams& p, hipStream_t stream) {
-  // Slots per row: about one per 4 splits, at most 8.
-  const int want = (max_parts + 3) / 4;
+  // Slots per row: one per batch of 8 splits (one round of loads), at most 8.
+  const int want = (max_parts + 7) / 8;
   const int slots = want <= 1 ? 1 : (want <= 2 ? 2 : (want <= 4 ? 4 : 8));
   const int rpb = 256 / (D / 4 * slots);
   const dim3 grid((unsigned)n_items, (unsigned)((p.rows_cap + rpb - 1) / rpb)), block(256);

@@ -588,7 +588,6 @@ int run_attention(const tge_batch* b, const tge_kv_pool* p, int layer, const flo
   if (ev) TGE_HIP(hipEventRecord((*ev)[1], st));
   if (!pl.lists.reduce.empty()) {
     tge::ReduceParams r{};
-    r.sessions = a.sessions;
     r.items = reinterpret_cast<const tge::ReduceRec*>(pl.image.dev + pl.off_reduce);
     r.part_o = reinterpret_cast<const float*>(pl.part_o.dev);
     r.part_ml = reinterpret_cast<const float*>(pl.part_ml.dev);
@@ -913,7 +912,6 @@ int tge_decode_attention_static(const tge_batch_desc* d, const tge_kv_pool* p, i
   TGE_HIP(tge::launch_decode(f, sf32, hd, lists.row_groups, lists.groups, a, st));
   if (!lists.reduce.empty()) {
     tge::ReduceParams r{};
-    r.sessions = a.sessions;
     r.items = reinterpret_cast<const tge::ReduceRec*>(base + o_work + l_red);
     r.part_o = a.part_o;
     r.part_ml = a.part_ml;

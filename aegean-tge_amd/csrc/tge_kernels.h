@@ -67,7 +67,6 @@ struct AttnParams {
 };
 
 struct ReduceParams {
-  const SessionRec* sessions;
   const ReduceRec* items;
   const float* part_o;
   const float* part_ml;

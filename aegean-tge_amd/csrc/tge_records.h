@@ -50,7 +50,7 @@ struct ReduceRec {
   int head_base;
   int first_part;
   int n_parts;
-  int pad;
+  int q_row;  // the session's first row in q/out (its SessionRec copy)
 };
 
 // One workgroup of a small decode step (append, attention and split merge

@@ -278,6 +278,7 @@ void build_decode(const Step& b, Residency res, AttnLists& pl, int only) {
       r.rows_per_query = w0.rows_per_query;
       r.head_base = w0.head_base;
       r.first_part = pl.parts;
+      r.q_row = w0.q_row;
       r.n_parts = n;
       for (std::size_t k = i; k < j; ++k) pl.work[k].part = pl.parts++;
       pl.reduce.push_back(r);
@@ -309,6 +310,7 @@ void add_units(std::vector<WorkRec>& work, std::vector<ReduceRec>& red, int& par
   r.rows_per_query = base.rows_per_query;
   r.head_base = base.head_base;
   r.first_part = parts;
+  r.q_row = base.q_row;
   r.n_parts = 0;
   for (int b = 0; b < pages; b += chunk) {
     WorkRec w = base;
