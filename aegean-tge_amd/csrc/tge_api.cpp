@@ -923,6 +923,53 @@ int tge_decode_attention_static(const tge_batch_desc* d, const tge_kv_pool* p, i
   return TGE_OK;
 }
 
+int tge_eligible_gqa(int requested, int span, int threads, int follows_schedule,
+                     int dense_only) {
+  // eligible_gqa = requested && want_gqa_gpu(span, threads) && follows && dense
+  // (backend.hpp:170-174); want_gqa_gpu = threads > 1 && span >= kGqaMinSpan
+  // (backend.hpp:124-126).
+  return requested && threads > 1 && span >= TGE_GQA_MIN_SPAN && follows_schedule && dense_only
+             ? 1
+             : 0;
+}
+
+int tge_attention_group(const tge_attention_group_args* a, void* stream) {
+  if (!a || !a->pool) return fail(TGE_ERR_INVALID, "attention_group: null argument");
+  const tge_kv_pool* p = a->pool;
+  if (a->layer < 0 || a->layer >= p->desc.layers)
+    return fail(TGE_ERR_INVALID, "attention_group: layer out of range");
+  if (a->kv_head < 0 || a->kv_head >= p->desc.kv_heads)
+    return fail(TGE_ERR_INVALID, "attention_group: kv_head out of range");
+  if (!a->page_ids || !a->queries || !a->maxima || !a->sums || !a->accumulators)
+    return fail(TGE_ERR_INVALID, "attention_group: null pointer");
+  if (a->first < 0 || a->count < 0)
+    return fail(TGE_ERR_INVALID, "attention_group: first and count must be >= 0");
+  if (a->group_heads < 1 || a->group_heads > tge::kPrefillRows)
+    return fail(TGE_ERR_INVALID, "attention_group: group_heads must be 1..128");
+  int s = backend_ready();
+  if (s != TGE_OK) return fail(s, "attention_group: backend unavailable");
+  tge_kv_layer_view v{};
+  tge_kv_pool_layer(p, a->layer, &v);
+  tge::GroupParams g{};
+  g.pool = v.k;
+  g.block_bytes = (uint32_t)p->geom.block_bytes;
+  g.pages = p->desc.pages;
+  g.kv_heads = p->desc.kv_heads;
+  g.kv_head = a->kv_head;
+  g.page_ids = a->page_ids;
+  g.first = a->first;
+  g.count = a->count;
+  g.queries = a->queries;
+  g.group_heads = a->group_heads;
+  g.scale = a->scale;
+  g.maxima = a->maxima;
+  g.sums = a->sums;
+  g.accumulators = a->accumulators;
+  TGE_HIP(tge::launch_attention_group(p->desc.format, p->desc.scale_format == TGE_SCALE_F32,
+                                      p->desc.head_dim, g, static_cast<hipStream_t>(stream)));
+  return TGE_OK;
+}
+
 int tge_kv_gather(const tge_batch* b, const tge_kv_pool* p, int layer, int session,
                   int count, void* k_rows, void* v_rows, void* k_scales, void* v_scales,
                   void* stream) {

@@ -90,7 +90,29 @@ struct StepParams {
   float scale_log2;
 };
 
+// Kernel-level group attention (tge_attention_group): one KV head's query
+// group over positions [first, first + count) of one session's pages.
+struct GroupParams {
+  const void* pool;      // layer base
+  uint32_t block_bytes;  // block stride
+  int pages;             // pages of the pool (ids outside give NaN outputs)
+  int kv_heads;
+  int kv_head;
+  const int* page_ids;   // device, the session's block table
+  int first;
+  int count;
+  const float* queries;  // [group_heads][head_dim]
+  int group_heads;
+  float scale;
+  float* maxima;         // [group_heads]
+  float* sums;           // [group_heads]
+  float* accumulators;   // [group_heads][head_dim]
+};
+
 hipError_t launch_kv_append(int format, const AppendParams& p, hipStream_t stream);
+// One workgroup per query head of the group.
+hipError_t launch_attention_group(int format, int scale_f32, int head_dim, const GroupParams& p,
+                                  hipStream_t stream);
 // One workgroup per StepRec; row_groups = ceil(max n_new * group / 16).
 hipError_t launch_step(int format, int scale_f32, int head_dim, int row_groups, int n_recs,
                        const StepParams& p, hipStream_t stream);

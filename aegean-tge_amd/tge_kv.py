@@ -58,6 +58,14 @@ class Qwen2Config(C.Structure):
 
 # (name, restype, argtypes) of every symbol include/tge_kv.h declares.
 _VP, _I, _PI = C.c_void_p, C.c_int, C.POINTER(C.c_int)
+class AttentionGroupArgs(C.Structure):
+    """tge_attention_group_args (AttentionGroupArgs over pages)."""
+    _fields_ = [("pool", C.c_void_p), ("layer", C.c_int), ("kv_head", C.c_int),
+                ("page_ids", C.c_void_p), ("first", C.c_int), ("count", C.c_int),
+                ("queries", C.c_void_p), ("group_heads", C.c_int), ("scale", C.c_float),
+                ("maxima", C.c_void_p), ("sums", C.c_void_p), ("accumulators", C.c_void_p)]
+
+
 class RopeAppendArgs(C.Structure):
     _fields_ = [("q", C.c_void_p), ("q_out", C.c_void_p), ("k", C.c_void_p), ("v", C.c_void_p),
                 ("q_bias", C.c_void_p), ("k_bias", C.c_void_p), ("v_bias", C.c_void_p),
@@ -98,6 +106,8 @@ SIGNATURES = [
     ("tge_kv_pool_bytes", C.c_size_t, [_VP]),
     ("tge_kv_copy_page", _I, [_VP, _I, _I, _VP]),
     ("tge_kv_append_rope", _I, [_VP, _VP, _I, C.POINTER(RopeAppendArgs), _VP]),
+    ("tge_eligible_gqa", _I, [_I, _I, _I, _I, _I]),
+    ("tge_attention_group", _I, [C.POINTER(AttentionGroupArgs), _VP]),
     ("tge_batch_attention", _I, [_VP, _VP, _I, _VP, _VP, _VP]),
     ("tge_batch_set_sparse", _I, [_VP, _I, _I, _I, _I]),
     ("tge_rope_tables", _I, [_I, _I, C.c_float, C.c_float, _VP, _VP, _VP]),
@@ -165,6 +175,31 @@ def lib():
             fn.argtypes = args
         _lib = L
     return _lib
+
+
+def attention_group(pool, layer, kv_head, page_ids, first, count, queries, scale=None,
+                    stream=None):
+    """tge_attention_group for one KV head's query group over positions
+    [first, first + count): page_ids (host ints) and queries ([group][head_dim]
+    fp32, host) are copied to the device; returns (maxima, sums,
+    accumulators) as numpy arrays after synchronising."""
+    q = np.ascontiguousarray(queries, np.float32)
+    g = q.shape[0]
+    ids = DeviceArray.from_numpy(np.ascontiguousarray(page_ids, np.int32))
+    dq = DeviceArray.from_numpy(q)
+    m = DeviceArray((g,), np.float32)
+    sm = DeviceArray((g,), np.float32)
+    acc = DeviceArray((g, pool.head_dim), np.float32)
+    a = AttentionGroupArgs(pool.h, layer, kv_head, ids.ptr, first, count, dq.ptr, g,
+                           float(1.0 / np.sqrt(pool.head_dim)) if scale is None else float(scale),
+                           m.ptr, sm.ptr, acc.ptr)
+    try:
+        check(lib().tge_attention_group(C.byref(a), stream), "attention_group")
+        hip().sync()
+        return m.numpy(), sm.numpy(), acc.numpy()
+    finally:
+        for x in (ids, dq, m, sm, acc):
+            x.close()
 
 
 def check(status, what=""):

@@ -302,6 +302,58 @@ int tge_kv_gather(const tge_batch* batch, const tge_kv_pool* pool, int layer,
                   void* k_scales, void* v_scales, void* stream);
 
 /* ---------------------------------------------------------------------------
+ * Kernel level: the reference's GPU placement predicate and its
+ * attention_group plugin slot (KernelSet::attention_group,
+ * include/tge/core/dispatch.hpp:31-33), for a caller that keeps the
+ * reference's own schedule (Qwen2::attention_gqa, qwen2.cpp:1382-1467: KV
+ * heads x position chunks, then merge_gqa_chunks) and routes each chunk
+ * here instead of to attention_group_avx2.
+ * ------------------------------------------------------------------------ */
+#define TGE_GQA_MIN_SPAN 256 /* GpuThresholds::kGqaMinSpan, backend.hpp:49 */
+
+/* gpu::eligible_gqa (backend.hpp:170-174 with want_gqa_gpu :124-126, the
+ * predicate Qwen2::wants_gpu_gqa wraps, qwen2.cpp:786-795): 1 when the GPU
+ * was requested, more than one thread runs the schedule, the span reaches
+ * TGE_GQA_MIN_SPAN, the caller follows the grouped schedule (uses_gqa) and
+ * the attention is dense; else 0. A pure function (no device call): backend
+ * readiness is tge_backend_init's, as the reference's dispatcher adds
+ * use_gpu(). */
+int tge_eligible_gqa(int requested, int span, int threads, int follows_schedule,
+                     int dense_only);
+
+/* AttentionGroupArgs (kernels.hpp:262-283) over pages. The group_heads query
+ * heads of KV head `kv_head` (rows of `queries`, [group_heads][head_dim]
+ * fp32, device) attend to positions [first, first + count) of one session
+ * of layer `layer`, whose block table is page_ids (device, logical order,
+ * covering position first + count - 1). Per head the outputs are the
+ * reference group kernel's running online-softmax state (attention_group_
+ * scalar, attention_scalar.cpp:117-199): maxima[h] the largest score,
+ * sums[h] = sum of exp(score - max), accumulators[h][d] = sum of
+ * exp(score - max) * v[d], for the caller's chunk merge (merge_gqa_chunks,
+ * qwen2.cpp:1469-1522); count 0 gives (-inf, 0, 0). Scores are
+ * (q . k) * scale in fp32; K and V are dequantised in fp32. Rejects
+ * (TGE_ERR_INVALID) null pointers, a layer or KV head outside the pool,
+ * first < 0, count < 0 and group_heads outside 1..128. A page id outside
+ * the pool is not read: that call's outputs become NaN. Asynchronous on
+ * `stream`. */
+typedef struct {
+  const tge_kv_pool* pool;
+  int layer;
+  int kv_head;
+  const int* page_ids;  /* device */
+  int first;
+  int count;
+  const float* queries; /* device [group_heads][head_dim] */
+  int group_heads;
+  float scale;          /* the reference passes 1/sqrt(head_dim) */
+  float* maxima;        /* device [group_heads] */
+  float* sums;          /* device [group_heads] */
+  float* accumulators;  /* device [group_heads][head_dim] */
+} tge_attention_group_args;
+
+int tge_attention_group(const tge_attention_group_args* args, void* stream);
+
+/* ---------------------------------------------------------------------------
  * Fused bias + RoPE + append: the per-token sequence before the store in
  * forward / forward_batch / prefill_run (qwen2.cpp:2062-2093, 1665-1702,
  * 2286-2329): q += q_bias; k += k_bias; v += v_bias; apply_rope(q);

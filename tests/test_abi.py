@@ -272,3 +272,28 @@ def test_prefix_entry_points_reject_null_handles(tk):
     assert L.tge_qwen2_kv_shared_prefix_len(None, toks, 4) == tk.ERR_INVALID
     assert L.tge_qwen2_kv_attach_prefix(None, 0, toks, 4) == tk.ERR_INVALID
     assert L.tge_kv_copy_page(None, 0, 1, None) == tk.ERR_INVALID
+
+
+def test_eligible_gqa_matches_the_reference_predicate(tk):
+    # gpu::eligible_gqa (backend.hpp:170-174) = requested && want_gqa_gpu(span,
+    # threads) && follows_schedule && dense_only, want_gqa_gpu = threads > 1 &&
+    # span >= kGqaMinSpan (256), over every combination of the flags and the
+    # boundary values of span and threads.
+    L = tk.lib()
+    for req in (0, 1):
+        for follows in (0, 1):
+            for dense in (0, 1):
+                for span in (0, 1, 255, 256, 257, 100000):
+                    for threads in (0, 1, 2, 16):
+                        want = bool(req and threads > 1 and span >= 256 and follows and dense)
+                        got = L.tge_eligible_gqa(req, span, threads, follows, dense)
+                        assert got == int(want), (req, span, threads, follows, dense)
+
+
+def test_attention_group_argument_checks(tk):
+    # Rejected on the host, before any device work (the reference's
+    # invalid_argument rules, attention_scalar.cpp:11-44, restated for pages).
+    L = tk.lib()
+    assert L.tge_attention_group(None, None) == tk.ERR_INVALID
+    a = tk.AttentionGroupArgs()
+    assert L.tge_attention_group(C.byref(a), None) == tk.ERR_INVALID  # no pool
