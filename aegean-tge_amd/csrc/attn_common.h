@@ -201,6 +201,168 @@ __device__ __forceinline__ void wait_vmcnt_pages(int n) {
   }
 }
 
+// ---- In-kernel split merge (the last piece of a split record merges) ------
+// A piece of a split (session, KV head[, query tile]) writes its partial
+// (max, sum, acc) with the device-coherent cache policy sc1 (written
+// through, and read past, the XCD's non-coherent L2: the bits gfx950's
+// agent-scope relaxed atomics carry), waits for those stores, and bumps the
+// record's arrival counter; the piece that arrives last reads every partial
+// of the record (again with sc1) and writes the output rows, then re-arms
+// the counter for the next launch. No agent-scope fence is used: on gfx950
+// it writes back the XCD's whole L2.
+constexpr int kCohPolicy = 16;  // buffer cache-policy operand: sc1
+__device__ __forceinline__ void coh_store4(__amdgpu_buffer_rsrc_t rs, uint32_t off, float4_t v) {
+  __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4_t, v), rs, off, 0, kCohPolicy);
+}
+__device__ __forceinline__ void coh_store2(__amdgpu_buffer_rsrc_t rs, uint32_t off, float a, float b) {
+  typedef uint32_t u32x2_t __attribute__((ext_vector_type(2)));
+  __builtin_amdgcn_raw_buffer_store_b64(u32x2_t{__float_as_uint(a), __float_as_uint(b)}, rs, off, 0,
+                                        kCohPolicy);
+}
+__device__ __forceinline__ float4_t coh_load4(__amdgpu_buffer_rsrc_t rs, uint32_t off) {
+  return __builtin_bit_cast(float4_t, __builtin_amdgcn_raw_buffer_load_b128(rs, off, 0, kCohPolicy));
+}
+__device__ __forceinline__ float2 coh_load2(__amdgpu_buffer_rsrc_t rs, uint32_t off) {
+  const auto v = __builtin_amdgcn_raw_buffer_load_b64(rs, off, 0, kCohPolicy);
+  return make_float2(__uint_as_float(v[0]), __uint_as_float(v[1]));
+}
+
+// Partial slot `part`, row r: its accumulators (4 dims at d4) and its
+// (max, sum), written coherently.
+template <int D>
+__device__ __forceinline__ void store_partial_row(const AttnParams& p, int part, int r, int d4,
+                                                  float4_t acc) {
+  const auto rs = make_rsrc(p.part_o, 0x7fffffff);
+  coh_store4(rs, (uint32_t)((((size_t)part * p.rows_cap + r) * D + 4 * d4) * 4), acc);
+}
+__device__ __forceinline__ void store_partial_ml(const AttnParams& p, int part, int r, float m,
+                                                 float sum) {
+  const auto rs = make_rsrc(p.part_ml, 0x7fffffff);
+  coh_store2(rs, (uint32_t)(((size_t)part * p.rows_cap + r) * 8), m, sum);
+}
+
+// merge_gqa_chunks (qwen2.cpp:1469-1522) over the partial slots of record
+// `rr` (at most RMAX rows) by the 256 threads of one workgroup; slots with
+// no visible position are skipped, none at all gives zeros. `lds` is
+// scratch of at least 10 * RMAX floats.
+//   A. each row's common base M (the largest max of its visible slots) and
+//      total sum S, one thread per row folding the slots in order;
+//   B. the accumulators slot by slot: for a batch of slots the weights
+//      2^(max - M) go to LDS, then every thread loads its (row, 4 dims)
+//      pairs of those slots at once and adds them in slot order.
+template <int D, int RMAX>
+__device__ __forceinline__ void merge_record(const AttnParams& p, const ReduceRec& rr, float* lds) {
+  constexpr int NT = 256;
+  constexpr int L = D / 4;
+  constexpr int PJ = (RMAX * L + NT - 1) / NT;       // pairs per thread
+  constexpr int SB = PJ >= 32 ? 1 : 32 / PJ > 8 ? 8 : 32 / PJ;  // slots per batch of loads
+  float* lM = lds;              // [RMAX]
+  float* lS = lds + RMAX;       // [RMAX]
+  float* lw = lds + 2 * RMAX;   // [8][RMAX] weights of a batch of slots
+  const auto rs_o = make_rsrc(p.part_o, 0x7fffffff);
+  const auto rs_ml = make_rsrc(p.part_ml, 0x7fffffff);
+  const int n = rr.n_parts, rows = rr.rows;
+  const int t = threadIdx.x;
+  auto ml_off = [&](int k, int r) { return (uint32_t)((((size_t)(rr.first_part + k)) * p.rows_cap + r) * 8); };
+  // A.
+  if (t < rows) {
+    float m = -INFINITY, sum = 0.0f;
+    for (int k0 = 0; k0 < n; k0 += 8) {
+      float2 x[8];
+#pragma unroll
+      for (int i = 0; i < 8; ++i) x[i] = coh_load2(rs_ml, ml_off(min(k0 + i, n - 1), t));
+      float bm = m;
+#pragma unroll
+      for (int i = 0; i < 8; ++i)
+        if (k0 + i < n && x[i].y > 0.0f) bm = fmaxf(bm, x[i].x);
+      if (bm == -INFINITY) continue;
+      sum *= m == -INFINITY ? 0.0f : pow2i(m - bm);
+#pragma unroll
+      for (int i = 0; i < 8; ++i)
+        if (k0 + i < n && x[i].y > 0.0f) sum += x[i].y * pow2i(x[i].x - bm);
+      m = bm;
+    }
+    lM[t] = m;
+    lS[t] = sum;
+  }
+  __syncthreads();
+  // B.
+  float4_t acc[PJ];
+#pragma unroll
+  for (int j = 0; j < PJ; ++j) acc[j] = float4_t{0, 0, 0, 0};
+  for (int k0 = 0; k0 < n; k0 += 8) {
+    const int kn = min(8, n - k0);
+    for (int i = t; i < kn * rows; i += NT) {
+      const int kk = i / rows, r = i - kk * rows;
+      const float2 x = coh_load2(rs_ml, ml_off(k0 + kk, r));
+      const float mm = lM[r];
+      lw[kk * RMAX + r] = x.y > 0.0f && mm != -INFINITY ? pow2i(x.x - mm) : 0.0f;
+    }
+    __syncthreads();
+    for (int kb = 0; kb < kn; kb += SB) {
+      float4_t v[SB][PJ];
+#pragma unroll
+      for (int b = 0; b < SB; ++b) {
+        const int k = k0 + min(kb + b, kn - 1);
+#pragma unroll
+        for (int j = 0; j < PJ; ++j) {
+          const int pair = min(t + NT * j, rows * L - 1);
+          const int r = pair / L, d4 = pair - r * L;
+          v[b][j] = coh_load4(rs_o, (uint32_t)(((((size_t)(rr.first_part + k)) * p.rows_cap + r) * D + 4 * d4) * 4));
+        }
+      }
+#pragma unroll
+      for (int b = 0; b < SB; ++b) {
+        if (kb + b >= kn) break;
+#pragma unroll
+        for (int j = 0; j < PJ; ++j) {
+          const int pair = t + NT * j;
+          if (pair < rows * L) acc[j] += v[b][j] * lw[(kb + b) * RMAX + pair / L];
+        }
+      }
+    }
+    __syncthreads();  // the weights of this batch are read
+  }
+  const int q_stride = p.q_heads * D;
+#pragma unroll
+  for (int j = 0; j < PJ; ++j) {
+    const int pair = t + NT * j;
+    if (pair >= rows * L) continue;
+    const int r = pair / L, d4 = pair - r * L;
+    const float sum = lS[r];
+    const int qi = rr.row_begin + r / rr.rows_per_query;
+    const int head = rr.head_base + r % rr.rows_per_query;
+    float4_t res = float4_t{0, 0, 0, 0};
+    if (sum > 0.0f) res = div4(acc[j], sum);
+    *reinterpret_cast<float4_t*>(p.out + (size_t)(rr.q_row + qi) * q_stride + (size_t)head * D + 4 * d4) = res;
+  }
+}
+
+// Called by every thread of a (256-thread) workgroup once its piece of
+// split record `red` has written its partial rows (coherently): counts the
+// arrival, and the last piece merges the record and re-arms its counter.
+// `flag` is an LDS int of the workgroup, `scratch` 10 * RMAX LDS floats that
+// nothing else uses meanwhile. Waits for all of this workgroup's memory
+// operations (loads in flight included).
+template <int D, int RMAX>
+__device__ __forceinline__ void arrive_and_merge(const AttnParams& p, int red, int* flag, float* scratch) {
+  const ReduceRec rr = p.reduce[red];
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup");
+  wait_vmcnt<0>();  // this wave's partial stores have completed
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    const int prev = __hip_atomic_fetch_add(p.counters + red, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    *flag = prev == rr.n_parts - 1;
+  }
+  __syncthreads();
+  const bool last = *flag != 0;
+  __syncthreads();  // every wave has read the flag before a later arrival rewrites it
+  if (!last) return;
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup");
+  merge_record<D, RMAX>(p, rr, scratch);
+  if (threadIdx.x == 0) __hip_atomic_store(p.counters + red, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
 // K operand (16x16x32 A) of 32-dim block pp.
 template <int FMT, bool SF32, int D>
 __device__ __forceinline__ half8_t k_operand(const PageRegs<FMT, SF32, D>& r, int pp) {

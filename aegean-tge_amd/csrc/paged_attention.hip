@@ -86,7 +86,10 @@ constexpr int kLdsBytes = 160 * 1024;  // LDS of one CU (gfx950)
 // Launch shape of a decode variant: W waves per workgroup at WPE waves per
 // SIMD (PER_CU = 4*WPE/W workgroups per CU), NB ring slots per wave, and the
 // Q^T operands of up to MAXU units resident in LDS.
-template <int FMT, bool SF32, int D, int NRG, bool SP = false>
+// MIX: the decode role of the mixed-step kernel (paged_mixed_kernel below):
+// always four waves (its workgroups are also block-prefill tiles of 256
+// threads) at two per SIMD (one for more than 32 rows).
+template <int FMT, bool SF32, int D, int NRG, bool SP = false, bool MIX = false>
 struct DecodeCfg {
   static constexpr int WANT = SP ? TGE_DECODE_WPE_SPARSE : TGE_DECODE_WPE;
   static constexpr int SLOT = Ring<FMT, SF32, D>::SLOT;
@@ -103,8 +106,8 @@ struct DecodeCfg {
   // fit (f16 pages at head_dim 128).
   static constexpr bool kBig = NRG > 2;
   static constexpr bool kFits = nb_fit(TGE_DECODE_WAVES, WANT) >= 2;
-  static constexpr int W = kBig ? 4 : (kFits ? TGE_DECODE_WAVES : 8);
-  static constexpr int WPE = kBig ? 1 : (kFits ? WANT : 2);
+  static constexpr int W = MIX ? 4 : (kBig ? 4 : (kFits ? TGE_DECODE_WAVES : 8));
+  static constexpr int WPE = kBig ? 1 : (MIX ? 2 : (kFits ? WANT : 2));
   static constexpr int PER_CU = 4 * WPE / W > 1 ? 4 * WPE / W : 1;  // workgroups per CU
   static constexpr int LDS = kLdsBytes / PER_CU - 256;             // one workgroup's share
   static constexpr int NB = nb_fit(W, WPE) > TGE_DECODE_MAX_SLOTS ? TGE_DECODE_MAX_SLOTS : nb_fit(W, WPE);
@@ -115,14 +118,15 @@ struct DecodeCfg {
   static_assert(8 * (D + 4) * 4 <= SLOT, "merge staging fits a slot");
 };
 
-template <int FMT, bool SF32, int D, int NRG, bool SP>
+template <int FMT, bool SF32, int D, int NRG, bool SP, bool MIX = false>
 struct DecodeShared {
-  using C = DecodeCfg<FMT, SF32, D, NRG, SP>;
+  using C = DecodeCfg<FMT, SF32, D, NRG, SP, MIX>;
   static constexpr int ROWS = 16 * NRG;
   static constexpr int MERGE_FLOATS = 2 * C::W * ROWS + 2 * ROWS + C::W;
   alignas(16) char ring[C::W * C::NB * C::SLOT];
   alignas(16) half8_t q[C::MAXU * NRG * (D / 32) * 64];  // [unit][rg][pp][lane]
   alignas(16) float merge[MERGE_FLOATS];
+  int flag;  // arrival broadcast of the in-kernel split merge
 };
 
 typedef const __attribute__((address_space(4))) WorkRec sconst_work;
@@ -158,6 +162,7 @@ __device__ __forceinline__ WorkRec load_work(const sconst_work* w) {
   r.ctx = q[9];
   r.q_row = q[10];
   r.table_off = q[11];
+  r.red = q[12];
   return r;
 }
 
@@ -182,11 +187,11 @@ struct PageFifo {
   __device__ __forceinline__ int front() const { return t[0]; }
 };
 
-template <int FMT, bool SF32, int D, int NRG, int W, int WPE, bool SP>
-__global__ __launch_bounds__(64 * W) __attribute__((amdgpu_waves_per_eu(WPE, WPE)))
-void paged_decode_kernel(AttnParams p) {
-  using CFG = DecodeCfg<FMT, SF32, D, NRG, SP>;
-  using SH = DecodeShared<FMT, SF32, D, NRG, SP>;
+template <int FMT, bool SF32, int D, int NRG, int W, int WPE, bool SP, bool MIX>
+__device__ __forceinline__ void decode_body(const AttnParams& p,
+                                            DecodeShared<FMT, SF32, D, NRG, SP, MIX>& sh,
+                                            const int group) {
+  using CFG = DecodeCfg<FMT, SF32, D, NRG, SP, MIX>;
   using U = Unit<FMT, SF32, D, NRG>;
   using RG = Ring<FMT, SF32, D>;
   static_assert(CFG::W == W && CFG::WPE == WPE, "launch shape");
@@ -196,10 +201,9 @@ void paged_decode_kernel(AttnParams p) {
   constexpr int NT = D / 16;
   constexpr int ROWS = 16 * NRG;
   constexpr int QUNIT = NRG * NP * 64;  // half8 entries of one unit's Q^T
-  __shared__ SH sh;
 
-  const int first = p.wg_first[blockIdx.x];
-  const int last = p.wg_first[blockIdx.x + 1];
+  const int first = p.wg_first[group];
+  const int last = p.wg_first[group + 1];
   if (first >= last) return;  // the whole workgroup leaves together
 
   const int lane = threadIdx.x & 63;
@@ -476,6 +480,9 @@ void paged_decode_kernel(AttnParams p) {
             float4_t res = float4_t{0, 0, 0, 0};
             if (sum > 0.0f) res = div4(acc, sum);
             *reinterpret_cast<float4_t*>(p.out + (size_t)(cw.q_row + qi) * q_stride + (size_t)head * D + 4 * d4) = res;
+          } else if (MIX && p.counters) {  // merged in this launch: coherent stores
+            store_partial_row<D>(p, cw.part, r, d4, acc);
+            if (d4 == 0) store_partial_ml(p, cw.part, r, lds_mm[r], sum);
           } else {
             *reinterpret_cast<float4_t*>(p.part_o + ((size_t)cw.part * p.rows_cap + r) * D + 4 * d4) = acc;
             if (d4 == 0) {
@@ -533,6 +540,10 @@ void paged_decode_kernel(AttnParams p) {
       int fs = head + count;
       fs = fs >= NB ? fs - NB : fs;
       finalize(fs);
+      if constexpr (MIX) {
+        // (the merge area is free again after finalize)
+        if (p.counters && cw.part >= 0) arrive_and_merge<D, ROWS>(p, cw.red, &sh.flag, sh.merge);
+      }
       next_unit();
     }
   };
@@ -569,6 +580,13 @@ void paged_decode_kernel(AttnParams p) {
   }
 }
 
+template <int FMT, bool SF32, int D, int NRG, int W, int WPE, bool SP>
+__global__ __launch_bounds__(64 * W) __attribute__((amdgpu_waves_per_eu(WPE, WPE)))
+void paged_decode_kernel(AttnParams p) {
+  __shared__ DecodeShared<FMT, SF32, D, NRG, SP> sh;
+  decode_body<FMT, SF32, D, NRG, W, WPE, SP, false>(p, sh, blockIdx.x);
+}
+
 // ---------------------------------------------------------------------------
 // Block-prefill kernel: one workgroup per (session, KV head, query tile,
 // page split). The tile holds up to 128 rows, (query, head) pairs of the KV
@@ -587,11 +605,13 @@ struct PrefillShared {
   static constexpr int NB = NB_FIT > 4 ? 4 : NB_FIT;
   static_assert(NB >= 2, "the prefill ring needs two tiles");
   alignas(16) char ring[NB * TILE];
+  int flag;  // arrival broadcast of the in-kernel split merge
 };
 
-template <int FMT, bool SF32, int D, int WPE, bool SP>
-__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(WPE, WPE)))
-void paged_prefill_kernel(AttnParams p) {
+// MERGE: split tiles are merged in the launch (the mixed-step kernel).
+template <int FMT, bool SF32, int D, int WPE, bool SP, bool MERGE = false>
+__device__ __forceinline__ void prefill_body(const AttnParams& p, PrefillShared<FMT, SF32, D, WPE>& sh,
+                                             const int item) {
   constexpr int NRG = 2;  // 32 rows per wave
   using SH = PrefillShared<FMT, SF32, D, WPE>;
   using U = Unit<FMT, SF32, D, NRG>;
@@ -600,9 +620,8 @@ void paged_prefill_kernel(AttnParams p) {
   constexpr int NB = SH::NB;
   constexpr int NP = D / 32;
   constexpr int NT = D / 16;
-  __shared__ SH sh;
 
-  const WorkRec w = load_work((const sconst_work*)p.work + blockIdx.x);
+  const WorkRec w = load_work((const sconst_work*)p.work + item);
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int col = lane & 15;
@@ -700,33 +719,89 @@ void paged_prefill_kernel(AttnParams p) {
       }
     }
   }
-  if (!has_rows) return;
-
   // Write this wave's rows: normalised output, or the split's partial state.
+  if (has_rows) {
 #pragma unroll
-  for (int rg = 0; rg < NRG; ++rg) {
-    const int r = row0 + rg * 16 + col;
-    if (r >= w.rows) continue;
-    const float sum = u.l4[rg][0];
-    if (w.part < 0) {
-      const int qi = w.row_begin + r / w.rows_per_query;
-      const int head = w.head_base + r % w.rows_per_query;
-      float* op = p.out + (size_t)(w.q_row + qi) * q_stride + (size_t)head * D + 4 * grp;
+    for (int rg = 0; rg < NRG; ++rg) {
+      const int r = row0 + rg * 16 + col;
+      if (r >= w.rows) continue;
+      const float sum = u.l4[rg][0];
+      const float mx = u.thr[rg] == -INFINITY ? -INFINITY : u.base[rg];
+      if (w.part < 0) {
+        const int qi = w.row_begin + r / w.rows_per_query;
+        const int head = w.head_base + r % w.rows_per_query;
+        float* op = p.out + (size_t)(w.q_row + qi) * q_stride + (size_t)head * D + 4 * grp;
 #pragma unroll
-      for (int t = 0; t < NT; ++t) {
-        float4_t res = float4_t{0, 0, 0, 0};
-        if (sum > 0.0f) res = div4(u.o[rg][t], sum);
-        *reinterpret_cast<float4_t*>(op + 16 * t) = res;
-      }
-    } else {
-      float* po = p.part_o + ((size_t)w.part * p.rows_cap + r) * D + 4 * grp;
+        for (int t = 0; t < NT; ++t) {
+          float4_t res = float4_t{0, 0, 0, 0};
+          if (sum > 0.0f) res = div4(u.o[rg][t], sum);
+          *reinterpret_cast<float4_t*>(op + 16 * t) = res;
+        }
+      } else if (MERGE && p.counters) {  // merged in this launch: coherent stores
 #pragma unroll
-      for (int t = 0; t < NT; ++t) *reinterpret_cast<float4_t*>(po + 16 * t) = u.o[rg][t];
-      if (grp == 0) {
-        p.part_ml[((size_t)w.part * p.rows_cap + r) * 2] = u.thr[rg] == -INFINITY ? -INFINITY : u.base[rg];
-        p.part_ml[((size_t)w.part * p.rows_cap + r) * 2 + 1] = sum;
+        for (int t = 0; t < NT; ++t) store_partial_row<D>(p, w.part, r, 4 * t + grp, u.o[rg][t]);
+        if (grp == 0) store_partial_ml(p, w.part, r, mx, sum);
+      } else {
+        float* po = p.part_o + ((size_t)w.part * p.rows_cap + r) * D + 4 * grp;
+#pragma unroll
+        for (int t = 0; t < NT; ++t) *reinterpret_cast<float4_t*>(po + 16 * t) = u.o[rg][t];
+        if (grp == 0) {
+          p.part_ml[((size_t)w.part * p.rows_cap + r) * 2] = mx;
+          p.part_ml[((size_t)w.part * p.rows_cap + r) * 2 + 1] = sum;
+        }
       }
     }
+  }
+  // the last piece of a split tile merges it (every wave takes part)
+  if constexpr (MERGE) {
+    // (every tile of the ring is consumed: its LDS is the merge scratch)
+    if (p.counters && w.part >= 0)
+      arrive_and_merge<D, kPrefillRows>(p, w.red, &sh.flag, reinterpret_cast<float*>(sh.ring));
+  }
+}
+
+template <int FMT, bool SF32, int D, int WPE, bool SP>
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(WPE, WPE)))
+void paged_prefill_kernel(AttnParams p) {
+  __shared__ PrefillShared<FMT, SF32, D, WPE> sh;
+  prefill_body<FMT, SF32, D, WPE, SP>(p, sh, blockIdx.x);
+}
+
+// ---------------------------------------------------------------------------
+// Mixed-step kernel (continuous batching: some sessions decoding, some
+// prefilling a chunk, forward_batch qwen2.cpp:1613-1747): one launch whose
+// first n_dec workgroups run the decode role over the decode plan's
+// persistent shares and whose remaining workgroups are block-prefill tiles
+// of the prefill plan; the tiles take over each CU's slots as its decode
+// workgroups finish, so the decode tail overlaps the prefill. Split pieces of
+// either kind are merged in the same launch by the last piece to arrive.
+// The two roles share the workgroup's LDS (a union) and its register budget.
+// ---------------------------------------------------------------------------
+template <int FMT, bool SF32, int D, int NRG>
+struct MixCfg {
+  using DC = DecodeCfg<FMT, SF32, D, NRG, false, true>;
+  static constexpr int WPE = DC::WPE;
+};
+
+template <int FMT, bool SF32, int D, int NRG>
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(MixCfg<FMT, SF32, D, NRG>::WPE,
+                                                                     MixCfg<FMT, SF32, D, NRG>::WPE)))
+void paged_mixed_kernel(AttnParams dec, AttnParams pf, int n_dec) {
+  using DC = typename MixCfg<FMT, SF32, D, NRG>::DC;
+  constexpr int WPE = MixCfg<FMT, SF32, D, NRG>::WPE;
+  static_assert(DC::W == 4, "both roles run 256 threads");
+  static_assert(DecodeShared<FMT, SF32, D, NRG, false, true>::MERGE_FLOATS >= 10 * 16 * NRG,
+                "the decode merge area holds the split merge's scratch");
+  static_assert(sizeof(PrefillShared<FMT, SF32, D, WPE>::ring) >= 10 * kPrefillRows * sizeof(float),
+                "the prefill ring holds the split merge's scratch");
+  __shared__ union {
+    DecodeShared<FMT, SF32, D, NRG, false, true> d;
+    PrefillShared<FMT, SF32, D, WPE> p;
+  } sh;
+  if ((int)blockIdx.x < n_dec) {
+    decode_body<FMT, SF32, D, NRG, 4, WPE, false, true>(dec, sh.d, blockIdx.x);
+  } else {
+    prefill_body<FMT, SF32, D, WPE, false, true>(pf, sh.p, blockIdx.x - n_dec);
   }
 }
 
@@ -921,6 +996,62 @@ hipError_t launch_prefill_d(int n_units, const AttnParams& p, hipStream_t stream
                        dim3(256), 0, stream, p);
   }
   return hipGetLastError();
+}
+
+template <int FMT, bool SF32, int D>
+hipError_t launch_mixed_d(int row_groups, int n_dec, int n_pf, const AttnParams& dec,
+                          const AttnParams& pf, hipStream_t stream) {
+  const dim3 grid((unsigned)(n_dec + n_pf)), block(256);
+  switch (row_groups) {
+    case 1: hipLaunchKernelGGL((paged_mixed_kernel<FMT, SF32, D, 1>), grid, block, 0, stream, dec, pf, n_dec); break;
+    case 2: hipLaunchKernelGGL((paged_mixed_kernel<FMT, SF32, D, 2>), grid, block, 0, stream, dec, pf, n_dec); break;
+    case 3: hipLaunchKernelGGL((paged_mixed_kernel<FMT, SF32, D, 3>), grid, block, 0, stream, dec, pf, n_dec); break;
+    case 4: hipLaunchKernelGGL((paged_mixed_kernel<FMT, SF32, D, 4>), grid, block, 0, stream, dec, pf, n_dec); break;
+    default: return hipErrorInvalidValue;
+  }
+  return hipGetLastError();
+}
+
+hipError_t launch_mixed(int format, int scale_f32, int head_dim, int row_groups, int n_dec,
+                        int n_pf, const AttnParams& dec, const AttnParams& pf, hipStream_t stream) {
+  if (n_dec + n_pf <= 0) return hipSuccess;
+  if (!dec.wg_first || !dec.counters || !pf.counters) return hipErrorInvalidValue;
+  if (format == kF16) {
+    if (head_dim == 64) return launch_mixed_d<kF16, false, 64>(row_groups, n_dec, n_pf, dec, pf, stream);
+    if (head_dim == 128) return launch_mixed_d<kF16, false, 128>(row_groups, n_dec, n_pf, dec, pf, stream);
+  } else if (format == kI8) {
+    if (head_dim == 64)
+      return scale_f32 ? launch_mixed_d<kI8, true, 64>(row_groups, n_dec, n_pf, dec, pf, stream)
+                       : launch_mixed_d<kI8, false, 64>(row_groups, n_dec, n_pf, dec, pf, stream);
+    if (head_dim == 128)
+      return scale_f32 ? launch_mixed_d<kI8, true, 128>(row_groups, n_dec, n_pf, dec, pf, stream)
+                       : launch_mixed_d<kI8, false, 128>(row_groups, n_dec, n_pf, dec, pf, stream);
+  }
+  return hipErrorInvalidValue;
+}
+
+template <int FMT, bool SF32, int D>
+int mixed_blocks_d(int row_groups) {
+  int n = 0;
+  hipError_t e = hipErrorInvalidValue;
+  switch (row_groups) {
+    case 1: e = hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, paged_mixed_kernel<FMT, SF32, D, 1>, 256, 0); break;
+    case 2: e = hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, paged_mixed_kernel<FMT, SF32, D, 2>, 256, 0); break;
+    case 3: e = hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, paged_mixed_kernel<FMT, SF32, D, 3>, 256, 0); break;
+    case 4: e = hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, paged_mixed_kernel<FMT, SF32, D, 4>, 256, 0); break;
+    default: break;
+  }
+  return e == hipSuccess ? n : 0;
+}
+
+int mixed_blocks_per_cu(int format, int scale_f32, int head_dim, int row_groups) {
+  if (format == kF16) {
+    return head_dim == 64 ? mixed_blocks_d<kF16, false, 64>(row_groups)
+                          : mixed_blocks_d<kF16, false, 128>(row_groups);
+  }
+  if (head_dim == 64)
+    return scale_f32 ? mixed_blocks_d<kI8, true, 64>(row_groups) : mixed_blocks_d<kI8, false, 64>(row_groups);
+  return scale_f32 ? mixed_blocks_d<kI8, true, 128>(row_groups) : mixed_blocks_d<kI8, false, 128>(row_groups);
 }
 
 hipError_t launch_prefill(int format, int scale_f32, int head_dim, int n_units,

@@ -167,6 +167,10 @@ struct tge_batch {
   // whose rows fit a decode unit, the prefill kernel over the others.
   AttnPlan mix_decode, mix_prefill;
   bool mix_built = false;
+  bool mix_one = false;  // dense: one paged_mixed_kernel launch, splits merged in it
+  // arrival counters of the mixed launch: the decode plan's records, then
+  // the prefill plan's (zero between launches)
+  tge::plan::Scratch mix_counters;
   // Static sparse subset of every attention call (stride 0: dense).
   int sp_sink = 0, sp_window = 0, sp_stride = 0;
 
@@ -183,6 +187,7 @@ struct tge_batch {
 
   ~tge_batch() {
     image.release(g_mem);
+    mix_counters.release(g_mem);
     for (auto& t : prof)
       for (hipEvent_t e : t)
         if (e) (void)hipEventDestroy(e);
@@ -364,19 +369,39 @@ tge::plan::Residency resident_groups(int format, int scale_f32, int head_dim, in
   return r;
 }
 
+// Resident workgroups of the mixed-step kernel (cached): its decode role's
+// persistent shares are cut for all of them.
+tge::plan::Residency resident_groups_mixed(int format, int scale_f32, int head_dim, int row_groups) {
+  static std::mutex mu;
+  static std::vector<std::pair<int, tge::plan::Residency>> cache;
+  const int key = ((format * 2 + scale_f32) * 256 + head_dim) * 8 + row_groups;
+  std::lock_guard<std::mutex> lock(mu);
+  for (const auto& kv : cache)
+    if (kv.first == key) return kv.second;
+  const int cus = device_cus();
+  int per_cu = tge::mixed_blocks_per_cu(format, scale_f32, head_dim, row_groups);
+  if (per_cu <= 0) per_cu = 1;
+  const tge::plan::Residency r{per_cu * cus, cus};
+  cache.emplace_back(key, r);
+  return r;
+}
+
 // Builds and uploads a decode plan over the sessions `only` selects
 // (0 all, 1 those a decode unit holds), balanced for the decode kernel the
-// batch's current sparse setting launches.
-int build_decode_plan(tge_batch* b, const tge_kv_pool* p, AttnPlan& pl, int only, hipStream_t st) {
+// batch's current sparse setting launches (`mixed`: the decode role of the
+// mixed-step kernel).
+int build_decode_plan(tge_batch* b, const tge_kv_pool* p, AttnPlan& pl, int only, hipStream_t st,
+                      bool mixed = false) {
   int max_rows = 0;
   for (const auto& sr : b->step.sessions)
     if (tge::plan::take_session(b->step, sr, only))
       max_rows = std::max(max_rows, sr.n_new * b->step.group);
   const int rg = std::max(1, std::min(4, (max_rows + 15) / 16));
   const bool sparse = b->sp_stride > 0;
+  const int sf32 = p->desc.scale_format == TGE_SCALE_F32;
   tge::plan::build_decode(b->step,
-                          resident_groups(p->desc.format, p->desc.scale_format == TGE_SCALE_F32,
-                                          b->step.head_dim, rg, sparse),
+                          mixed ? resident_groups_mixed(p->desc.format, sf32, b->step.head_dim, rg)
+                                : resident_groups(p->desc.format, sf32, b->step.head_dim, rg, sparse),
                           pl.lists, only);
   pl.sparse = sparse;
   return upload_plan(pl, b->step.head_dim, st);
@@ -556,28 +581,35 @@ tge::AttnParams attn_params(const tge_batch* b, const tge_kv_pool* p, int layer,
   return a;
 }
 
+// The next triple of timing events of an attention call while profiling is
+// on (created on demand and reused), else null.
+int profile_events(tge_batch* b, std::array<hipEvent_t, 3>** ev) {
+  *ev = nullptr;
+  if (!b->profiling) return TGE_OK;
+  if (b->prof_used == b->prof.size()) {
+    std::array<hipEvent_t, 3> t{nullptr, nullptr, nullptr};
+    for (hipEvent_t& e : t) {
+      const hipError_t err = hipEventCreate(&e);
+      if (err != hipSuccess) {
+        for (hipEvent_t x : t)
+          if (x) (void)hipEventDestroy(x);
+        return fail(TGE_ERR_DEVICE, std::string("hipEventCreate: ") + hipGetErrorString(err));
+      }
+    }
+    b->prof.push_back(t);
+  }
+  *ev = &b->prof[b->prof_used++];
+  return TGE_OK;
+}
+
 int run_attention(const tge_batch* b, const tge_kv_pool* p, int layer, const float* q,
                   float* out, void* stream, const AttnPlan& pl, bool decode) {
   hipStream_t st = static_cast<hipStream_t>(stream);
   const tge::AttnParams a = attn_params(b, p, layer, q, out, pl);
   std::array<hipEvent_t, 3>* ev = nullptr;
-  if (b->profiling) {
-    tge_batch* mb = const_cast<tge_batch*>(b);
-    if (mb->prof_used == mb->prof.size()) {
-      std::array<hipEvent_t, 3> t{nullptr, nullptr, nullptr};
-      for (hipEvent_t& e : t) {
-        const hipError_t err = hipEventCreate(&e);
-        if (err != hipSuccess) {
-          for (hipEvent_t x : t)
-            if (x) (void)hipEventDestroy(x);
-          return fail(TGE_ERR_DEVICE, std::string("hipEventCreate: ") + hipGetErrorString(err));
-        }
-      }
-      mb->prof.push_back(t);
-    }
-    ev = &mb->prof[mb->prof_used++];
-    TGE_HIP(hipEventRecord((*ev)[0], st));
-  }
+  const int ps = profile_events(const_cast<tge_batch*>(b), &ev);
+  if (ps != TGE_OK) return ps;
+  if (ev) TGE_HIP(hipEventRecord((*ev)[0], st));
   if (decode) {
     TGE_HIP(tge::launch_decode(p->desc.format, p->desc.scale_format == TGE_SCALE_F32, b->step.head_dim,
                                pl.lists.row_groups, pl.lists.groups, a, st));
@@ -767,20 +799,55 @@ int tge_batch_attention(const tge_batch* b, const tge_kv_pool* p, int layer, con
   if (n_pf == 0) return tge_decode_attention(b, p, layer, q, out, stream);
   if (n_dec == 0) return tge_prefill_attention(b, p, layer, q, out, stream);
   hipStream_t st = static_cast<hipStream_t>(stream);
-  if (!mb->mix_built || mb->mix_decode.sparse != (b->sp_stride > 0)) {
-    // Built on first use after each plan, reused by every layer.
-    s = build_decode_plan(mb, p, mb->mix_decode, 1, st);
+  const bool sparse = b->sp_stride > 0;
+  if (!mb->mix_built || mb->mix_decode.sparse != sparse) {
+    // Built on first use after each plan, reused by every layer. Dense
+    // steps run as one launch (the decode shares balanced for the mixed
+    // kernel); a static sparse subset keeps the two kernels.
+    mb->mix_one = !sparse;
+    s = build_decode_plan(mb, p, mb->mix_decode, 1, st, mb->mix_one);
     if (s != TGE_OK) return s;
     tge::plan::build_prefill(mb->step, device_cus(), mb->mix_prefill.lists, 2);
     s = upload_plan(mb->mix_prefill, b->step.head_dim, st);
     if (s != TGE_OK) return s;
+    if (mb->mix_one) {
+      const size_t n = mb->mix_decode.lists.reduce.size() + mb->mix_prefill.lists.reduce.size();
+      const size_t had = mb->mix_counters.bytes;
+      s = mb->mix_counters.reserve(g_mem, std::max<size_t>(n, 1) * sizeof(int), st);
+      if (s != TGE_OK) return s;
+      if (mb->mix_counters.bytes != had)
+        TGE_HIP(hipMemsetAsync(mb->mix_counters.dev, 0, mb->mix_counters.bytes, st));
+    }
     mb->mix_built = true;
   }
-  // Long chunks first: the prefill tiles are MFMA-bound, the persistent
-  // decode workgroups HBM-bound; both write disjoint rows of `out`.
-  s = run_attention(b, p, layer, q, out, stream, b->mix_prefill, false);
+  if (!b->mix_one) {
+    // Long chunks first: the prefill tiles are MFMA-bound, the persistent
+    // decode workgroups HBM-bound; both write disjoint rows of `out`.
+    s = run_attention(b, p, layer, q, out, stream, b->mix_prefill, false);
+    if (s != TGE_OK) return s;
+    return run_attention(b, p, layer, q, out, stream, b->mix_decode, true);
+  }
+  // One launch: the decode shares first, then the prefill tiles; each
+  // plan's split records are merged in the launch (arrival counters).
+  tge::AttnParams dec = attn_params(b, p, layer, q, out, b->mix_decode);
+  tge::AttnParams pf = attn_params(b, p, layer, q, out, b->mix_prefill);
+  int* counters = reinterpret_cast<int*>(b->mix_counters.dev);
+  dec.reduce = reinterpret_cast<const tge::ReduceRec*>(b->mix_decode.image.dev + b->mix_decode.off_reduce);
+  dec.counters = counters;
+  pf.reduce = reinterpret_cast<const tge::ReduceRec*>(b->mix_prefill.image.dev + b->mix_prefill.off_reduce);
+  pf.counters = counters + b->mix_decode.lists.reduce.size();
+  std::array<hipEvent_t, 3>* ev = nullptr;
+  s = profile_events(mb, &ev);
   if (s != TGE_OK) return s;
-  return run_attention(b, p, layer, q, out, stream, b->mix_decode, true);
+  if (ev) TGE_HIP(hipEventRecord((*ev)[0], st));
+  TGE_HIP(tge::launch_mixed(p->desc.format, p->desc.scale_format == TGE_SCALE_F32, b->step.head_dim,
+                            b->mix_decode.lists.row_groups, b->mix_decode.lists.groups,
+                            (int)b->mix_prefill.lists.work.size(), dec, pf, st));
+  if (ev) {
+    TGE_HIP(hipEventRecord((*ev)[1], st));
+    TGE_HIP(hipEventRecord((*ev)[2], st));
+  }
+  return TGE_OK;
 }
 
 }  // extern "C"

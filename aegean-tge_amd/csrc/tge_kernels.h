@@ -64,6 +64,11 @@ struct AttnParams {
   // sp_sink + sp_window keep positions < sp_sink, every sp_stride-th one
   // from sp_sink on, and the last sp_window.
   int sp_sink, sp_window, sp_stride;
+  // In-kernel split merge (null: partials are merged by split_reduce_kernel
+  // after the launch): the plan's reduction records and one arrival counter
+  // each (zero at launch; each record's last piece re-arms it).
+  const ReduceRec* reduce;
+  int* counters;
 };
 
 struct ReduceParams {
@@ -122,6 +127,12 @@ hipError_t launch_kv_gather(int format, const GatherParams& p, hipStream_t strea
 // persistent workgroups (a fixed number per CU, see DecodeCfg).
 hipError_t launch_decode(int format, int scale_f32, int head_dim, int row_groups, int n_groups,
                          const AttnParams& p, hipStream_t stream);
+// Mixed step in one launch (paged_mixed_kernel): n_dec persistent decode
+// workgroups over `dec`'s plan, then n_pf block-prefill tiles of `pf`'s
+// plan; both plans merge their splits in the launch (counters required).
+hipError_t launch_mixed(int format, int scale_f32, int head_dim, int row_groups, int n_dec,
+                        int n_pf, const AttnParams& dec, const AttnParams& pf, hipStream_t stream);
+int mixed_blocks_per_cu(int format, int scale_f32, int head_dim, int row_groups);
 // Block prefill: one workgroup per work item (tiles of up to 128 rows).
 hipError_t launch_prefill(int format, int scale_f32, int head_dim, int n_units,
                           const AttnParams& p, hipStream_t stream);

@@ -37,9 +37,11 @@ struct WorkRec {
   int ctx;
   int q_row;
   int table_off;
+  int red;  // reduction record of a split item (its partial's merge), or -1
+  int pad[3];
 };
 
-static_assert(sizeof(WorkRec) == 12 * sizeof(int), "WorkRec is read as 12 ints");
+static_assert(sizeof(WorkRec) == 16 * sizeof(int), "WorkRec is read as 16 ints");
 
 // One row set whose context was split over several units.
 struct ReduceRec {

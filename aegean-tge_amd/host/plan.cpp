@@ -247,6 +247,7 @@ void build_decode(const Step& b, Residency res, AttnLists& pl, int only) {
       it.ctx = sr.ctx;
       it.q_row = sr.q_row;
       it.table_off = sr.table_off;
+      it.red = -1;
       pl.work.push_back(it);
       seg_of.push_back((int)si);
       started = true;
@@ -280,7 +281,10 @@ void build_decode(const Step& b, Residency res, AttnLists& pl, int only) {
       r.first_part = pl.parts;
       r.q_row = w0.q_row;
       r.n_parts = n;
-      for (std::size_t k = i; k < j; ++k) pl.work[k].part = pl.parts++;
+      for (std::size_t k = i; k < j; ++k) {
+        pl.work[k].part = pl.parts++;
+        pl.work[k].red = (int)pl.reduce.size();
+      }
       pl.reduce.push_back(r);
     }
     i = j;
@@ -299,6 +303,7 @@ void add_units(std::vector<WorkRec>& work, std::vector<ReduceRec>& red, int& par
     base.page_begin = 0;
     base.page_end = pages;
     base.part = -1;
+    base.red = -1;
     work.push_back(base);
     return;
   }
@@ -317,6 +322,7 @@ void add_units(std::vector<WorkRec>& work, std::vector<ReduceRec>& red, int& par
     w.page_begin = b;
     w.page_end = std::min(pages, b + chunk);
     w.part = parts++;
+    w.red = (int)red.size();
     work.push_back(w);
     ++r.n_parts;
   }

@@ -144,7 +144,7 @@ void check_lists(const Step& st, const AttnLists& l, int only, bool prefill) {
         const int n = (int)items.size();
         max_splits = std::max(max_splits, n);
         if (n == 1) {
-          REQUIRE(items[0]->part == -1, "an unsplit item writes the output");
+          REQUIRE(items[0]->part == -1 && items[0]->red == -1, "an unsplit item writes the output");
         } else {
           // one reduction record with n consecutive partial slots
           const ReduceRec* rr = nullptr;
@@ -152,6 +152,10 @@ void check_lists(const Step& st, const AttnLists& l, int only, bool prefill) {
             if (r.session == s && r.head_base == h * st.group && r.row_begin == a) rr = &r;
           REQUIRE(rr, "split session %d head %d has no reduction record", s, h);
           REQUIRE(rr->n_parts == n && rr->rows == items[0]->rows, "reduction record shape");
+          REQUIRE(rr->q_row == sr.q_row, "reduction record row");
+          for (const WorkRec* w : items)
+            REQUIRE(w->red >= 0 && w->red < (int)l.reduce.size() && &l.reduce[(std::size_t)w->red] == rr,
+                    "split item names another reduction record");
           std::vector<int> got;
           for (const WorkRec* w : items) got.push_back(w->part);
           std::sort(got.begin(), got.end());

@@ -552,6 +552,46 @@ def test_mixed_step_attention(gpu, fmt):
     case.close()
 
 
+@pytest.mark.parametrize("fmt", [tk.KV_F16, tk.KV_I8])
+def test_mixed_one_launch_split_merges_repeat(gpu, fmt):
+    """A dense mixed step is one launch whose split decode contexts and split
+    prefill tiles are merged in the launch by their last piece (arrival
+    counters that each merge re-arms): long decode contexts and a prefill
+    chunk over a long prefix, called four times on two layers; every call
+    matches the oracle and repeats bit for bit."""
+    say(f"mixed one launch fmt={fmt}")
+    case = PagedCase(28, 4, 128, fmt, [20000, 9000, 2000, 300, 0], [4, 4, 300, 2, 200], seed=44,
+                     layers=2, outlier_frac=0.01 if fmt == tk.KV_I8 else 0)
+    for layer in range(2):
+        case.fill(layer)
+    b = tk.Batch().plan(case.pool, case.sessions(True), case.qh)
+    kk = np.concatenate([k[c:] for k, c in zip(case.k, case.contexts)])
+    vv = np.concatenate([v[c:] for v, c in zip(case.v, case.contexts)])
+    dk, dv = tk.DeviceArray.from_numpy(kk), tk.DeviceArray.from_numpy(vv)
+    dq = tk.DeviceArray.from_numpy(case.q)
+    want = case.oracle_out()
+    first = None
+    for call in range(4):
+        layer = call % 2
+        if call < 2:
+            b.append(case.pool, layer, dk, dv)
+        out = tk.DeviceArray(case.q.shape, np.float32).zero()
+        b.attention(case.pool, layer, dq, out)
+        tk.hip().sync()
+        got = out.numpy()
+        out.close()
+        assert_attention_close(got, want, f"mixed one launch call {call}")
+        if first is None:
+            first = got
+        else:
+            assert np.array_equal(bits(got), bits(first)), f"call {call} differs from call 0"
+    say(f"  plan {b.info()}")
+    for a in (dk, dv, dq):
+        a.close()
+    b.close()
+    case.close()
+
+
 @pytest.mark.parametrize("fmt,sparse,kind", [
     (tk.KV_F16, (4, 64, 4), "decode"),
     (tk.KV_F16, (4, 100, 37), "decode"),   # stride > 16: pages with nothing kept are skipped
