@@ -282,10 +282,12 @@ int tge_prefill_attention(const tge_batch* batch, const tge_kv_pool* pool,
 /*
  * Attention for a mixed step (continuous batching: forward_batch rows of
  * many sessions, some decoding, some prefilling a chunk; qwen2.cpp:1613-1747
- * handles any mix per token): sessions with n_new*group <= 64 go through the
- * decode kernel, the others through the block-prefill kernel, in one call on
- * one plan. A step of only one kind is exactly tge_decode_attention or
- * tge_prefill_attention.
+ * handles any mix per token), in one call on one plan: sessions with
+ * n_new*group <= 64 take the decode path, the others the block-prefill path.
+ * A dense step is one kernel launch (decode shares and prefill tiles as
+ * roles of one kernel, split contexts merged inside the launch); with a
+ * static sparse subset the two kinds run as two launches. A step of only
+ * one kind is exactly tge_decode_attention or tge_prefill_attention.
  */
 int tge_batch_attention(const tge_batch* batch, const tge_kv_pool* pool,
                         int layer, const float* q, float* out, void* stream);
