@@ -36,6 +36,14 @@ __device__ __forceinline__ float pow2i(float e) {
   return __builtin_amdgcn_ldexpf(1.0f, (int)fmaxf(e, -300.0f));
 }
 
+// max(a, b, c) in one instruction (scores are never signalling NaNs, so
+// the operand quieting fmaxf would add is not needed).
+__device__ __forceinline__ float max3f(float a, float b, float c) {
+  float r;
+  asm("v_max3_f32 %0, %1, %2, %3" : "=v"(r) : "v"(a), "v"(b), "v"(c));
+  return r;
+}
+
 template <typename T, typename F>
 __device__ __forceinline__ T bitcast(F x) {
   static_assert(sizeof(T) == sizeof(F), "size");
@@ -453,11 +461,10 @@ struct Unit {
     return q[rg][pp];
   }
 
-  // S^T = K.Q^T of one page for every row group (fp32, K scales applied).
+  // S^T = K.Q^T of one page for every row group (fp32, K scales applied),
+  // added onto the values already in sacc.
   template <class QF>
-  __device__ __forceinline__ void scores(const Regs& r, const QF& qf, float4_t (&sacc)[NRG]) const {
-#pragma unroll
-    for (int rg = 0; rg < NRG; ++rg) sacc[rg] = float4_t{0, 0, 0, 0};
+  __device__ __forceinline__ void scores_onto(const Regs& r, const QF& qf, float4_t (&sacc)[NRG]) const {
 #pragma unroll
     for (int pp = 0; pp < NP; ++pp) {
       const half8_t ka = k_operand<FMT, SF32, D>(r, pp);
@@ -496,26 +503,97 @@ struct Unit {
   // 32 positions, and the value and row-sum products on 16x16x32 MFMAs with
   // k = 8g + j = token 4g+j of page A (j < 4) or 4g+j-4 of page B: lane (g, c)
   // already holds exactly those tokens of both pages, for P as for V.
+  // The score accumulators start at -base, so the scores come out relative
+  // to the row bases; the causal mask runs only for pages on the diagonal
+  // (masked_a / masked_b are wave-uniform), and one rarely taken branch
+  // rebases every row group, so the exponentials, the row sums and the value
+  // products of both row groups form one straight block.
   template <class QF>
   __device__ __forceinline__ void consume2(const Regs& ra, const Regs& rb, int pia, int pib, int grp,
                                            bool masked_a, bool masked_b, const QF& qf) {
     float4_t sa[NRG], sb[NRG];
-    scores(ra, qf, sa);
-    scores(rb, qf, sb);
+    start_scores(sa, sb);
+    scores_onto(ra, qf, sa);
+    scores_onto(rb, qf, sb);
     half8_t pw[NRG];
+    softmax2(sa, sb, pia, pib, grp, masked_a, masked_b, pw);
+    values2(
+        [&](int pp, int h) __attribute__((always_inline)) {
+          const half4_t va = v_operand(ra, pp, h), vb = v_operand(rb, pp, h);
+          return half8_t{va[0], va[1], va[2], va[3], vb[0], vb[1], vb[2], vb[3]};
+        },
+        pw);
+  }
+
+  // The same for two f16 pages still in their LDS slots: the K halves are
+  // read for the scores, and the V operands (four tokens of each page) are
+  // read straight into their MFMA operand registers while the softmax runs.
+  template <class QF>
+  __device__ __forceinline__ void consume2_slots(const char* slot_a, const char* slot_b, int lane,
+                                                 int pia, int pib, int grp, bool masked_a,
+                                                 bool masked_b, const QF& qf) {
+    static_assert(FMT == kF16, "f16 pages only");
+    using RG = Ring<FMT, SF32, D>;
+    Regs ra, rb;
+    read_half<FMT, SF32, D, false>(ra, slot_a, lane, grp);
+    read_half<FMT, SF32, D, false>(rb, slot_b, lane, grp);
+    half8_t v8[NP][2];
+#pragma unroll
+    for (int pp = 0; pp < NP; ++pp) {
+#pragma unroll
+      for (int h = 0; h < 2; ++h) {
+        const int off = RG::KV_BYTES + pp * 1024 + 16 * lane + 8 * h;
+        const half4_t va = *reinterpret_cast<const half4_t*>(slot_a + off);
+        const half4_t vb = *reinterpret_cast<const half4_t*>(slot_b + off);
+        v8[pp][h] = half8_t{va[0], va[1], va[2], va[3], vb[0], vb[1], vb[2], vb[3]};
+      }
+    }
+    float4_t sa[NRG], sb[NRG];
+    start_scores(sa, sb);
+    scores_onto(ra, qf, sa);
+    scores_onto(rb, qf, sb);
+    half8_t pw[NRG];
+    softmax2(sa, sb, pia, pib, grp, masked_a, masked_b, pw);
+    values2([&](int pp, int h) __attribute__((always_inline)) { return v8[pp][h]; }, pw);
+  }
+
+  __device__ __forceinline__ void start_scores(float4_t (&sa)[NRG], float4_t (&sb)[NRG]) const {
 #pragma unroll
     for (int rg = 0; rg < NRG; ++rg) {
-      sa[rg] -= base[rg];
-      sb[rg] -= base[rg];
+      sa[rg] = float4_t{-base[rg], -base[rg], -base[rg], -base[rg]};
+      sb[rg] = sa[rg];
+    }
+  }
+
+  // Online softmax over a page pair's scores (already relative to base):
+  // the f16 weights go to pw, the row sums are updated.
+  __device__ __forceinline__ void softmax2(float4_t (&sa)[NRG], float4_t (&sb)[NRG], int pia, int pib,
+                                           int grp, bool masked_a, bool masked_b, half8_t (&pw)[NRG]) {
+    if (masked_a || masked_b) {
 #pragma unroll
-      for (int e = 0; e < 4; ++e) {
-        if (masked_a && pia * 16 + 4 * grp + e > lim[rg]) sa[rg][e] = -INFINITY;
-        if (masked_b && pib * 16 + 4 * grp + e > lim[rg]) sb[rg][e] = -INFINITY;
+      for (int rg = 0; rg < NRG; ++rg) {
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          if (masked_a && pia * 16 + 4 * grp + e > lim[rg]) sa[rg][e] = -INFINITY;
+          if (masked_b && pib * 16 + 4 * grp + e > lim[rg]) sb[rg][e] = -INFINITY;
+        }
       }
-      const float lmax = fmaxf(fmaxf(fmaxf(sa[rg][0], sa[rg][1]), fmaxf(sa[rg][2], sa[rg][3])),
-                               fmaxf(fmaxf(sb[rg][0], sb[rg][1]), fmaxf(sb[rg][2], sb[rg][3])));
-      if (__builtin_expect(__any(lmax > thr[rg]), 0)) {
-        float rmax = fmaxf(lmax, __shfl_xor(lmax, 16));
+    }
+    float lmax[NRG];
+    bool over = false;
+#pragma unroll
+    for (int rg = 0; rg < NRG; ++rg) {
+      const float x = max3f(sa[rg][0], sa[rg][1], sa[rg][2]);
+      const float y = max3f(sa[rg][3], sb[rg][0], sb[rg][1]);
+      lmax[rg] = max3f(max3f(sb[rg][2], sb[rg][3], x), y, y);
+      over = over || lmax[rg] > thr[rg];
+    }
+    if (__builtin_expect(__any(over), 0)) {
+      // (a row group none of whose rows passes its threshold keeps its base:
+      // delta 0, alpha 1)
+#pragma unroll
+      for (int rg = 0; rg < NRG; ++rg) {
+        float rmax = fmaxf(lmax[rg], __shfl_xor(lmax[rg], 16));
         rmax = fmaxf(rmax, __shfl_xor(rmax, 32));
         const bool grow = rmax > thr[rg];
         const float delta = grow ? ceilf(rmax) : 0.0f;
@@ -528,20 +606,28 @@ struct Unit {
 #pragma unroll
         for (int t = 0; t < NT; ++t) o[rg][t] *= alpha;
       }
+    }
+    const half8_t ones = {(_Float16)1.0f, (_Float16)1.0f, (_Float16)1.0f, (_Float16)1.0f,
+                          (_Float16)1.0f, (_Float16)1.0f, (_Float16)1.0f, (_Float16)1.0f};
+#pragma unroll
+    for (int rg = 0; rg < NRG; ++rg) {
       pw[rg] = half8_t{(_Float16)__builtin_amdgcn_exp2f(sa[rg][0]), (_Float16)__builtin_amdgcn_exp2f(sa[rg][1]),
                        (_Float16)__builtin_amdgcn_exp2f(sa[rg][2]), (_Float16)__builtin_amdgcn_exp2f(sa[rg][3]),
                        (_Float16)__builtin_amdgcn_exp2f(sb[rg][0]), (_Float16)__builtin_amdgcn_exp2f(sb[rg][1]),
                        (_Float16)__builtin_amdgcn_exp2f(sb[rg][2]), (_Float16)__builtin_amdgcn_exp2f(sb[rg][3])};
-      const half8_t ones = {(_Float16)1.0f, (_Float16)1.0f, (_Float16)1.0f, (_Float16)1.0f,
-                            (_Float16)1.0f, (_Float16)1.0f, (_Float16)1.0f, (_Float16)1.0f};
       l4[rg] = MFMA16x16x32(ones, pw[rg], l4[rg]);
     }
+  }
+
+  // o += V^T . P^T over a page pair; vf(pp, h) yields the V operand of
+  // 16-dim tile 2pp+h (four tokens of each page).
+  template <class VF>
+  __device__ __forceinline__ void values2(const VF& vf, const half8_t (&pw)[NRG]) {
 #pragma unroll
     for (int pp = 0; pp < NP; ++pp) {
 #pragma unroll
       for (int h = 0; h < 2; ++h) {
-        const half4_t va = v_operand(ra, pp, h), vb = v_operand(rb, pp, h);
-        const half8_t v8 = {va[0], va[1], va[2], va[3], vb[0], vb[1], vb[2], vb[3]};
+        const half8_t v8 = vf(pp, h);
 #pragma unroll
         for (int rg = 0; rg < NRG; ++rg) o[rg][2 * pp + h] = MFMA16x16x32(v8, pw[rg], o[rg][2 * pp + h]);
       }

@@ -630,6 +630,25 @@ __device__ __forceinline__ void prefill_body(const AttnParams& p, PrefillShared<
   const int row0 = wave * 32;
   const bool has_rows = row0 < w.rows;
 
+  const int npages = w.page_end - w.page_begin;
+  const int ntiles = (npages + kWaves - 1) / kWaves;
+  const sconst_int* table = (const sconst_int*)(p.tables + w.table_off + w.page_begin);
+  // Tile k, page `wave` of it: fetched by this wave (nothing past the range).
+  auto fetch_tile = [&](int k) __attribute__((always_inline)) -> void {
+    const int j = k * kWaves + wave;
+    if (j < npages) {
+      const char* blk = static_cast<const char*>(p.pool) +
+                        ((size_t)table[j] * p.kv_heads + w.kv_head) * p.block_bytes;
+      fetch_page<FMT, SF32, D>(sh.ring + (k % NB) * SH::TILE + wave * RG::SLOT, blk,
+                               p.block_bytes, lane);
+    }
+  };
+  // The first tiles' fetches go out before the Q loads (both latencies overlap).
+#pragma unroll
+  for (int k = 0; k < NB - 1; ++k) {
+    if (k < ntiles) fetch_tile(k);
+  }
+
   // This wave's rows: Q^T operands (as in attend_unit) and visible limits.
   U u;
 #pragma unroll
@@ -661,25 +680,9 @@ __device__ __forceinline__ void prefill_body(const AttnParams& p, PrefillShared<
   u.set_sparse(p.sp_sink, p.sp_window, p.sp_stride,
                w.ctx + w.row_begin + (w.rows - 1) / w.rows_per_query + 1);
   // Pages at or past `unmasked` hold a position some row of the wave may not see.
-  const int unmasked = (w.ctx + w.row_begin + row0 / w.rows_per_query + 1) / 16;
+  const int unmasked =
+      __builtin_amdgcn_readfirstlane((w.ctx + w.row_begin + row0 / w.rows_per_query + 1) / 16);
 
-  const int npages = w.page_end - w.page_begin;
-  const int ntiles = (npages + kWaves - 1) / kWaves;
-  const sconst_int* table = (const sconst_int*)(p.tables + w.table_off + w.page_begin);
-  // Tile k, page `wave` of it: fetched by this wave (nothing past the range).
-  auto fetch_tile = [&](int k) __attribute__((always_inline)) -> void {
-    const int j = k * kWaves + wave;
-    if (j < npages) {
-      const char* blk = static_cast<const char*>(p.pool) +
-                        ((size_t)table[j] * p.kv_heads + w.kv_head) * p.block_bytes;
-      fetch_page<FMT, SF32, D>(sh.ring + (k % NB) * SH::TILE + wave * RG::SLOT, blk,
-                               p.block_bytes, lane);
-    }
-  };
-#pragma unroll
-  for (int k = 0; k < NB - 1; ++k) {
-    if (k < ntiles) fetch_tile(k);
-  }
   // Last tile holding a page of this wave.
   const int t_last = wave < npages ? (npages - 1 - wave) / kWaves : -1;
   for (int k = 0; k < ntiles; ++k) {
@@ -706,11 +709,16 @@ __device__ __forceinline__ void prefill_body(const AttnParams& p, PrefillShared<
                                      w.page_begin + k * kWaves + jj >= unmasked);
           }
         } else if (pg + 1 < npages) {
-          Regs ra, rb;
-          read_page<FMT, SF32, D>(ra, tile + j * RG::SLOT, lane, grp);
-          read_page<FMT, SF32, D>(rb, tile + (j + 1) * RG::SLOT, lane, grp);
-          u.consume2(ra, rb, pi, pi + 1, grp, pi >= unmasked, pi + 1 >= unmasked,
-                     [&](int rg, int pp) __attribute__((always_inline)) { return u.qop(rg, pp); });
+          const auto qf = [&](int rg, int pp) __attribute__((always_inline)) { return u.qop(rg, pp); };
+          if constexpr (FMT == kF16) {
+            u.consume2_slots(tile + j * RG::SLOT, tile + (j + 1) * RG::SLOT, lane, pi, pi + 1, grp,
+                             pi >= unmasked, pi + 1 >= unmasked, qf);
+          } else {
+            Regs ra, rb;
+            read_page<FMT, SF32, D>(ra, tile + j * RG::SLOT, lane, grp);
+            read_page<FMT, SF32, D>(rb, tile + (j + 1) * RG::SLOT, lane, grp);
+            u.consume2(ra, rb, pi, pi + 1, grp, pi >= unmasked, pi + 1 >= unmasked, qf);
+          }
         } else if (pg < npages) {
           Regs r;
           read_page<FMT, SF32, D>(r, tile + j * RG::SLOT, lane, grp);
