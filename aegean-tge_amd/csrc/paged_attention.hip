@@ -597,23 +597,39 @@ void paged_decode_kernel(AttnParams p) {
 // never meet across waves, so each wave writes its rows (or its split's
 // partial) directly.
 // ---------------------------------------------------------------------------
-template <int FMT, bool SF32, int D, int WPE>
+template <int FMT, bool SF32, int D, int WPE, int HALVES = 1>
 struct PrefillShared {
   static constexpr int SLOT = Ring<FMT, SF32, D>::SLOT;
   static constexpr int TILE = kWaves * SLOT;  // four pages
   static constexpr int NB_FIT = (160 * 1024 / WPE - 64) / TILE;
   static constexpr int NB = NB_FIT > 4 ? 4 : NB_FIT;
   static_assert(NB >= 2, "the prefill ring needs two tiles");
-  alignas(16) char ring[NB * TILE];
+  // one ring per half; afterwards the second half's states pass through it
+  static constexpr int XO = kWaves * 2 * (D / 16) * 64 * 16;  // accumulators (bytes)
+  static constexpr int XS = kWaves * 2 * 3 * 64 * 4;          // base, sum, empty flag
+  static_assert(HALVES == 1 || XO + XS <= HALVES * NB * TILE, "state exchange fits the rings");
+  alignas(16) char ring[HALVES * NB * TILE];
   int flag;  // arrival broadcast of the in-kernel split merge
 };
 
+// Waves of 32 rows per block-prefill workgroup, in halves of four: with two
+// halves (eight waves, one workgroup per CU at two waves per SIMD) each half
+// takes half of the item's pages for the same rows, and the halves' states
+// are merged through LDS at the end (no partial slots, no merge launch).
+template <int WPE>
+constexpr int halves_for_wpe() {
+  return WPE == 2 ? 2 : 1;
+}
+
 // MERGE: split tiles are merged in the launch (the mixed-step kernel).
-template <int FMT, bool SF32, int D, int WPE, bool SP, bool MERGE = false>
-__device__ __forceinline__ void prefill_body(const AttnParams& p, PrefillShared<FMT, SF32, D, WPE>& sh,
+// HALVES: 1 or 2 groups of four waves sharing the item's rows (see above).
+template <int FMT, bool SF32, int D, int WPE, bool SP, bool MERGE = false, int HALVES = 1>
+__device__ __forceinline__ void prefill_body(const AttnParams& p,
+                                             PrefillShared<FMT, SF32, D, WPE, HALVES>& sh,
                                              const int item) {
+  static_assert(HALVES == 1 || !MERGE, "the in-launch merge runs on four-wave workgroups");
   constexpr int NRG = 2;  // 32 rows per wave
-  using SH = PrefillShared<FMT, SF32, D, WPE>;
+  using SH = PrefillShared<FMT, SF32, D, WPE, HALVES>;
   using U = Unit<FMT, SF32, D, NRG>;
   using Regs = typename U::Regs;
   using RG = Ring<FMT, SF32, D>;
@@ -623,24 +639,33 @@ __device__ __forceinline__ void prefill_body(const AttnParams& p, PrefillShared<
 
   const WorkRec w = load_work((const sconst_work*)p.work + item);
   const int lane = threadIdx.x & 63;
-  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int wave_all = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int half = HALVES == 1 ? 0 : wave_all / kWaves;
+  const int wave = HALVES == 1 ? wave_all : wave_all % kWaves;
   const int col = lane & 15;
   const int grp = lane >> 4;
   const int q_stride = p.q_heads * D;
   const int row0 = wave * 32;
   const bool has_rows = row0 < w.rows;
 
-  const int npages = w.page_end - w.page_begin;
+  // This half's pages: the first half takes whole tiles of four.
+  const int all_pages = w.page_end - w.page_begin;
+  const int cut = HALVES == 1 ? all_pages : min(all_pages, ((all_pages + 1) / 2 + 3) / 4 * 4);
+  const int first_page = w.page_begin + (half == 0 ? 0 : cut);
+  const int npages = half == 0 ? cut : all_pages - cut;
   const int ntiles = (npages + kWaves - 1) / kWaves;
-  const sconst_int* table = (const sconst_int*)(p.tables + w.table_off + w.page_begin);
+  // (the halves' loops run in step: the barriers are the workgroup's)
+  const int ntiles_max = HALVES == 1 ? ntiles : (cut + kWaves - 1) / kWaves;
+  char* const ring = sh.ring + half * NB * SH::TILE;
+  const sconst_int* table = (const sconst_int*)(p.tables + w.table_off + first_page);
   // Tile k, page `wave` of it: fetched by this wave (nothing past the range).
   auto fetch_tile = [&](int k) __attribute__((always_inline)) -> void {
     const int j = k * kWaves + wave;
     if (j < npages) {
       const char* blk = static_cast<const char*>(p.pool) +
                         ((size_t)table[j] * p.kv_heads + w.kv_head) * p.block_bytes;
-      fetch_page<FMT, SF32, D>(sh.ring + (k % NB) * SH::TILE + wave * RG::SLOT, blk,
-                               p.block_bytes, lane);
+      fetch_page<FMT, SF32, D>(ring + (k % NB) * SH::TILE + wave * RG::SLOT, blk, p.block_bytes,
+                               lane);
     }
   };
   // The first tiles' fetches go out before the Q loads (both latencies overlap).
@@ -658,17 +683,19 @@ __device__ __forceinline__ void prefill_body(const AttnParams& p, PrefillShared<
     const int qi = w.row_begin + (valid ? r / w.rows_per_query : 0);
     const int head = w.head_base + (valid ? r % w.rows_per_query : 0);
     const float* qp = p.q + (size_t)(w.q_row + qi) * q_stride + (size_t)head * D + 4 * grp;
+    if (half == 0) {  // (the second half takes the first half's operands, below)
 #pragma unroll
-    for (int pp = 0; pp < NP; ++pp) {
-      float4 a = make_float4(0, 0, 0, 0), b = make_float4(0, 0, 0, 0);
-      if (valid) {
-        a = *reinterpret_cast<const float4*>(qp + 32 * pp);
-        b = *reinterpret_cast<const float4*>(qp + 32 * pp + 16);
+      for (int pp = 0; pp < NP; ++pp) {
+        float4 a = make_float4(0, 0, 0, 0), b = make_float4(0, 0, 0, 0);
+        if (valid) {
+          a = *reinterpret_cast<const float4*>(qp + 32 * pp);
+          b = *reinterpret_cast<const float4*>(qp + 32 * pp + 16);
+        }
+        const float c = p.scale_log2;
+        const float x[8] = {a.x * c, a.y * c, a.z * c, a.w * c, b.x * c, b.y * c, b.z * c, b.w * c};
+#pragma unroll
+        for (int j = 0; j < 8; ++j) u.q[rg][pp][j] = (_Float16)x[j];
       }
-      const float c = p.scale_log2;
-      const float x[8] = {a.x * c, a.y * c, a.z * c, a.w * c, b.x * c, b.y * c, b.z * c, b.w * c};
-#pragma unroll
-      for (int j = 0; j < 8; ++j) u.q[rg][pp][j] = (_Float16)x[j];
     }
     u.lim[rg] = valid ? w.ctx + w.row_begin + r / w.rows_per_query : -1;
     u.base[rg] = 0.0f;
@@ -676,6 +703,30 @@ __device__ __forceinline__ void prefill_body(const AttnParams& p, PrefillShared<
     u.l4[rg] = float4_t{0, 0, 0, 0};
 #pragma unroll
     for (int t = 0; t < NT; ++t) u.o[rg][t] = float4_t{0, 0, 0, 0};
+  }
+  if constexpr (HALVES == 2) {
+    // The first half's waves pass their f16 Q^T operands to the second
+    // half's through LDS (half the Q reads): each half's last ring slot is
+    // free until the loop's first fetch, two waves' operands to a slot.
+    static_assert(2 * NRG * NP * 64 * 16 <= SH::TILE, "two waves' Q operands fit a ring slot");
+    half8_t* stage = reinterpret_cast<half8_t*>(sh.ring + (wave / 2) * NB * SH::TILE +
+                                                (NB - 1) * SH::TILE) +
+                     (wave % 2) * NRG * NP * 64;
+    if (half == 0) {
+#pragma unroll
+      for (int rg = 0; rg < NRG; ++rg) {
+#pragma unroll
+        for (int pp = 0; pp < NP; ++pp) stage[(rg * NP + pp) * 64 + lane] = u.q[rg][pp];
+      }
+    }
+    lds_barrier();
+    if (half == 1) {
+#pragma unroll
+      for (int rg = 0; rg < NRG; ++rg) {
+#pragma unroll
+        for (int pp = 0; pp < NP; ++pp) u.q[rg][pp] = stage[(rg * NP + pp) * 64 + lane];
+      }
+    }
   }
   u.set_sparse(p.sp_sink, p.sp_window, p.sp_stride,
                w.ctx + w.row_begin + (w.rows - 1) / w.rows_per_query + 1);
@@ -685,7 +736,7 @@ __device__ __forceinline__ void prefill_body(const AttnParams& p, PrefillShared<
 
   // Last tile holding a page of this wave.
   const int t_last = wave < npages ? (npages - 1 - wave) / kWaves : -1;
-  for (int k = 0; k < ntiles; ++k) {
+  for (int k = 0; k < ntiles_max; ++k) {
     // this wave's page of tile k has landed (its pages of up to NB - 2
     // younger tiles may still be in flight), then every wave's has, and
     // every wave is done with tile k - 1, whose slot the fetch below refills
@@ -695,18 +746,18 @@ __device__ __forceinline__ void prefill_body(const AttnParams& p, PrefillShared<
     }
     lds_barrier();
     if (k + NB - 1 < ntiles) fetch_tile(k + NB - 1);
-    if (has_rows) {
-      const char* tile = sh.ring + (k % NB) * SH::TILE;
+    if (has_rows && k < ntiles) {
+      const char* tile = ring + (k % NB) * SH::TILE;
 #pragma unroll
       for (int j = 0; j < kWaves; j += 2) {
         const int pg = k * kWaves + j;
-        const int pi = w.page_begin + pg;
+        const int pi = first_page + pg;
         if (SP) {  // static sparse subsets take the pages one by one
           for (int jj = j; jj < j + 2 && k * kWaves + jj < npages; ++jj) {
             Regs r;
             read_page<FMT, SF32, D>(r, tile + jj * RG::SLOT, lane, grp);
-            u.template consume<true>(r, w.page_begin + k * kWaves + jj, grp,
-                                     w.page_begin + k * kWaves + jj >= unmasked);
+            u.template consume<true>(r, first_page + k * kWaves + jj, grp,
+                                     first_page + k * kWaves + jj >= unmasked);
           }
         } else if (pg + 1 < npages) {
           const auto qf = [&](int rg, int pp) __attribute__((always_inline)) { return u.qop(rg, pp); };
@@ -724,6 +775,41 @@ __device__ __forceinline__ void prefill_body(const AttnParams& p, PrefillShared<
           read_page<FMT, SF32, D>(r, tile + j * RG::SLOT, lane, grp);
           u.template consume<false>(r, pi, grp, pi >= unmasked);
         }
+      }
+    }
+  }
+  if constexpr (HALVES == 2) {
+    // The second half hands its states to the first through the rings'
+    // LDS (lane l of wave w holds the same rows and dims in both halves).
+    __syncthreads();  // every wave is done with the rings
+    float4_t* xo = reinterpret_cast<float4_t*>(sh.ring) + wave * NRG * NT * 64;
+    float* xs = reinterpret_cast<float*>(sh.ring + SH::XO) + wave * NRG * 3 * 64;
+    if (half == 1 && has_rows) {
+#pragma unroll
+      for (int rg = 0; rg < NRG; ++rg) {
+#pragma unroll
+        for (int t = 0; t < NT; ++t) xo[(rg * NT + t) * 64 + lane] = u.o[rg][t];
+        xs[(rg * 3 + 0) * 64 + lane] = u.base[rg];
+        xs[(rg * 3 + 1) * 64 + lane] = u.l4[rg][0];
+        xs[(rg * 3 + 2) * 64 + lane] = u.thr[rg] == -INFINITY ? 0.0f : 1.0f;
+      }
+    }
+    __syncthreads();
+    if (half == 1) return;
+    if (has_rows) {
+#pragma unroll
+      for (int rg = 0; rg < NRG; ++rg) {
+        if (xs[(rg * 3 + 2) * 64 + lane] == 0.0f) continue;  // the second half saw nothing
+        const float b1 = xs[(rg * 3 + 0) * 64 + lane], l1 = xs[(rg * 3 + 1) * 64 + lane];
+        const bool empty0 = u.thr[rg] == -INFINITY;
+        const float m = empty0 ? b1 : fmaxf(u.base[rg], b1);
+        const float a0 = empty0 ? 0.0f : pow2i(u.base[rg] - m), a1 = pow2i(b1 - m);
+        const float l = u.l4[rg][0] * a0 + l1 * a1;
+        u.l4[rg] = float4_t{l, l, l, l};
+#pragma unroll
+        for (int t = 0; t < NT; ++t) u.o[rg][t] = u.o[rg][t] * a0 + xo[(rg * NT + t) * 64 + lane] * a1;
+        u.base[rg] = m;
+        u.thr[rg] = kLazyMax;
       }
     }
   }
@@ -769,10 +855,11 @@ __device__ __forceinline__ void prefill_body(const AttnParams& p, PrefillShared<
 }
 
 template <int FMT, bool SF32, int D, int WPE, bool SP>
-__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(WPE, WPE)))
+__global__ __launch_bounds__(256 * halves_for_wpe<WPE>()) __attribute__((amdgpu_waves_per_eu(WPE, WPE)))
 void paged_prefill_kernel(AttnParams p) {
-  __shared__ PrefillShared<FMT, SF32, D, WPE> sh;
-  prefill_body<FMT, SF32, D, WPE, SP>(p, sh, blockIdx.x);
+  constexpr int H = halves_for_wpe<WPE>();
+  __shared__ PrefillShared<FMT, SF32, D, WPE, H> sh;
+  prefill_body<FMT, SF32, D, WPE, SP, false, H>(p, sh, blockIdx.x);
 }
 
 // ---------------------------------------------------------------------------
@@ -989,19 +1076,25 @@ int decode_blocks_per_cu(int format, int scale_f32, int head_dim, int row_groups
                    : decode_blocks_d<kI8, false, 128>(row_groups, sparse);
 }
 
+template <int FMT, int D>
+constexpr int prefill_wpe() {
+#ifdef TGE_PREFILL_WPE
+  return TGE_PREFILL_WPE;
+#else
+  return waves_per_eu<FMT, D, 2>();
+#endif
+}
+
 template <int FMT, bool SF32, int D>
 hipError_t launch_prefill_d(int n_units, const AttnParams& p, hipStream_t stream) {
-#ifdef TGE_PREFILL_WPE
-  constexpr int wpe = TGE_PREFILL_WPE;
-#else
-  constexpr int wpe = waves_per_eu<FMT, D, 2>();
-#endif
+  constexpr int wpe = prefill_wpe<FMT, D>();
+  const dim3 block(256 * halves_for_wpe<wpe>());
   if (p.sp_stride > 0) {
     hipLaunchKernelGGL((paged_prefill_kernel<FMT, SF32, D, wpe, true>), dim3((unsigned)n_units),
-                       dim3(256), 0, stream, p);
+                       block, 0, stream, p);
   } else {
     hipLaunchKernelGGL((paged_prefill_kernel<FMT, SF32, D, wpe, false>), dim3((unsigned)n_units),
-                       dim3(256), 0, stream, p);
+                       block, 0, stream, p);
   }
   return hipGetLastError();
 }
@@ -1060,6 +1153,13 @@ int mixed_blocks_per_cu(int format, int scale_f32, int head_dim, int row_groups)
   if (head_dim == 64)
     return scale_f32 ? mixed_blocks_d<kI8, true, 64>(row_groups) : mixed_blocks_d<kI8, false, 64>(row_groups);
   return scale_f32 ? mixed_blocks_d<kI8, true, 128>(row_groups) : mixed_blocks_d<kI8, false, 128>(row_groups);
+}
+
+int prefill_halves(int format, int head_dim) {
+  if (format == kF16) return head_dim == 64 ? halves_for_wpe<prefill_wpe<kF16, 64>()>()
+                                            : halves_for_wpe<prefill_wpe<kF16, 128>()>();
+  return head_dim == 64 ? halves_for_wpe<prefill_wpe<kI8, 64>()>()
+                        : halves_for_wpe<prefill_wpe<kI8, 128>()>();
 }
 
 hipError_t launch_prefill(int format, int scale_f32, int head_dim, int n_units,

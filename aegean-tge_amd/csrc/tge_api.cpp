@@ -781,7 +781,8 @@ int tge_prefill_attention(const tge_batch* b, const tge_kv_pool* p, int layer,
   // steps never pay for them) and reused by every layer.
   tge_batch* mb = const_cast<tge_batch*>(b);
   if (!mb->prefill.built) {
-    tge::plan::build_prefill(mb->step, device_cus(), mb->prefill.lists, 0);
+    tge::plan::build_prefill(mb->step, device_cus(), mb->prefill.lists, 0,
+                             tge::prefill_halves(p->desc.format, b->step.head_dim));
     s = upload_plan(mb->prefill, b->step.head_dim, static_cast<hipStream_t>(stream));
     if (s != TGE_OK) return s;
   }

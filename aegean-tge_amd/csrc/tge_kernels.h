@@ -134,6 +134,10 @@ hipError_t launch_mixed(int format, int scale_f32, int head_dim, int row_groups,
                         int n_pf, const AttnParams& dec, const AttnParams& pf, hipStream_t stream);
 int mixed_blocks_per_cu(int format, int scale_f32, int head_dim, int row_groups);
 // Block prefill: one workgroup per work item (tiles of up to 128 rows).
+// Groups of four waves per block-prefill workgroup (1 or 2): with two, an
+// item's pages are shared by both halves and the plan's items may be twice
+// as long.
+int prefill_halves(int format, int head_dim);
 hipError_t launch_prefill(int format, int scale_f32, int head_dim, int n_units,
                           const AttnParams& p, hipStream_t stream);
 // Resident decode workgroups per CU (of the static sparse variant when

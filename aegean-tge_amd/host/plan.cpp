@@ -335,7 +335,7 @@ void add_units(std::vector<WorkRec>& work, std::vector<ReduceRec>& red, int& par
 #define TGE_PREFILL_MIN_SPLIT 32
 #endif
 
-void build_prefill(const Step& b, int cus, AttnLists& pl, int only) {
+void build_prefill(const Step& b, int cus, AttnLists& pl, int only, int halves) {
   pl.work.clear();
   pl.reduce.clear();
   pl.wg_first.clear();
@@ -343,16 +343,18 @@ void build_prefill(const Step& b, int cus, AttnLists& pl, int only) {
   pl.parts = pl.max_splits = 0;
   pl.row_groups = kPrefillRows / 16;
   const int tq = std::max(1, kPrefillRows / b.group);
-  // Page-split size: enough items for about two rounds of two workgroups
-  // on each compute unit, at least 32 pages (eight tiles of four).
+  // Page-split size: enough items for about two rounds of two four-wave
+  // workgroups on each compute unit (of one eight-wave workgroup with two
+  // halves), at least 32 pages (eight tiles of four) per half.
   long pages_total = 0;
   for (const auto& sr : b.sessions) {
     if (!take_session(b, sr, only)) continue;
     for (int a = 0; a < sr.n_new; a += tq)
       pages_total += (long)((sr.ctx + std::min(sr.n_new, a + tq) + 15) / 16) * b.kv_heads;
   }
-  const long target_units = 2L * std::max(1, cus) * 2;
-  const int pps = (int)std::max<long>(TGE_PREFILL_MIN_SPLIT,
+  halves = halves == 2 ? 2 : 1;
+  const long target_units = 2L * std::max(1, cus) * (halves == 2 ? 1 : 2);
+  const int pps = (int)std::max<long>((long)TGE_PREFILL_MIN_SPLIT * halves,
                                       ((pages_total + target_units - 1) / target_units + 3) / 4 * 4);
   for (int s = 0; s < (int)b.sessions.size(); ++s) {
     const SessionRec& sr = b.sessions[(std::size_t)s];

@@ -111,7 +111,9 @@ void build_decode(const Step& s, Residency res, AttnLists& out, int only);
 
 // Block-prefill work: (session, KV head, query tile) x page splits sized so
 // the launch covers `cus` compute units about twice; longest items first.
-void build_prefill(const Step& s, int cus, AttnLists& out, int only);
+// `halves`: groups of four waves per workgroup (2: an item's pages are
+// shared by two halves, so items may be twice as long).
+void build_prefill(const Step& s, int cus, AttnLists& out, int only, int halves = 1);
 
 // A small decode step in one launch (paged_step_kernel): one workgroup per
 // piece of a (session, KV head) segment; pieces of a split segment own

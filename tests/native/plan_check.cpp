@@ -288,7 +288,8 @@ void random_plans(int cases) {
         check_lists(st, dec, only, false);
         REQUIRE(dec.groups <= res.groups, "more workgroups than resident");
       }
-      build_prefill(st, cus, pf, only);
+      const int halves = 1 + (int)(rng() % 2);
+      build_prefill(st, cus, pf, only, halves);
       check_lists(st, pf, only, true);
       std::size_t ofr = 0, off = 0;
       const std::size_t bytes = image_layout(pf, &ofr, &off);
