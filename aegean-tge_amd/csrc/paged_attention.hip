@@ -609,7 +609,8 @@ struct PrefillShared {
   static constexpr int XS = kWaves * 2 * 3 * 64 * 4;          // base, sum, empty flag
   static_assert(HALVES == 1 || XO + XS <= HALVES * NB * TILE, "state exchange fits the rings");
   alignas(16) char ring[HALVES * NB * TILE];
-  int flag;  // arrival broadcast of the in-kernel split merge
+  int flag;      // arrival broadcast of the in-kernel split merge
+  int hbar[2];   // per-half tile barriers (arrivals, counting up)
 };
 
 // Waves of 32 rows per block-prefill workgroup, in halves of four: with two
@@ -619,6 +620,23 @@ struct PrefillShared {
 template <int WPE>
 constexpr int halves_for_wpe() {
   return WPE == 2 ? 2 : 1;
+}
+
+// Tile barrier of one half's four waves (the two halves run their tile
+// loops independently): this wave's LDS reads are complete, it counts in,
+// and waits until all four have counted `target` arrivals in total. The
+// wait is bounded (about 0.2 s): past the bound the wave goes on and the
+// launch completes with wrong rows instead of hanging.
+__device__ __forceinline__ void half_barrier(int* ctr, int target) {
+  asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+  if ((threadIdx.x & 63) == 0) __hip_atomic_fetch_add(ctr, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+  for (int spin = 0; spin < (1 << 21); ++spin) {
+    const int seen = __builtin_amdgcn_readfirstlane(
+        __hip_atomic_load(ctr, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP));
+    if (seen >= target) break;
+    __builtin_amdgcn_s_sleep(1);
+  }
+  __atomic_signal_fence(__ATOMIC_SEQ_CST);
 }
 
 // MERGE: split tiles are merged in the launch (the mixed-step kernel).
@@ -654,8 +672,6 @@ __device__ __forceinline__ void prefill_body(const AttnParams& p,
   const int first_page = w.page_begin + (half == 0 ? 0 : cut);
   const int npages = half == 0 ? cut : all_pages - cut;
   const int ntiles = (npages + kWaves - 1) / kWaves;
-  // (the halves' loops run in step: the barriers are the workgroup's)
-  const int ntiles_max = HALVES == 1 ? ntiles : (cut + kWaves - 1) / kWaves;
   char* const ring = sh.ring + half * NB * SH::TILE;
   const sconst_int* table = (const sconst_int*)(p.tables + w.table_off + first_page);
   // Tile k, page `wave` of it: fetched by this wave (nothing past the range).
@@ -719,6 +735,7 @@ __device__ __forceinline__ void prefill_body(const AttnParams& p,
         for (int pp = 0; pp < NP; ++pp) stage[(rg * NP + pp) * 64 + lane] = u.q[rg][pp];
       }
     }
+    if (threadIdx.x < 2) sh.hbar[threadIdx.x] = 0;
     lds_barrier();
     if (half == 1) {
 #pragma unroll
@@ -736,7 +753,7 @@ __device__ __forceinline__ void prefill_body(const AttnParams& p,
 
   // Last tile holding a page of this wave.
   const int t_last = wave < npages ? (npages - 1 - wave) / kWaves : -1;
-  for (int k = 0; k < ntiles_max; ++k) {
+  for (int k = 0; k < ntiles; ++k) {
     // this wave's page of tile k has landed (its pages of up to NB - 2
     // younger tiles may still be in flight), then every wave's has, and
     // every wave is done with tile k - 1, whose slot the fetch below refills
@@ -744,9 +761,13 @@ __device__ __forceinline__ void prefill_body(const AttnParams& p,
       const int younger = (k + NB - 2 < t_last ? k + NB - 2 : t_last) - k;
       wait_vmcnt_pages<NB - 2, RG::LOADS>(younger);
     }
-    lds_barrier();
+    if constexpr (HALVES == 2) {
+      half_barrier(&sh.hbar[half], kWaves * (k + 1));
+    } else {
+      lds_barrier();
+    }
     if (k + NB - 1 < ntiles) fetch_tile(k + NB - 1);
-    if (has_rows && k < ntiles) {
+    if (has_rows) {
       const char* tile = ring + (k % NB) * SH::TILE;
 #pragma unroll
       for (int j = 0; j < kWaves; j += 2) {
