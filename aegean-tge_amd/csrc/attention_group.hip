@@ -87,7 +87,8 @@ __global__ __launch_bounds__(64 * kGroupWaves) void attention_group_kernel(Group
   float q[PER], acc[PER];
 #pragma unroll
   for (int e = 0; e < PER; ++e) {
-    q[e] = p.queries[(size_t)head * D + lane + 64 * e];
+    const int d = lane + 64 * e;  // (dims past the head's own are zeros)
+    q[e] = d < p.dims ? p.queries[(size_t)head * p.dims + d] : 0.0f;
     acc[e] = 0.0f;
   }
   float maximum = -INFINITY, sum = 0.0f;
@@ -166,7 +167,10 @@ __global__ __launch_bounds__(64 * kGroupWaves) void attention_group_kernel(Group
     p.sums[head] = fail ? NAN : s;
   }
 #pragma unroll
-  for (int e = 0; e < PER; ++e) p.accumulators[(size_t)head * D + lane + 64 * e] = fail ? NAN : a[e];
+  for (int e = 0; e < PER; ++e) {
+    const int d = lane + 64 * e;
+    if (d < p.dims) p.accumulators[(size_t)head * p.dims + d] = fail ? NAN : a[e];
+  }
 }
 
 }  // namespace

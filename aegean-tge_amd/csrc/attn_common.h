@@ -331,18 +331,19 @@ __device__ __forceinline__ void merge_record(const AttnParams& p, const ReduceRe
     }
     __syncthreads();  // the weights of this batch are read
   }
-  const int q_stride = p.q_heads * D;
+  const int q_stride = p.q_heads * p.dims;
 #pragma unroll
   for (int j = 0; j < PJ; ++j) {
     const int pair = t + NT * j;
     if (pair >= rows * L) continue;
     const int r = pair / L, d4 = pair - r * L;
+    if (4 * d4 >= p.dims) continue;  // a dim past the head's own
     const float sum = lS[r];
     const int qi = rr.row_begin + r / rr.rows_per_query;
     const int head = rr.head_base + r % rr.rows_per_query;
     float4_t res = float4_t{0, 0, 0, 0};
     if (sum > 0.0f) res = div4(acc[j], sum);
-    *reinterpret_cast<float4_t*>(p.out + (size_t)(rr.q_row + qi) * q_stride + (size_t)head * D + 4 * d4) = res;
+    *reinterpret_cast<float4_t*>(p.out + (size_t)(rr.q_row + qi) * q_stride + (size_t)head * p.dims + 4 * d4) = res;
   }
 }
 

@@ -35,9 +35,10 @@ __global__ __launch_bounds__(256) void kv_append_kernel(AppendParams p) {
   const int which = (int)(rest & 1);
   const int row = (int)(rest >> 1);
 
-  const int kv_dim = p.kv_heads * p.head_dim;
-  float x[8];
-  load8(x, (which ? p.v : p.k) + (size_t)row * kv_dim + h * p.head_dim + b * 32 + quarter * 8);
+  // (dims past the head's own are stored as zeros)
+  const int d0 = b * 32 + quarter * 8;
+  float x[8] = {0, 0, 0, 0, 0, 0, 0, 0};
+  if (d0 < p.dims) load8(x, (which ? p.v : p.k) + (size_t)row * p.kv_heads * p.dims + h * p.dims + d0);
   store_lane<FMT>(p, x, p.rows[row], which, h, b, quarter, live);
 }
 
@@ -68,7 +69,7 @@ __device__ __forceinline__ void rope_pair(float l, float h, float c, float s, bo
 //     high partners together and writes both, so q_out may alias q.
 template <int FMT>
 __global__ __launch_bounds__(256) void kv_append_rope_kernel(AppendParams p) {
-  const int D = p.head_dim, half = D >> 1, nb = D >> 5;
+  const int D = p.dims, half = D >> 1, nb = p.head_dim >> 5;  // pairs of the head's own dims
   const int kv_lanes = 2 * p.kv_heads * nb * 4;
   const int q_lanes = p.q ? p.q_heads * (half >> 3) : 0;
   const int per_row = kv_lanes + q_lanes;  // a multiple of 4: blocks stay aligned
@@ -122,6 +123,11 @@ __global__ __launch_bounds__(256) void kv_append_rope_kernel(AppendParams p) {
   const int which = rest / p.kv_heads;
   const int kv_dim = p.kv_heads * D;
   const int d0 = 32 * b + 8 * quarter;
+  if (d0 >= D) {  // a dim past the head's own: stored as zero
+    const float z[8] = {0, 0, 0, 0, 0, 0, 0, 0};
+    store_lane<FMT>(p, z, rr, which, h, b, quarter, live);
+    return;
+  }
   const float* src = (which ? p.v : p.k) + (size_t)row * kv_dim + h * D;
   const float* bias = which ? p.v_bias : p.k_bias;
   float x[8];
@@ -133,7 +139,8 @@ __global__ __launch_bounds__(256) void kv_append_rope_kernel(AppendParams p) {
     for (int i = 0; i < 8; ++i) x[i] = __fadd_rn(x[i], bx[i]);
   }
   if (which == 0) {
-    // the partner half: dims d0 +- half (a 32-value block lies in one half)
+    // the partner half: dims d0 +- half (a lane's 8 dims lie in one half:
+    // half is a multiple of 8)
     const bool low = d0 < half;
     const int dp = low ? d0 + half : d0 - half;
     float y[8];
@@ -161,13 +168,13 @@ __global__ __launch_bounds__(256) void kv_append_rope_kernel(AppendParams p) {
 // One thread per (position, kv head, element) of the gathered rows.
 template <typename T>
 __global__ __launch_bounds__(256) void kv_gather_kernel(GatherParams p) {
-  const int kv_dim = p.kv_heads * p.head_dim;
+  const int kv_dim = p.kv_heads * p.dims;
   const long idx = (long)blockIdx.x * blockDim.x + threadIdx.x;
   const long total = (long)p.count * kv_dim;
   if (idx >= total) return;
   const int pos = (int)(idx / kv_dim);
   const int c = (int)(idx % kv_dim);
-  const int h = c / p.head_dim, d = c % p.head_dim;
+  const int h = c / p.dims, d = c % p.dims;
   const int page = p.table[pos >> 4], t = pos & 15;
   const int np = p.head_dim >> 5;
   const char* blk = static_cast<const char*>(p.pool) + ((size_t)page * p.kv_heads + h) * p.geom.block_bytes;
@@ -204,7 +211,7 @@ hipError_t launch_kv_append(int format, const AppendParams& p, hipStream_t strea
 
 hipError_t launch_kv_append_rope(int format, const AppendParams& p, hipStream_t stream) {
   const int nb = p.head_dim >> 5;
-  const long per_row = 2L * p.kv_heads * nb * 4 + (p.q ? (long)p.q_heads * (p.head_dim >> 4) : 0);
+  const long per_row = 2L * p.kv_heads * nb * 4 + (p.q ? (long)p.q_heads * (p.dims >> 4) : 0);
   const long total = (long)p.n_rows * per_row;
   if (total == 0) return hipSuccess;
   const dim3 grid((unsigned)((total + 255) / 256)), block(256);
@@ -217,7 +224,7 @@ hipError_t launch_kv_append_rope(int format, const AppendParams& p, hipStream_t 
 }
 
 hipError_t launch_kv_gather(int format, const GatherParams& p, hipStream_t stream) {
-  const long total = (long)p.count * p.kv_heads * p.head_dim;
+  const long total = (long)p.count * p.kv_heads * p.dims;
   if (total == 0) return hipSuccess;
   const dim3 grid((unsigned)((total + 255) / 256)), block(256);
   if (format == kF16) {

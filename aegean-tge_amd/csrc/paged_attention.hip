@@ -211,7 +211,7 @@ __device__ __forceinline__ void decode_body(const AttnParams& p,
   const int col = lane & 15;
   const int grp = lane >> 4;
   const sconst_work* work = (const sconst_work*)p.work;
-  const int q_stride = p.q_heads * D;
+  const int q_stride = p.q_heads * p.dims;
 
   char* ring = sh.ring + wave * NB * RG::SLOT;
 
@@ -234,9 +234,11 @@ __device__ __forceinline__ void decode_body(const AttnParams& p,
         if (r < w.rows) {
           const int qi = w.row_begin + r / w.rows_per_query;
           const int head = w.head_base + r % w.rows_per_query;
-          const float* qp = p.q + (size_t)(w.q_row + qi) * q_stride + (size_t)head * D + 32 * pp + 4 * (l >> 4);
-          const float4 a = *reinterpret_cast<const float4*>(qp);
-          const float4 b = *reinterpret_cast<const float4*>(qp + 16);
+          const int d = 32 * pp + 4 * (l >> 4);  // (dims past the head's own read as zeros)
+          const float* qp = p.q + (size_t)(w.q_row + qi) * q_stride + (size_t)head * p.dims + d;
+          const float4 z = make_float4(0, 0, 0, 0);
+          const float4 a = d < p.dims ? *reinterpret_cast<const float4*>(qp) : z;
+          const float4 b = d + 16 < p.dims ? *reinterpret_cast<const float4*>(qp + 16) : z;
           const float c = p.scale_log2;
           h = half8_t{(_Float16)(a.x * c), (_Float16)(a.y * c), (_Float16)(a.z * c), (_Float16)(a.w * c),
                       (_Float16)(b.x * c), (_Float16)(b.y * c), (_Float16)(b.z * c), (_Float16)(b.w * c)};
@@ -268,9 +270,10 @@ __device__ __forceinline__ void decode_body(const AttnParams& p,
       const int rr = ok[k] ? r : 0;
       const int qi = w.row_begin + rr / w.rows_per_query;
       const int head = w.head_base + rr % w.rows_per_query;
-      const float* qp = p.q + (size_t)(w.q_row + qi) * q_stride + (size_t)head * D + 32 * pp + 4 * (l >> 4);
-      qa[k] = *reinterpret_cast<const float4*>(qp);
-      qb[k] = *reinterpret_cast<const float4*>(qp + 16);
+      const int d = 32 * pp + 4 * (l >> 4);  // (dims past the head's own read as zeros)
+      const float* qp = p.q + (size_t)(w.q_row + qi) * q_stride + (size_t)head * p.dims + d;
+      qa[k] = d < p.dims ? *reinterpret_cast<const float4*>(qp) : make_float4(0, 0, 0, 0);
+      qb[k] = d + 16 < p.dims ? *reinterpret_cast<const float4*>(qp + 16) : make_float4(0, 0, 0, 0);
     }
 #pragma unroll
     for (int k = 0; k < PER; ++k) {
@@ -479,7 +482,8 @@ __device__ __forceinline__ void decode_body(const AttnParams& p,
             const int head = cw.head_base + r % cw.rows_per_query;
             float4_t res = float4_t{0, 0, 0, 0};
             if (sum > 0.0f) res = div4(acc, sum);
-            *reinterpret_cast<float4_t*>(p.out + (size_t)(cw.q_row + qi) * q_stride + (size_t)head * D + 4 * d4) = res;
+            if (4 * d4 < p.dims)
+              *reinterpret_cast<float4_t*>(p.out + (size_t)(cw.q_row + qi) * q_stride + (size_t)head * p.dims + 4 * d4) = res;
           } else if (MIX && p.counters) {  // merged in this launch: coherent stores
             store_partial_row<D>(p, cw.part, r, d4, acc);
             if (d4 == 0) store_partial_ml(p, cw.part, r, lds_mm[r], sum);
@@ -662,7 +666,7 @@ __device__ __forceinline__ void prefill_body(const AttnParams& p,
   const int wave = HALVES == 1 ? wave_all : wave_all % kWaves;
   const int col = lane & 15;
   const int grp = lane >> 4;
-  const int q_stride = p.q_heads * D;
+  const int q_stride = p.q_heads * p.dims;
   const int row0 = wave * 32;
   const bool has_rows = row0 < w.rows;
 
@@ -698,15 +702,14 @@ __device__ __forceinline__ void prefill_body(const AttnParams& p,
     const bool valid = r < w.rows;
     const int qi = w.row_begin + (valid ? r / w.rows_per_query : 0);
     const int head = w.head_base + (valid ? r % w.rows_per_query : 0);
-    const float* qp = p.q + (size_t)(w.q_row + qi) * q_stride + (size_t)head * D + 4 * grp;
+    const float* qp = p.q + (size_t)(w.q_row + qi) * q_stride + (size_t)head * p.dims + 4 * grp;
     if (half == 0) {  // (the second half takes the first half's operands, below)
 #pragma unroll
       for (int pp = 0; pp < NP; ++pp) {
+        // (dims past the head's own read as zeros)
         float4 a = make_float4(0, 0, 0, 0), b = make_float4(0, 0, 0, 0);
-        if (valid) {
-          a = *reinterpret_cast<const float4*>(qp + 32 * pp);
-          b = *reinterpret_cast<const float4*>(qp + 32 * pp + 16);
-        }
+        if (valid && 32 * pp + 4 * grp < p.dims) a = *reinterpret_cast<const float4*>(qp + 32 * pp);
+        if (valid && 32 * pp + 16 + 4 * grp < p.dims) b = *reinterpret_cast<const float4*>(qp + 32 * pp + 16);
         const float c = p.scale_log2;
         const float x[8] = {a.x * c, a.y * c, a.z * c, a.w * c, b.x * c, b.y * c, b.z * c, b.w * c};
 #pragma unroll
@@ -845,12 +848,12 @@ __device__ __forceinline__ void prefill_body(const AttnParams& p,
       if (w.part < 0) {
         const int qi = w.row_begin + r / w.rows_per_query;
         const int head = w.head_base + r % w.rows_per_query;
-        float* op = p.out + (size_t)(w.q_row + qi) * q_stride + (size_t)head * D + 4 * grp;
+        float* op = p.out + (size_t)(w.q_row + qi) * q_stride + (size_t)head * p.dims + 4 * grp;
 #pragma unroll
         for (int t = 0; t < NT; ++t) {
           float4_t res = float4_t{0, 0, 0, 0};
           if (sum > 0.0f) res = div4(u.o[rg][t], sum);
-          *reinterpret_cast<float4_t*>(op + 16 * t) = res;
+          if (16 * t + 4 * grp < p.dims) *reinterpret_cast<float4_t*>(op + 16 * t) = res;
         }
       } else if (MERGE && p.counters) {  // merged in this launch: coherent stores
 #pragma unroll
@@ -1003,12 +1006,13 @@ __global__ __launch_bounds__(256) void split_reduce_kernel(ReduceParams p) {
   } else {
     if (!active) return;
   }
-  const int q_stride = p.q_heads * D;
+  if (4 * d4 >= p.dims) return;  // a dim past the head's own
+  const int q_stride = p.q_heads * p.dims;
   const int qi = it.row_begin + r / it.rows_per_query;
   const int head = it.head_base + r % it.rows_per_query;
   float4_t res = float4_t{0, 0, 0, 0};
   if (sum > 0.0f) res = div4(acc, sum);
-  *reinterpret_cast<float4_t*>(p.out + (size_t)(it.q_row + qi) * q_stride + (size_t)head * D + 4 * d4) = res;
+  *reinterpret_cast<float4_t*>(p.out + (size_t)(it.q_row + qi) * q_stride + (size_t)head * p.dims + 4 * d4) = res;
 }
 
 }  // namespace

@@ -167,8 +167,9 @@ __global__ __launch_bounds__(64 * kStepWaves) void paged_step_kernel(StepParams 
   const int grp = lane >> 4;
   const int group = p.group;
   const int kv_heads = p.app.kv_heads;
-  const int kv_dim = kv_heads * D;
-  const int q_stride = p.app.q_heads * D;
+  const int dims = p.app.dims;  // the head's own dims (rows of q, k, v, out)
+  const int kv_dim = kv_heads * dims;
+  const int q_stride = p.app.q_heads * dims;
   const int rows = rec.n_new * group;
   // the block geometry is fixed by the kernel's format and head size: taken
   // as constants (no argument load, which the compiler would defer to the
@@ -209,10 +210,15 @@ __global__ __launch_bounds__(64 * kStepWaves) void paged_step_kernel(StepParams 
     const int j = rest >> 1;
     const int pos = rec.ctx + j;
     jb.rr = RowRec{p.tables[rec.table_off + pos / 16], pos % 16, pos};
-    const size_t off = (size_t)(rec.q_row + j) * kv_dim + rec.kv_head * D + jb.b * 32 + jb.quarter * 8;
+    const int d0 = jb.b * 32 + jb.quarter * 8;  // (dims past the head's own store zeros)
+    const size_t off = (size_t)(rec.q_row + j) * kv_dim + rec.kv_head * dims + (d0 < dims ? d0 : 0);
     const float* ks = kbase + off;
     const float* vs = vbase + off;
     load8(jb.x, jb.which ? vs : ks);
+    if (d0 >= dims) {
+#pragma unroll
+      for (int i = 0; i < 8; ++i) jb.x[i] = 0.0f;
+    }
   };
   Job job;
   if (lanes > 0) fetch_job(0, job);
@@ -230,13 +236,13 @@ __global__ __launch_bounds__(64 * kStepWaves) void paged_step_kernel(StepParams 
     const int pp = blk % NP;
     const int rg = blk / NP;
     const int r = rg * 16 + (l & 15);
+    const int d = 32 * pp + 4 * (l >> 4);  // (dims past the head's own read as zeros)
     if (idx < QUNIT && r < rows) {
       const int qi = r / group;
       const int head = rec.kv_head * group + r % group;
-      const float* qp =
-          p.q + (size_t)(rec.q_row + qi) * q_stride + (size_t)head * D + 32 * pp + 4 * (l >> 4);
-      qa[k] = *reinterpret_cast<const float4*>(qp);
-      qb[k] = *reinterpret_cast<const float4*>(qp + 16);
+      const float* qp = p.q + (size_t)(rec.q_row + qi) * q_stride + (size_t)head * dims + d;
+      qa[k] = d < dims ? *reinterpret_cast<const float4*>(qp) : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+      qb[k] = d + 16 < dims ? *reinterpret_cast<const float4*>(qp + 16) : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
     } else {
       qa[k] = qb[k] = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
     }
@@ -364,8 +370,9 @@ __global__ __launch_bounds__(64 * kStepWaves) void paged_step_kernel(StepParams 
           const int head = rec.kv_head * group + r % group;
           float4_t res = float4_t{0, 0, 0, 0};
           if (sum > 0.0f) res = div4(acc, sum);
-          *reinterpret_cast<float4_t*>(p.out + (size_t)(rec.q_row + qi) * q_stride + (size_t)head * D +
-                                       4 * d4) = res;
+          if (4 * d4 < dims)
+            *reinterpret_cast<float4_t*>(p.out + (size_t)(rec.q_row + qi) * q_stride + (size_t)head * dims +
+                                         4 * d4) = res;
         } else {
           const uint32_t slot_row = (uint32_t)rec.part * p.rows_cap + r;
           store_partial(rs_o, (slot_row * D + 4 * d4) * 4, acc);
@@ -466,7 +473,8 @@ __global__ __launch_bounds__(64 * kStepWaves) void paged_step_kernel(StepParams 
         const int head = rec.kv_head * group + r % group;
         float4_t res = float4_t{0, 0, 0, 0};
         if (sum > 0.0f) res = div4(acc, sum);
-        *reinterpret_cast<float4_t*>(p.out + (size_t)(rec.q_row + qi) * q_stride + (size_t)head * D + 4 * d4) = res;
+        if (4 * d4 < dims)
+          *reinterpret_cast<float4_t*>(p.out + (size_t)(rec.q_row + qi) * q_stride + (size_t)head * dims + 4 * d4) = res;
       }
     } else {
       // one pass (slices * pairs <= the workgroup): park the slice sums
@@ -491,7 +499,8 @@ __global__ __launch_bounds__(64 * kStepWaves) void paged_step_kernel(StepParams 
         const int head = rec.kv_head * group + rr % group;
         float4_t res = float4_t{0, 0, 0, 0};
         if (su > 0.0f) res = div4(a, su);
-        *reinterpret_cast<float4_t*>(p.out + (size_t)(rec.q_row + qi) * q_stride + (size_t)head * D + 4 * dd) = res;
+        if (4 * dd < dims)
+          *reinterpret_cast<float4_t*>(p.out + (size_t)(rec.q_row + qi) * q_stride + (size_t)head * dims + 4 * dd) = res;
       }
     }
   }

@@ -75,6 +75,7 @@ int backend_ready() {
 struct tge_kv_pool {
   tge_kv_pool_desc desc{};
   void* blocks = nullptr;   // layers x (pages * kv_heads) page blocks
+  int bd = 0;               // block width (dims per token of a page block)
   tge::BlockGeom geom{};
   size_t layer_blocks = 0;  // pages * kv_heads
   size_t bytes = 0;
@@ -131,7 +132,7 @@ struct AttnPlan {
   tge::plan::Staged image;  // work | reduce | wg_first
   size_t off_reduce = 0;
   size_t off_first = 0;
-  tge::plan::Scratch part_o;   // [parts][rows_cap][head_dim] fp32
+  tge::plan::Scratch part_o;   // [parts][rows_cap][block width] fp32
   tge::plan::Scratch part_ml;  // [parts][rows_cap][2] fp32
   ~AttnPlan() {
     image.release(g_mem);
@@ -239,10 +240,12 @@ int tge_kv_pool_create(const tge_kv_pool_desc* desc, tge_kv_pool** out) {
   const tge_kv_pool_desc& d = *desc;
   if (d.layers <= 0 || d.pages <= 0 || d.kv_heads <= 0)
     return fail(TGE_ERR_INVALID, "kv_pool_create: non-positive size");
-  if (d.head_dim != 64 && d.head_dim != 128)
-    return fail(TGE_ERR_INVALID, "kv_pool_create: head_dim must be 64 or 128");
   if (d.format != TGE_KV_F16 && d.format != TGE_KV_I8)
     return fail(TGE_ERR_INVALID, "kv_pool_create: unknown format");
+  if (tge::block_dims_for(d.head_dim, d.format) == 0)
+    return fail(TGE_ERR_INVALID, d.format == TGE_KV_I8
+                                     ? "kv_pool_create: int8 head_dim must be 32, 64, 96 or 128"
+                                     : "kv_pool_create: head_dim must be a multiple of 16 up to 128");
   if (d.format == TGE_KV_I8 && d.scale_format != TGE_SCALE_F16 &&
       d.scale_format != TGE_SCALE_F32)
     return fail(TGE_ERR_INVALID, "kv_pool_create: unknown scale format");
@@ -251,7 +254,8 @@ int tge_kv_pool_create(const tge_kv_pool_desc* desc, tge_kv_pool** out) {
 
   auto* p = new tge_kv_pool;
   p->desc = d;
-  p->geom = tge::block_geom(d.format, d.head_dim, d.format == TGE_KV_I8 && d.scale_format == TGE_SCALE_F32);
+  p->bd = tge::block_dims_for(d.head_dim, d.format);
+  p->geom = tge::block_geom(d.format, p->bd, d.format == TGE_KV_I8 && d.scale_format == TGE_SCALE_F32);
   p->layer_blocks = (size_t)d.pages * d.kv_heads;
   // Kernels address a page block by its 64-bit address (one buffer
   // resource per block), so a layer's array has no 32-bit limit.
@@ -287,6 +291,7 @@ int tge_kv_pool_layer(const tge_kv_pool* p, int layer, tge_kv_layer_view* out) {
   out->v = base + p->geom.v_off();
   out->k_scales = i8 ? base + p->geom.ks_off() : nullptr;
   out->v_scales = i8 ? base + p->geom.vs_off() : nullptr;
+  out->block_dims = p->bd;
   out->kv_block_bytes = (size_t)p->geom.kv_bytes;
   out->scale_block_bytes = (size_t)p->geom.scale_bytes;
   out->block_bytes = (size_t)p->geom.block_bytes;
@@ -322,8 +327,9 @@ void tge_batch_destroy(tge_batch* b) { delete b; }
 
 namespace {
 
-// Uploads an attention plan's lists and sizes its split-K partial buffers.
-int upload_plan(AttnPlan& pl, int head_dim, hipStream_t st) {
+// Uploads an attention plan's lists and sizes its split-K partial buffers
+// (rows of the page blocks' width).
+int upload_plan(AttnPlan& pl, int block_dims, hipStream_t st) {
   pl.built = false;
   const size_t total = tge::plan::image_layout(pl.lists, &pl.off_reduce, &pl.off_first);
   int s = pl.image.upload(g_mem, total, st, [&](char* h) {
@@ -332,7 +338,7 @@ int upload_plan(AttnPlan& pl, int head_dim, hipStream_t st) {
   if (s != TGE_OK) return s;
   const size_t rows_cap = 16 * (size_t)pl.lists.row_groups;
   const size_t parts = (size_t)std::max(pl.lists.parts, 1);
-  s = pl.part_o.reserve(g_mem, parts * rows_cap * head_dim * sizeof(float), st);
+  s = pl.part_o.reserve(g_mem, parts * rows_cap * block_dims * sizeof(float), st);
   if (s == TGE_OK) s = pl.part_ml.reserve(g_mem, parts * rows_cap * 2 * sizeof(float), st);
   if (s != TGE_OK) return s;
   pl.built = true;
@@ -400,11 +406,11 @@ int build_decode_plan(tge_batch* b, const tge_kv_pool* p, AttnPlan& pl, int only
   const bool sparse = b->sp_stride > 0;
   const int sf32 = p->desc.scale_format == TGE_SCALE_F32;
   tge::plan::build_decode(b->step,
-                          mixed ? resident_groups_mixed(p->desc.format, sf32, b->step.head_dim, rg)
-                                : resident_groups(p->desc.format, sf32, b->step.head_dim, rg, sparse),
+                          mixed ? resident_groups_mixed(p->desc.format, sf32, b->step.block_dims, rg)
+                                : resident_groups(p->desc.format, sf32, b->step.block_dims, rg, sparse),
                           pl.lists, only);
   pl.sparse = sparse;
-  return upload_plan(pl, b->step.head_dim, st);
+  return upload_plan(pl, b->step.block_dims, st);
 }
 
 }  // namespace
@@ -427,7 +433,7 @@ int upload_step_plan(tge_batch* b, const tge_kv_pool* pool, hipStream_t st) {
   if (s != TGE_OK) return s;
   const size_t rows_cap = 16 * (size_t)L.row_groups;
   const size_t parts = (size_t)std::max(L.parts, 1);
-  s = sp.part_o.reserve(g_mem, parts * rows_cap * b->step.head_dim * sizeof(float), st);
+  s = sp.part_o.reserve(g_mem, parts * rows_cap * b->step.block_dims * sizeof(float), st);
   if (s == TGE_OK) s = sp.part_ml.reserve(g_mem, parts * rows_cap * 2 * sizeof(float), st);
   if (s != TGE_OK) return s;
   const size_t had = sp.counters.bytes;
@@ -577,6 +583,7 @@ tge::AttnParams attn_params(const tge_batch* b, const tge_kv_pool* p, int layer,
   a.rows_cap = 16 * pl.lists.row_groups;
   a.kv_heads = b->step.kv_heads;
   a.q_heads = b->step.q_heads;
+  a.dims = b->step.head_dim;
   a.scale_log2 = (float)(1.4426950408889634 / std::sqrt((double)b->step.head_dim));
   return a;
 }
@@ -611,11 +618,11 @@ int run_attention(const tge_batch* b, const tge_kv_pool* p, int layer, const flo
   if (ps != TGE_OK) return ps;
   if (ev) TGE_HIP(hipEventRecord((*ev)[0], st));
   if (decode) {
-    TGE_HIP(tge::launch_decode(p->desc.format, p->desc.scale_format == TGE_SCALE_F32, b->step.head_dim,
+    TGE_HIP(tge::launch_decode(p->desc.format, p->desc.scale_format == TGE_SCALE_F32, b->step.block_dims,
                                pl.lists.row_groups, pl.lists.groups, a, st));
   } else {
     TGE_HIP(tge::launch_prefill(p->desc.format, p->desc.scale_format == TGE_SCALE_F32,
-                                b->step.head_dim, (int)pl.lists.work.size(), a, st));
+                                b->step.block_dims, (int)pl.lists.work.size(), a, st));
   }
   if (ev) TGE_HIP(hipEventRecord((*ev)[1], st));
   if (!pl.lists.reduce.empty()) {
@@ -626,7 +633,8 @@ int run_attention(const tge_batch* b, const tge_kv_pool* p, int layer, const flo
     r.out = out;
     r.rows_cap = a.rows_cap;
     r.q_heads = b->step.q_heads;
-    TGE_HIP(tge::launch_reduce(b->step.head_dim, (int)pl.lists.reduce.size(), pl.lists.max_splits, r, st));
+    r.dims = b->step.head_dim;
+    TGE_HIP(tge::launch_reduce(b->step.block_dims, (int)pl.lists.reduce.size(), pl.lists.max_splits, r, st));
   }
   if (ev) TGE_HIP(hipEventRecord((*ev)[2], st));
   return TGE_OK;
@@ -649,7 +657,8 @@ int tge_kv_append(const tge_batch* b, tge_kv_pool* p, int layer, const float* k,
   a.rows = reinterpret_cast<const tge::RowRec*>(b->image.dev + b->off_rows);
   a.n_rows = (int)b->step.rows.size();
   a.kv_heads = b->step.kv_heads;
-  a.head_dim = b->step.head_dim;
+  a.head_dim = p->bd;
+  a.dims = b->step.head_dim;
   a.scale_f32 = p->desc.scale_format == TGE_SCALE_F32;
   TGE_HIP(tge::launch_kv_append(p->desc.format, a, static_cast<hipStream_t>(stream)));
   return TGE_OK;
@@ -676,7 +685,8 @@ int tge_kv_append_rope(const tge_batch* b, tge_kv_pool* p, int layer,
   a.rows = reinterpret_cast<const tge::RowRec*>(b->image.dev + b->off_rows);
   a.n_rows = (int)b->step.rows.size();
   a.kv_heads = b->step.kv_heads;
-  a.head_dim = b->step.head_dim;
+  a.head_dim = p->bd;
+  a.dims = b->step.head_dim;
   a.scale_f32 = p->desc.scale_format == TGE_SCALE_F32;
   a.q = r->q;
   a.q_out = r->q_out;
@@ -753,7 +763,8 @@ int tge_decode_step(const tge_batch* b, tge_kv_pool* p, int layer, const float* 
   a.app.pool = view.k;
   a.app.geom = p->geom;
   a.app.kv_heads = b->step.kv_heads;
-  a.app.head_dim = b->step.head_dim;
+  a.app.head_dim = p->bd;
+  a.app.dims = b->step.head_dim;
   a.app.scale_f32 = p->desc.scale_format == TGE_SCALE_F32;
   a.app.q_heads = b->step.q_heads;
   a.recs = reinterpret_cast<const tge::StepRec*>(sp.image.dev);
@@ -767,7 +778,7 @@ int tge_decode_step(const tge_batch* b, tge_kv_pool* p, int layer, const float* 
   a.group = b->step.group;
   a.scale_log2 = (float)(1.4426950408889634 / std::sqrt((double)b->step.head_dim));
   TGE_HIP(tge::launch_step(p->desc.format, p->desc.scale_format == TGE_SCALE_F32,
-                           b->step.head_dim, sp.lists.row_groups, (int)sp.lists.recs.size(), a,
+                           b->step.block_dims, sp.lists.row_groups, (int)sp.lists.recs.size(), a,
                            static_cast<hipStream_t>(stream)));
   return TGE_OK;
 }
@@ -782,8 +793,8 @@ int tge_prefill_attention(const tge_batch* b, const tge_kv_pool* p, int layer,
   tge_batch* mb = const_cast<tge_batch*>(b);
   if (!mb->prefill.built) {
     tge::plan::build_prefill(mb->step, device_cus(), mb->prefill.lists, 0,
-                             tge::prefill_halves(p->desc.format, b->step.head_dim));
-    s = upload_plan(mb->prefill, b->step.head_dim, static_cast<hipStream_t>(stream));
+                             tge::prefill_halves(p->desc.format, b->step.block_dims));
+    s = upload_plan(mb->prefill, b->step.block_dims, static_cast<hipStream_t>(stream));
     if (s != TGE_OK) return s;
   }
   return run_attention(b, p, layer, q, out, stream, b->prefill, false);
@@ -809,7 +820,7 @@ int tge_batch_attention(const tge_batch* b, const tge_kv_pool* p, int layer, con
     s = build_decode_plan(mb, p, mb->mix_decode, 1, st, mb->mix_one);
     if (s != TGE_OK) return s;
     tge::plan::build_prefill(mb->step, device_cus(), mb->mix_prefill.lists, 2);
-    s = upload_plan(mb->mix_prefill, b->step.head_dim, st);
+    s = upload_plan(mb->mix_prefill, b->step.block_dims, st);
     if (s != TGE_OK) return s;
     if (mb->mix_one) {
       const size_t n = mb->mix_decode.lists.reduce.size() + mb->mix_prefill.lists.reduce.size();
@@ -841,7 +852,7 @@ int tge_batch_attention(const tge_batch* b, const tge_kv_pool* p, int layer, con
   s = profile_events(mb, &ev);
   if (s != TGE_OK) return s;
   if (ev) TGE_HIP(hipEventRecord((*ev)[0], st));
-  TGE_HIP(tge::launch_mixed(p->desc.format, p->desc.scale_format == TGE_SCALE_F32, b->step.head_dim,
+  TGE_HIP(tge::launch_mixed(p->desc.format, p->desc.scale_format == TGE_SCALE_F32, b->step.block_dims,
                             b->mix_decode.lists.row_groups, b->mix_decode.lists.groups,
                             (int)b->mix_prefill.lists.work.size(), dec, pf, st));
   if (ev) {
@@ -922,7 +933,8 @@ int tge_decode_attention_static(const tge_batch_desc* d, const tge_kv_pool* p, i
     return fail(TGE_ERR_INVALID, "decode_attention_static: n_new * group exceeds 64 rows");
   const int f = p->desc.format, sf32 = p->desc.scale_format == TGE_SCALE_F32;
   const int rg = std::max(1, std::min(4, (step.max_rows + 15) / 16));
-  tge::plan::build_decode(step, resident_groups(f, sf32, hd, rg, false), lists, 0);
+  const int bd = p->bd;
+  tge::plan::build_decode(step, resident_groups(f, sf32, bd, rg, false), lists, 0);
 
   // scratch: [ sessions | tables | work | reduce | wg_first ] in the first
   // kStaticImageBytes, then part_o [parts][rows_cap][hd] and part_ml
@@ -934,7 +946,7 @@ int tge_decode_attention_static(const tge_batch_desc* d, const tge_kv_pool* p, i
   const size_t total = o_work + l_total;
   const size_t rows_cap = 16 * (size_t)lists.row_groups;
   const size_t parts = (size_t)std::max(lists.parts, 1);
-  const size_t part_floats = parts * rows_cap * hd;
+  const size_t part_floats = parts * rows_cap * bd;
   const size_t part_bytes = (part_floats + parts * rows_cap * 2) * sizeof(float);
   if (total > kStaticImageBytes)
     return fail(TGE_ERR_CAPACITY, "decode_attention_static: the step's plan (" +
@@ -976,8 +988,9 @@ int tge_decode_attention_static(const tge_batch_desc* d, const tge_kv_pool* p, i
   a.rows_cap = (int)rows_cap;
   a.kv_heads = step.kv_heads;
   a.q_heads = step.q_heads;
+  a.dims = hd;
   a.scale_log2 = (float)(1.4426950408889634 / std::sqrt((double)hd));
-  TGE_HIP(tge::launch_decode(f, sf32, hd, lists.row_groups, lists.groups, a, st));
+  TGE_HIP(tge::launch_decode(f, sf32, bd, lists.row_groups, lists.groups, a, st));
   if (!lists.reduce.empty()) {
     tge::ReduceParams r{};
     r.items = reinterpret_cast<const tge::ReduceRec*>(base + o_work + l_red);
@@ -986,7 +999,8 @@ int tge_decode_attention_static(const tge_batch_desc* d, const tge_kv_pool* p, i
     r.out = out;
     r.rows_cap = a.rows_cap;
     r.q_heads = step.q_heads;
-    TGE_HIP(tge::launch_reduce(hd, (int)lists.reduce.size(), lists.max_splits, r, st));
+    r.dims = hd;
+    TGE_HIP(tge::launch_reduce(bd, (int)lists.reduce.size(), lists.max_splits, r, st));
   }
   return TGE_OK;
 }
@@ -1029,12 +1043,13 @@ int tge_attention_group(const tge_attention_group_args* a, void* stream) {
   g.count = a->count;
   g.queries = a->queries;
   g.group_heads = a->group_heads;
+  g.dims = p->desc.head_dim;
   g.scale = a->scale;
   g.maxima = a->maxima;
   g.sums = a->sums;
   g.accumulators = a->accumulators;
   TGE_HIP(tge::launch_attention_group(p->desc.format, p->desc.scale_format == TGE_SCALE_F32,
-                                      p->desc.head_dim, g, static_cast<hipStream_t>(stream)));
+                                      p->bd, g, static_cast<hipStream_t>(stream)));
   return TGE_OK;
 }
 
@@ -1059,7 +1074,8 @@ int tge_kv_gather(const tge_batch* b, const tge_kv_pool* p, int layer, int sessi
   g.table = reinterpret_cast<const int*>(b->image.dev + b->off_tables) + sr.table_off;
   g.count = count;
   g.kv_heads = b->step.kv_heads;
-  g.head_dim = b->step.head_dim;
+  g.head_dim = p->bd;
+  g.dims = b->step.head_dim;
   g.scale_bytes = p->desc.scale_format == TGE_SCALE_F32 ? 4 : 2;
   g.k_rows = k_rows;
   g.v_rows = v_rows;

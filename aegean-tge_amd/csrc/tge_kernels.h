@@ -8,24 +8,28 @@
 
 namespace tge {
 
+// Head sizes: `dims` is the model's head_dim (the row stride of q, k, v,
+// out and the biases); `head_dim` where it remains is the page blocks'
+// width (block_dims_for), whose dims from `dims` on are stored as zeros.
 struct AppendParams {
-  const float* k;  // [n_rows][kv_heads*head_dim]
+  const float* k;  // [n_rows][kv_heads*dims]
   const float* v;
   void* pool;      // layer base: the layer's page blocks
   BlockGeom geom;
   const RowRec* rows;  // device, n_rows
   int n_rows;
   int kv_heads;
-  int head_dim;
+  int head_dim;  // block width
+  int dims;      // the head's dims
   int scale_f32;
   // Fused bias + RoPE (launch_kv_append_rope only): k/v above are the
   // pre-bias, pre-RoPE rows; q (optional) is rotated into q_out.
-  const float* q;  // [n_rows][q_heads*head_dim], or null
+  const float* q;  // [n_rows][q_heads*dims], or null
   float* q_out;    // may alias q
-  const float* q_bias;  // [q_heads*head_dim] or null
-  const float* k_bias;  // [kv_heads*head_dim] or null
+  const float* q_bias;  // [q_heads*dims] or null
+  const float* k_bias;  // [kv_heads*dims] or null
   const float* v_bias;
-  const float* rope_cos;  // [positions][head_dim/2]
+  const float* rope_cos;  // [positions][dims/2]
   const float* rope_sin;
   int q_heads;
   int rope_fma;  // 1: one rounding per output (FMA), 0: product, product, sum
@@ -37,7 +41,8 @@ struct GatherParams {
   const int* table;  // device, the session's page ids
   int count;         // positions to gather
   int kv_heads;
-  int head_dim;
+  int head_dim;      // block width
+  int dims;          // the head's dims (rows of k_rows / v_rows)
   int scale_bytes;  // 2 or 4
   void* k_rows;
   void* v_rows;
@@ -52,14 +57,15 @@ struct AttnParams {
   const WorkRec* work;
   const int* wg_first;  // [grid+1] first work item of each workgroup, or null
   const int* tables;
-  const float* q;
+  const float* q;  // [rows][q_heads*dims]
   float* out;
-  float* part_o;   // [parts][rows_cap][head_dim]
+  float* part_o;   // [parts][rows_cap][block width]
   float* part_ml;  // [parts][rows_cap][2]: max (log2 domain), sum
   int rows_cap;    // 16 * row groups of the plan
   int kv_heads;
   int q_heads;
-  float scale_log2;  // log2(e) / sqrt(head_dim)
+  int dims;          // the head's dims
+  float scale_log2;  // log2(e) / sqrt(dims)
   // Static sparse subset (sp_stride 0: dense): rows whose span exceeds
   // sp_sink + sp_window keep positions < sp_sink, every sp_stride-th one
   // from sp_sink on, and the last sp_window.
@@ -78,6 +84,7 @@ struct ReduceParams {
   float* out;
   int rows_cap;
   int q_heads;
+  int dims;  // the head's dims (out's row stride is q_heads * dims)
 };
 
 // Small decode step (paged_step_kernel): append + attention + split merge.
@@ -85,9 +92,9 @@ struct StepParams {
   AppendParams app;       // pool, geometry, k/v rows, scale format (rows unused)
   const StepRec* recs;    // one per workgroup
   const int* tables;
-  const float* q;
+  const float* q;         // [rows][q_heads*app.dims]
   float* out;
-  float* part_o;          // [parts][rows_cap][head_dim]
+  float* part_o;          // [parts][rows_cap][block width]
   float* part_ml;         // [parts][rows_cap][2]
   int* counters;          // [segments], zero between launches
   int rows_cap;
@@ -106,12 +113,13 @@ struct GroupParams {
   const int* page_ids;   // device, the session's block table
   int first;
   int count;
-  const float* queries;  // [group_heads][head_dim]
+  const float* queries;  // [group_heads][dims]
   int group_heads;
+  int dims;              // the head's dims
   float scale;
   float* maxima;         // [group_heads]
   float* sums;           // [group_heads]
-  float* accumulators;   // [group_heads][head_dim]
+  float* accumulators;   // [group_heads][dims]
 };
 
 hipError_t launch_kv_append(int format, const AppendParams& p, hipStream_t stream);

@@ -135,6 +135,7 @@ int build_step(Step& step, int ns, const int* ctx, const int* n_new, const int* 
   }
   step.kv_heads = kv_heads;
   step.head_dim = head_dim;
+  step.block_dims = head_dim <= 64 ? 64 : 128;
   step.q_heads = q_heads;
   step.group = group;
   step.pages = pool_pages;
@@ -397,12 +398,12 @@ bool build_step_lists(const Step& b, bool i8, bool scale_f32, StepLists& out) {
   // 64 rows at head_dim 128 (48 with int8 K/V and fp32 scales) do not fit
   // the step kernel's registers beside its page images (it would spill);
   // those steps take the decode kernel
-  if (!step_fits(i8, scale_f32, b.head_dim, b.max_rows)) return false;
+  if (!step_fits(i8, scale_f32, b.block_dims, b.max_rows)) return false;
   out.row_groups = std::max(1, std::min(4, (b.max_rows + 15) / 16));
   // A piece is a whole number of batches (every wave of the workgroup loads
   // one batch of pages at once), as few as keep every context within
   // kStepMaxParts pieces.
-  const int batch = kStepWaves * step_batch_pages(i8, scale_f32, b.head_dim, out.row_groups);
+  const int batch = kStepWaves * step_batch_pages(i8, scale_f32, b.block_dims, out.row_groups);
   const int heads = kStepMaxParts - 1;  // pieces before the appending one
   const int piece = batch * std::max(1, (max_pages + batch * heads - 1) / (batch * heads));
   out.piece_pages = piece;

@@ -41,7 +41,8 @@ class PoolDesc(C.Structure):
 class LayerView(C.Structure):
     _fields_ = [("k", C.c_void_p), ("v", C.c_void_p), ("k_scales", C.c_void_p),
                 ("v_scales", C.c_void_p), ("kv_block_bytes", C.c_size_t),
-                ("scale_block_bytes", C.c_size_t), ("block_bytes", C.c_size_t)]
+                ("scale_block_bytes", C.c_size_t), ("block_bytes", C.c_size_t),
+                ("block_dims", C.c_int)]
 
 
 class BatchDesc(C.Structure):

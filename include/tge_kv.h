@@ -77,16 +77,22 @@ const char* tge_backend_arch(void);
 
 /* ---------------------------------------------------------------------------
  * Page pool. Device memory for `layers` x `pages` x `kv_heads` page blocks.
- * Each page block holds TGE_PAGE_TOKENS tokens of one KV head, its parts
- * back to back (one contiguous run of memory per block):
- *   K part, then V part: 16 * head_dim elements each (f16 bits or int8 codes)
- *   I8 only, K scales, then V scales: 16 * head_dim/32 scales each (f16 bits
- *   or fp32)
+ * Each page block holds TGE_PAGE_TOKENS tokens of one KV head at the block
+ * width W = 64 (head_dim <= 64) or 128 (head_dim <= 128), dims from head_dim
+ * on stored as zeros, its parts back to back (one contiguous run of memory
+ * per block):
+ *   K part, then V part: 16 * W elements each (f16 bits or int8 codes)
+ *   I8 only, K scales, then V scales: 16 * W/32 scales each (f16 bits or
+ *   fp32)
  * Block (page, kv_head) of a layer is block number page*kv_heads + kv_head.
  * Element (token t, dim d) of a block's part sits at:
- *   K: tge_kv_k_index(t, d, head_dim)      V: tge_kv_v_index(t, d, head_dim)
- *   scale of (t, block b = d/32): tge_kv_scale_index(t, b, head_dim)
- * head_dim must be 64 or 128 (the configurations' head sizes).
+ *   K: tge_kv_k_index(t, d, W)      V: tge_kv_v_index(t, d, W)
+ *   scale of (t, block b = d/32): tge_kv_scale_index(t, b, W)
+ * head_dim: a multiple of 16 up to 128 (F16) or of 32 up to 128 (I8, whose
+ * scales cover 32-dim blocks). The reference takes any head_dim > 0
+ * (attention_scalar.cpp:11-14; int8 % 32, qwen2.cpp:406-409); wider heads
+ * (e.g. 256) are not supported here. q, k, v and out rows always have the
+ * model's head_dim.
  * ------------------------------------------------------------------------ */
 typedef struct tge_kv_pool tge_kv_pool;
 
@@ -109,6 +115,7 @@ typedef struct {
   size_t kv_block_bytes;    /* bytes of one K (or V) part */
   size_t scale_block_bytes; /* bytes of one scale part (0 for F16) */
   size_t block_bytes;       /* bytes of a whole page block: the block stride */
+  int block_dims;           /* the block width W (64 or 128) */
 } tge_kv_layer_view;
 
 int tge_kv_pool_create(const tge_kv_pool_desc* desc, tge_kv_pool** out);
@@ -124,7 +131,9 @@ size_t tge_kv_pool_bytes(const tge_kv_pool* pool);
 int tge_kv_copy_page(tge_kv_pool* pool, int src_page, int dst_page, void* stream);
 
 /* In-page element index of (token, dim) for K and V blocks, and of the
- * scale of (token, 32-dim block). With NP = head_dim/32:
+ * scale of (token, 32-dim block), for blocks of width W (the third
+ * argument, 64 or 128; the pool's tge_kv_layer_view.block_dims). With
+ * NP = W/32:
  *   K:     ((((d/4)&3)*16 + t)*NP + d/32)*8 + ((d/16)&1)*4 + (d&3)
  *   V:     ((t/4*16 + (d&15))*NP + d/32)*8 + ((d/16)&1)*4 + (t&3)
  *   scale: ((t/4)*NP + b)*4 + (t&3) */

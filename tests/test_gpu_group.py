@@ -54,6 +54,9 @@ CASES = {
                              [(0, 900), (5, 16), (100, 611), (16, 16)]),
     "i8_d64_g1_f32scales": (2, 2, 64, tk.KV_I8, tk.SCALE_F32, 300, [(0, 300), (17, 2)]),
     "f16_d128_g16": (32, 2, 128, tk.KV_F16, 0, 700, [(0, 700), (333, 64)]),
+    # head sizes the pool pads to the block width
+    "f16_d80_g7": (14, 2, 80, tk.KV_F16, 0, 500, [(0, 500), (33, 100)]),
+    "i8_d96_g4_f32scales": (16, 4, 96, tk.KV_I8, tk.SCALE_F32, 400, [(0, 400), (7, 64)]),
 }
 
 

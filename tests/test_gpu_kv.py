@@ -22,15 +22,20 @@ def say(*a):
 
 def raw_pool_rows(case, layer, s, count):
     """Decode positions [0, count) of session s straight from the pool bytes
-    with the documented layout formulas (independent of tge_kv_gather)."""
+    with the documented layout formulas (independent of tge_kv_gather); the
+    dims of a block past the head's own must hold zeros (codes, bits and
+    the scales of whole padding blocks)."""
     view = case.pool.layer(layer)
     pages = case.pool.pages
+    W = view.block_dims
+    assert W == (64 if case.hd <= 64 else 128)
     elem = np.uint16 if case.fmt == tk.KV_F16 else np.int8
     esz = np.dtype(elem).itemsize
     bb = view.block_bytes
-    assert view.v - view.k == 16 * case.hd * esz == view.kv_block_bytes
+    assert view.v - view.k == 16 * W * esz == view.kv_block_bytes
+    sbytes = 0
     if case.fmt == tk.KV_I8:
-        sbytes = 16 * (case.hd // 32) * (4 if case.sf == tk.SCALE_F32 else 2)
+        sbytes = 16 * (W // 32) * (4 if case.sf == tk.SCALE_F32 else 2)
         assert view.scale_block_bytes == sbytes and bb == 2 * view.kv_block_bytes + 2 * sbytes
         assert view.k_scales - view.k == 2 * view.kv_block_bytes
         assert view.v_scales - view.k_scales == sbytes
@@ -38,21 +43,29 @@ def raw_pool_rows(case, layer, s, count):
         assert bb == 2 * view.kv_block_bytes and not view.k_scales
     raw = tk.hip().download(view.k, np.empty(pages * case.kvh * bb, np.uint8))
     t = np.arange(16)[:, None]
-    d = np.arange(case.hd)[None, :]
-    n = case.hd // 32
+    d = np.arange(W)[None, :]
+    n = W // 32
     kidx = ((((d >> 2) & 3) * 16 + t) * n + (d >> 5)) * 8 + (((d >> 4) & 1) << 2) + (d & 3)
     vidx = (((t >> 2) * 16 + (d & 15)) * n + (d >> 5)) * 8 + (((d >> 4) & 1) << 2) + (t & 3)
+    sidx = ((t >> 2) * n + np.arange(n)[None, :]) * 4 + (t & 3)
     k = np.empty((count, case.kv_dim), elem)
     v = np.empty((count, case.kv_dim), elem)
     for pos0 in range(0, count, 16):
         page = case.pages[s][pos0 // 16]
-        n = min(16, count - pos0)
+        n_t = min(16, count - pos0)
         for h in range(case.kvh):
             blk = raw[(page * case.kvh + h) * bb:(page * case.kvh + h + 1) * bb]
-            kpart = blk[:view.kv_block_bytes].view(elem)
-            vpart = blk[view.kv_block_bytes:2 * view.kv_block_bytes].view(elem)
-            k[pos0:pos0 + n, h * case.hd:(h + 1) * case.hd] = kpart[kidx][:n]
-            v[pos0:pos0 + n, h * case.hd:(h + 1) * case.hd] = vpart[vidx][:n]
+            kpart = blk[:view.kv_block_bytes].view(elem)[kidx][:n_t]
+            vpart = blk[view.kv_block_bytes:2 * view.kv_block_bytes].view(elem)[vidx][:n_t]
+            k[pos0:pos0 + n_t, h * case.hd:(h + 1) * case.hd] = kpart[:, :case.hd]
+            v[pos0:pos0 + n_t, h * case.hd:(h + 1) * case.hd] = vpart[:, :case.hd]
+            assert not kpart[:, case.hd:].any() and not vpart[:, case.hd:].any(), "padding dims"
+            if sbytes and case.hd < W:
+                sc = blk[2 * view.kv_block_bytes:].view(np.uint8)
+                ks = sc[:sbytes].view(np.uint16 if case.sf != tk.SCALE_F32 else np.uint32)
+                vs = sc[sbytes:2 * sbytes].view(ks.dtype)
+                pad = sidx[:n_t, case.hd // 32:]
+                assert not ks[pad].any() and not vs[pad].any(), "padding scales"
     return k, v
 
 
@@ -436,6 +449,11 @@ def test_prefill_i8_matches_oracle(gpu):
     (tk.KV_I8, tk.SCALE_F16, 4, 128, True),
     (tk.KV_I8, tk.SCALE_F32, 2, 64, False),
     (tk.KV_F16, tk.SCALE_F16, 2, 64, False),
+    # head sizes padded to the block width (the NeoX halves are the head's:
+    # pairs (i, i + head_dim/2))
+    (tk.KV_F16, tk.SCALE_F16, 2, 80, True),
+    (tk.KV_I8, tk.SCALE_F16, 2, 96, False),
+    (tk.KV_F16, tk.SCALE_F16, 1, 48, False),
 ])
 def test_append_rope_bitexact(gpu, fmt, sf, kvh, hd, fma):
     """Fused bias + RoPE + append (tge_kv_append_rope): the pool contents and
@@ -682,6 +700,47 @@ def test_random_cases(gpu, i):
     err = assert_attention_close(got, case.oracle_out(), f"random case {i}")
     say(f"  max abs err {err:.2e}")
     b.close()
+    case.close()
+
+
+# Head sizes between the block widths: (q_heads, kv_heads, head_dim, format,
+# scale format); dims past the head's own are stored as zeros and every
+# path reads and writes only the head's own dims of q, k, v and out.
+HEAD_SIZES = {
+    "f16_d80": (14, 2, 80, tk.KV_F16, 0),
+    "f16_d112_g4": (16, 4, 112, tk.KV_F16, 0),
+    "f16_d48_g8": (8, 1, 48, tk.KV_F16, 0),
+    "f16_d16": (4, 2, 16, tk.KV_F16, 0),
+    "i8_d96_f16scales": (12, 2, 96, tk.KV_I8, tk.SCALE_F16),
+    "i8_d32_f32scales": (8, 4, 32, tk.KV_I8, tk.SCALE_F32),
+}
+
+
+@pytest.mark.parametrize("name", list(HEAD_SIZES))
+@pytest.mark.parametrize("kind", ["decode", "step", "prefill", "mixed"])
+def test_head_sizes_between_block_widths(gpu, name, kind):
+    """Decode (the decode kernel and the one-launch step), block prefill and
+    a mixed step at head sizes the pool pads to 64 or 128 dims: attention
+    against the oracle at the model's head_dim, the stored rows bit-exact
+    (gather and raw layout, padding zero)."""
+    qh, kvh, hd, fmt, sf = HEAD_SIZES[name]
+    group = qh // kvh
+    contexts = [700, 0, 33, 1600] if kind != "prefill" else [0, 160, 517]
+    if kind in ("decode", "step"):
+        n_new = [max(1, min(3, 64 // group))] * len(contexts)
+    elif kind == "mixed":
+        n_new = [2, 90, 1, 40]
+    else:
+        n_new = [70, 33, 129]
+    say(f"head size case {name} {kind}: contexts {contexts} n_new {n_new}")
+    case = PagedCase(qh, kvh, hd, fmt, contexts, n_new, scale_format=sf, seed=7100 + hd,
+                     outlier_frac=0.01 if fmt == tk.KV_I8 else 0)
+    case.fill()
+    got, b = case.step(kind=kind)
+    err = assert_attention_close(got, case.oracle_out(), f"head size {name} {kind}")
+    say(f"  max abs err {err:.2e}")
+    b.close()
+    check_contents(case)
     case.close()
 
 
