@@ -266,7 +266,10 @@ __global__ __launch_bounds__(64 * kStepWaves) void paged_step_kernel(StepParams 
     for (int i = 0; i < PB; ++i)
       load_page<FMT, SF32, D>(r[i], pool + ((size_t)ids[i] * kv_heads + rec.kv_head) * bb, lane, grp);
   };
-  if (!rec.append) first_batch();
+  // (an appending piece whose first batch ends before the new positions
+  // issues it now as well)
+  const bool early = !rec.append || rec.page_begin + W * PB <= rec.ctx / 16;
+  if (early) first_batch();
 
 #pragma unroll
   for (int k = 0; k < QPER; ++k) {
@@ -287,7 +290,7 @@ __global__ __launch_bounds__(64 * kStepWaves) void paged_step_kernel(StepParams 
     __threadfence_block();  // the stored rows before any wave reads their page
   }
   __syncthreads();  // the Q table is written (and the new rows stored)
-  if (rec.append) first_batch();
+  if (!early) first_batch();
 
   // ---- the piece's pages ---------------------------------------------------
   U u;

@@ -384,6 +384,12 @@ void build_prefill(const Step& b, int cus, AttnLists& pl, int only, int halves) 
   pl.groups = (int)pl.work.size();
 }
 
+// When every context of the step fits this many batches, each is one piece:
+// a batch more per wave (about a microsecond) costs less than the split
+// merge it saves (the partials' coherent stores, the arrival counter and
+// the last piece's reads, 3-4 microseconds), and no piece waits for another.
+constexpr int kStepUnsplitBatches = 3;
+
 bool build_step_lists(const Step& b, bool i8, bool scale_f32, StepLists& out) {
   out = StepLists{};
   if (b.max_rows > kMaxRows || b.sessions.empty()) return false;
@@ -407,6 +413,7 @@ bool build_step_lists(const Step& b, bool i8, bool scale_f32, StepLists& out) {
   const int heads = kStepMaxParts - 1;  // pieces before the appending one
   const int piece = batch * std::max(1, (max_pages + batch * heads - 1) / (batch * heads));
   out.piece_pages = piece;
+  const bool unsplit = max_pages <= kStepUnsplitBatches * batch;
   for (int s = 0; s < (int)b.sessions.size(); ++s) {
     const SessionRec& sr = b.sessions[(std::size_t)s];
     const int pages = (sr.ctx + sr.n_new + 15) / 16;
@@ -415,7 +422,7 @@ bool build_step_lists(const Step& b, bool i8, bool scale_f32, StepLists& out) {
     // the remainder), then one piece of the pages the new positions fall in
     // (at most 5: n_new <= 64), which stores the new rows first.
     const int written = sr.ctx / 16;
-    const int head = pages <= piece ? 0 : (written + piece - 1) / piece;
+    const int head = unsplit || pages <= piece ? 0 : (written + piece - 1) / piece;
     const int n = head + 1;
     out.max_pieces = std::max(out.max_pieces, n);
     for (int h = 0; h < b.kv_heads; ++h) {

@@ -196,7 +196,11 @@ void check_step_lists(const Step& st, bool i8, bool sf32) {
     return;
   }
   REQUIRE(16 * sl.row_groups >= st.max_rows && sl.row_groups <= 4, "row groups %d", sl.row_groups);
-  const int batch = kStepWaves * step_batch_pages(i8, sf32, st.head_dim, sl.row_groups);
+  const int batch = kStepWaves * step_batch_pages(i8, sf32, st.block_dims, sl.row_groups);
+  int step_pages = 0;  // the step's longest context, in pages
+  for (const SessionRec& sr : st.sessions) step_pages = std::max(step_pages, (sr.ctx + sr.n_new + 15) / 16);
+  // every context within three batches: each is one piece (no split merge)
+  const bool unsplit = step_pages <= 3 * batch;
   REQUIRE(sl.piece_pages >= batch && sl.piece_pages % batch == 0, "piece %d batch %d",
           sl.piece_pages, batch);
   REQUIRE(sl.piece_pages == batch || sl.max_pieces > kStepMaxParts / 2, "pieces longer than needed");
@@ -226,8 +230,9 @@ void check_step_lists(const Step& st, bool i8, bool sf32) {
           REQUIRE(r.page_end - r.page_begin == sl.piece_pages || k == 0, "piece length");
           REQUIRE(r.page_end - r.page_begin <= sl.piece_pages, "first piece length");
         } else {
-          REQUIRE(pages <= sl.piece_pages, "one piece of %d pages", pages);
+          REQUIRE(pages <= sl.piece_pages || unsplit, "one piece of %d pages", pages);
         }
+        REQUIRE(!unsplit || n == 1, "a split context in a step of short contexts");
         at = r.page_end;
         REQUIRE(r.append == (k == n - 1), "append flag");
         if (r.append) REQUIRE(16 * r.page_begin <= sr.ctx, "new positions before the last piece");
