@@ -396,6 +396,47 @@ __device__ __forceinline__ float4_t scales4(const uint32_t* s, int b) {
   }
 }
 
+// Byte address within the workgroup's LDS of a pointer into it.
+__device__ __forceinline__ uint32_t lds_addr(const char* p) {
+  return (uint32_t)(uintptr_t)(const __attribute__((address_space(3))) char*)p;
+}
+// 8 bytes of LDS at addr + OFF into an f16x4, as one ds_read_b64 that the
+// compiler neither fuses with its neighbours nor waits for: the caller
+// waits with lds_wait_operands before any use of the result.
+template <int OFF>
+__device__ __forceinline__ half4_t lds_read_b64(uint32_t addr) {
+  static_assert(OFF >= 0 && OFF < 65536, "ds offset field");
+  half4_t v;
+  asm volatile("ds_read_b64 %0, %1 offset:%2" : "=v"(v) : "v"(addr), "i"(OFF));
+  return v;
+}
+// The PV operands of a page pair from its two LDS slots (lane chunk bases
+// la, lb): operand (pp, h) = page A's then page B's 8 bytes at 1024*pp + 8*h.
+template <int PP, int NP>
+__device__ __forceinline__ void read_v_pairs(half8_t (&v8)[NP][2], uint32_t la, uint32_t lb) {
+  if constexpr (PP < NP) {
+    const half4_t a0 = lds_read_b64<1024 * PP>(la), b0 = lds_read_b64<1024 * PP>(lb);
+    const half4_t a1 = lds_read_b64<1024 * PP + 8>(la), b1 = lds_read_b64<1024 * PP + 8>(lb);
+    v8[PP][0] = half8_t{a0[0], a0[1], a0[2], a0[3], b0[0], b0[1], b0[2], b0[3]};
+    v8[PP][1] = half8_t{a1[0], a1[1], a1[2], a1[3], b1[0], b1[1], b1[2], b1[3]};
+    read_v_pairs<PP + 1, NP>(v8, la, lb);
+  }
+}
+// Waits for this wave's LDS reads; the operands pass through the wait, so
+// no use of them can be scheduled before it.
+template <int NP>
+__device__ __forceinline__ void lds_wait_operands(half8_t (&v)[NP][2]) {
+  static_assert(NP == 2 || NP == 4, "64 or 128 dims");
+  if constexpr (NP == 2) {
+    asm volatile("s_waitcnt lgkmcnt(0)"
+                 : "+v"(v[0][0]), "+v"(v[0][1]), "+v"(v[1][0]), "+v"(v[1][1]));
+  } else {
+    asm volatile("s_waitcnt lgkmcnt(0)"
+                 : "+v"(v[0][0]), "+v"(v[0][1]), "+v"(v[1][0]), "+v"(v[1][1]), "+v"(v[2][0]),
+                   "+v"(v[2][1]), "+v"(v[3][0]), "+v"(v[3][1]));
+  }
+}
+
 #define MFMA16x16x16(a, b, c) __builtin_amdgcn_mfma_f32_16x16x16f16((a), (b), (c), 0, 0, 0)
 #define MFMA16x16x32(a, b, c) __builtin_amdgcn_mfma_f32_16x16x32_f16((a), (b), (c), 0, 0, 0)
 
@@ -538,23 +579,23 @@ struct Unit {
     Regs ra, rb;
     read_half<FMT, SF32, D, false>(ra, slot_a, lane, grp);
     read_half<FMT, SF32, D, false>(rb, slot_b, lane, grp);
+    // V operands: page A's 8 bytes and page B's 8 bytes side by side in one
+    // operand, each read by its own ds_read_b64 into its half of the
+    // operand's registers (written as plain loads, the compiler fuses a
+    // lane's two halves into one 16-byte read and splits it with moves).
+    // The reads are not tracked by the compiler: lds_wait_operands below
+    // waits for them before the first use.
+    const uint32_t la = lds_addr(slot_a + RG::KV_BYTES + 16 * lane);
+    const uint32_t lb = lds_addr(slot_b + RG::KV_BYTES + 16 * lane);
     half8_t v8[NP][2];
-#pragma unroll
-    for (int pp = 0; pp < NP; ++pp) {
-#pragma unroll
-      for (int h = 0; h < 2; ++h) {
-        const int off = RG::KV_BYTES + pp * 1024 + 16 * lane + 8 * h;
-        const half4_t va = *reinterpret_cast<const half4_t*>(slot_a + off);
-        const half4_t vb = *reinterpret_cast<const half4_t*>(slot_b + off);
-        v8[pp][h] = half8_t{va[0], va[1], va[2], va[3], vb[0], vb[1], vb[2], vb[3]};
-      }
-    }
+    read_v_pairs<0, NP>(v8, la, lb);
     float4_t sa[NRG], sb[NRG];
     start_scores(sa, sb);
     scores_onto(ra, qf, sa);
     scores_onto(rb, qf, sb);
     half8_t pw[NRG];
     softmax2(sa, sb, pia, pib, grp, masked_a, masked_b, pw);
+    lds_wait_operands<NP>(v8);
     values2([&](int pp, int h) __attribute__((always_inline)) { return v8[pp][h]; }, pw);
   }
 
