@@ -508,10 +508,10 @@ def run_mixed(tk, synth, cfg, decode_sessions=32, chunk=512, prompt_done=1536, r
     """A continuous-batching step on the c5 shape (one layer's attention):
     `decode_sessions` sessions verifying 4 draft tokens next to one session
     prefilling a `chunk`-token chunk after `prompt_done` prompt tokens.
-    Times the mixed call (tge_batch_attention: decode kernel for the short
-    sessions, block-prefill kernel for the chunk), the same step forced
-    through the block-prefill kernel alone, and the two kinds as separate
-    steps."""
+    Times the mixed call (tge_batch_attention: one paged_mixed_kernel
+    launch whose workgroups take the decode shares of the short sessions
+    and the block-prefill tiles of the chunk), the same step forced through
+    the block-prefill kernel alone, and the two kinds as separate steps."""
     from types import SimpleNamespace
     sh = cfg.shape
     ctxs = list(cfg.contexts[:decode_sessions]) + [prompt_done]
