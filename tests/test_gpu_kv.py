@@ -744,6 +744,34 @@ def test_head_sizes_between_block_widths(gpu, name, kind):
     case.close()
 
 
+@pytest.mark.parametrize("kind", ["decode", "prefill", "mixed"])
+def test_head_size_96_int8_sparse(gpu, kind):
+    """The static sparse subset at a padded head size (int8, 96 dims in
+    128-dim blocks): decode, block prefill and mixed steps against the
+    oracle's sparse head."""
+    contexts, n_new = [3000, 150, 900], ([2, 2, 2] if kind == "decode" else
+                                        [40, 2, 70] if kind == "mixed" else [60, 20, 33])
+    case = PagedCase(12, 2, 96, tk.KV_I8, contexts, n_new, scale_format=tk.SCALE_F16, seed=7300,
+                     outlier_frac=0.01)
+    case.fill()
+    case.sparse = (4, 300, 24)
+    b = tk.Batch().plan(case.pool, case.sessions(True), case.qh).set_sparse(*case.sparse)
+    kk = np.concatenate([k[c:] for k, c in zip(case.k, case.contexts)])
+    vv = np.concatenate([v[c:] for v, c in zip(case.v, case.contexts)])
+    dk, dv = tk.DeviceArray.from_numpy(kk), tk.DeviceArray.from_numpy(vv)
+    dq = tk.DeviceArray.from_numpy(case.q)
+    out = tk.DeviceArray(case.q.shape, np.float32).zero()
+    b.append(case.pool, 0, dk, dv)
+    {"decode": b.decode, "prefill": b.prefill, "mixed": b.attention}[kind](case.pool, 0, dq, out)
+    tk.hip().sync()
+    err = assert_attention_close(out.numpy(), case.oracle_out(), f"sparse head 96 {kind}")
+    say(f"sparse head 96 {kind}: max abs err {err:.2e}")
+    for a in (dk, dv, dq, out):
+        a.close()
+    b.close()
+    case.close()
+
+
 @pytest.mark.parametrize("i", range(12))
 def test_random_sparse_cases(gpu, i):
     """Twelve seeded random static sparse subsets (sink 0-40, window 1-600,

@@ -57,6 +57,14 @@ def test_static_decode_equals_allocating_decode(gpu):
     s2, a2, _ = run_both(small)
     assert np.array_equal(bits(s2), bits(a2)), "static and allocating decode differ (call 2)"
     assert_attention_close(s2, small.oracle_out(), "static decode call 2")
+    # third call: a head size the pool pads (80 dims in 128-dim blocks)
+    say("static decode: third call (head_dim 80)")
+    pad = PagedCase(14, 2, 80, tk.KV_F16, [2500, 33], 2, seed=73)
+    pad.fill()
+    s3, a3, _ = run_both(pad)
+    assert np.array_equal(bits(s3), bits(a3)), "static and allocating decode differ (call 3)"
+    assert_attention_close(s3, pad.oracle_out(), "static decode call 3")
+    pad.close()
     small.close()
     big.close()
 
