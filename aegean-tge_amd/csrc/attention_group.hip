@@ -183,12 +183,15 @@ hipError_t launch_attention_group(int format, int scale_f32, int head_dim, const
   if (format == kF16) {
     if (head_dim == 64) TGE_GRP(kF16, false, 64);
     else if (head_dim == 128) TGE_GRP(kF16, false, 128);
+    else if (head_dim == 256) TGE_GRP(kF16, false, 256);
     else return hipErrorInvalidValue;
   } else if (format == kI8) {
     if (head_dim == 64) {
       if (scale_f32) TGE_GRP(kI8, true, 64); else TGE_GRP(kI8, false, 64);
     } else if (head_dim == 128) {
       if (scale_f32) TGE_GRP(kI8, true, 128); else TGE_GRP(kI8, false, 128);
+    } else if (head_dim == 256) {
+      if (scale_f32) TGE_GRP(kI8, true, 256); else TGE_GRP(kI8, false, 256);
     } else {
       return hipErrorInvalidValue;
     }

@@ -113,7 +113,7 @@ struct Ring {
 // leaving room for a second wave to hide latency.
 template <int FMT, int D, int NRG>
 constexpr int waves_per_eu() {
-  return D == 64 ? (NRG <= 2 ? 3 : 2) : (NRG <= 2 ? 2 : 1);
+  return D == 64 ? (NRG <= 2 ? 3 : 2) : D == 128 ? (NRG <= 2 ? 2 : 1) : 1;
 }
 
 // Issue the direct-to-LDS loads of the page block at `block` into `slot`:
@@ -426,14 +426,20 @@ __device__ __forceinline__ void read_v_pairs(half8_t (&v8)[NP][2], uint32_t la, 
 // no use of them can be scheduled before it.
 template <int NP>
 __device__ __forceinline__ void lds_wait_operands(half8_t (&v)[NP][2]) {
-  static_assert(NP == 2 || NP == 4, "64 or 128 dims");
+  static_assert(NP == 2 || NP == 4 || NP == 8, "64, 128 or 256 dims");
   if constexpr (NP == 2) {
     asm volatile("s_waitcnt lgkmcnt(0)"
                  : "+v"(v[0][0]), "+v"(v[0][1]), "+v"(v[1][0]), "+v"(v[1][1]));
-  } else {
+  } else if constexpr (NP == 4) {
     asm volatile("s_waitcnt lgkmcnt(0)"
                  : "+v"(v[0][0]), "+v"(v[0][1]), "+v"(v[1][0]), "+v"(v[1][1]), "+v"(v[2][0]),
                    "+v"(v[2][1]), "+v"(v[3][0]), "+v"(v[3][1]));
+  } else {
+    asm volatile("s_waitcnt lgkmcnt(0)"
+                 : "+v"(v[0][0]), "+v"(v[0][1]), "+v"(v[1][0]), "+v"(v[1][1]), "+v"(v[2][0]),
+                   "+v"(v[2][1]), "+v"(v[3][0]), "+v"(v[3][1]), "+v"(v[4][0]), "+v"(v[4][1]),
+                   "+v"(v[5][0]), "+v"(v[5][1]), "+v"(v[6][0]), "+v"(v[6][1]), "+v"(v[7][0]),
+                   "+v"(v[7][1]));
   }
 }
 

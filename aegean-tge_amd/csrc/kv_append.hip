@@ -71,8 +71,10 @@ template <int FMT>
 __global__ __launch_bounds__(256) void kv_append_rope_kernel(AppendParams p) {
   const int D = p.dims, half = D >> 1, nb = p.head_dim >> 5;  // pairs of the head's own dims
   const int kv_lanes = 2 * p.kv_heads * nb * 4;
-  const int q_lanes = p.q ? p.q_heads * (half >> 3) : 0;
-  const int per_row = kv_lanes + q_lanes;  // a multiple of 4: blocks stay aligned
+  const int q_used = p.q ? p.q_heads * (half >> 3) : 0;
+  // rounded up to a multiple of 4 so every row starts on a quad and the
+  // int8 blocks' four lanes stay in one aligned quad of the wave
+  const int per_row = kv_lanes + ((q_used + 3) & ~3);
   const long total = (long)p.n_rows * per_row;
   const long idx = (long)blockIdx.x * blockDim.x + threadIdx.x;
   const bool live = idx < total;
@@ -85,8 +87,8 @@ __global__ __launch_bounds__(256) void kv_append_rope_kernel(AppendParams p) {
   const bool fma = p.rope_fma != 0;
 
   if (r >= kv_lanes) {  // Q lane (whole quads of lanes: no block shares a quad with it)
-    if (!live) return;
     const int qi = r - kv_lanes;
+    if (!live || qi >= q_used) return;  // past the grid, or a padding lane of the row
     const int hq = qi / (half >> 3);
     const int j = 8 * (qi % (half >> 3));
     const size_t o = (size_t)row * p.q_heads * D + (size_t)hq * D;
@@ -211,7 +213,8 @@ hipError_t launch_kv_append(int format, const AppendParams& p, hipStream_t strea
 
 hipError_t launch_kv_append_rope(int format, const AppendParams& p, hipStream_t stream) {
   const int nb = p.head_dim >> 5;
-  const long per_row = 2L * p.kv_heads * nb * 4 + (p.q ? (long)p.q_heads * (p.dims >> 4) : 0);
+  const long q_used = p.q ? (long)p.q_heads * (p.dims >> 4) : 0;
+  const long per_row = 2L * p.kv_heads * nb * 4 + ((q_used + 3) & ~3L);
   const long total = (long)p.n_rows * per_row;
   if (total == 0) return hipSuccess;
   const dim3 grid((unsigned)((total + 255) / 256)), block(256);

@@ -104,7 +104,7 @@ struct DecodeCfg {
   // More than 32 rows need a whole SIMD's registers per wave; otherwise the
   // configured shape, or eight waves at two per SIMD when its rings do not
   // fit (f16 pages at head_dim 128).
-  static constexpr bool kBig = NRG > 2;
+  static constexpr bool kBig = NRG > 2 || D > 128;  // (256-dim pages: 16 KB each)
   static constexpr bool kFits = nb_fit(TGE_DECODE_WAVES, WANT) >= 2;
   static constexpr int W = MIX ? 4 : (kBig ? 4 : (kFits ? TGE_DECODE_WAVES : 8));
   static constexpr int WPE = kBig ? 1 : (MIX ? 2 : (kFits ? WANT : 2));
@@ -609,8 +609,9 @@ struct PrefillShared {
   static constexpr int NB = NB_FIT > 4 ? 4 : NB_FIT;
   static_assert(NB >= 2, "the prefill ring needs two tiles");
   // one ring per half; afterwards the second half's states pass through it
-  static constexpr int XO = kWaves * 2 * (D / 16) * 64 * 16;  // accumulators (bytes)
-  static constexpr int XS = kWaves * 2 * 3 * 64 * 4;          // base, sum, empty flag
+  static constexpr int NRG = D > 128 ? 1 : 2;  // row groups of 16 per wave
+  static constexpr int XO = kWaves * NRG * (D / 16) * 64 * 16;  // accumulators (bytes)
+  static constexpr int XS = kWaves * NRG * 3 * 64 * 4;          // base, sum, empty flag
   static_assert(HALVES == 1 || XO + XS <= HALVES * NB * TILE, "state exchange fits the rings");
   alignas(16) char ring[HALVES * NB * TILE];
   int flag;      // arrival broadcast of the in-kernel split merge
@@ -650,8 +651,8 @@ __device__ __forceinline__ void prefill_body(const AttnParams& p,
                                              PrefillShared<FMT, SF32, D, WPE, HALVES>& sh,
                                              const int item) {
   static_assert(HALVES == 1 || !MERGE, "the in-launch merge runs on four-wave workgroups");
-  constexpr int NRG = 2;  // 32 rows per wave
   using SH = PrefillShared<FMT, SF32, D, WPE, HALVES>;
+  constexpr int NRG = SH::NRG;  // 32 rows per wave (16 at 256 dims)
   using U = Unit<FMT, SF32, D, NRG>;
   using Regs = typename U::Regs;
   using RG = Ring<FMT, SF32, D>;
@@ -667,7 +668,7 @@ __device__ __forceinline__ void prefill_body(const AttnParams& p,
   const int col = lane & 15;
   const int grp = lane >> 4;
   const int q_stride = p.q_heads * p.dims;
-  const int row0 = wave * 32;
+  const int row0 = wave * 16 * NRG;
   const bool has_rows = row0 < w.rows;
 
   // This half's pages: the first half takes whole tiles of four.
@@ -1017,20 +1018,30 @@ __global__ __launch_bounds__(256) void split_reduce_kernel(ReduceParams p) {
 
 }  // namespace
 
+// Row groups a decode unit may hold at a block width (max_unit_rows / 16).
+template <int D>
+constexpr int max_row_groups() {
+  return max_unit_rows(D) / 16;
+}
+
 template <int FMT, bool SF32, int D>
 hipError_t launch_decode_d(int row_groups, int n_groups, const AttnParams& p, hipStream_t stream) {
   switch (row_groups) {
 #define TGE_DEC(n)                                                                          \
   case n: {                                                                                 \
-    using C = DecodeCfg<FMT, SF32, D, n, false>;                                            \
-    using CS = DecodeCfg<FMT, SF32, D, n, true>;                                            \
-    if (p.sp_stride > 0)                                                                    \
-      hipLaunchKernelGGL((paged_decode_kernel<FMT, SF32, D, n, CS::W, CS::WPE, true>),      \
-                         dim3((unsigned)n_groups), dim3(64 * CS::W), 0, stream, p);         \
-    else                                                                                    \
-      hipLaunchKernelGGL((paged_decode_kernel<FMT, SF32, D, n, C::W, C::WPE, false>),       \
-                         dim3((unsigned)n_groups), dim3(64 * C::W), 0, stream, p);          \
-    break;                                                                                  \
+    if constexpr (n <= max_row_groups<D>()) {                                               \
+      using C = DecodeCfg<FMT, SF32, D, n, false>;                                          \
+      using CS = DecodeCfg<FMT, SF32, D, n, true>;                                          \
+      if (p.sp_stride > 0)                                                                  \
+        hipLaunchKernelGGL((paged_decode_kernel<FMT, SF32, D, n, CS::W, CS::WPE, true>),    \
+                           dim3((unsigned)n_groups), dim3(64 * CS::W), 0, stream, p);       \
+      else                                                                                  \
+        hipLaunchKernelGGL((paged_decode_kernel<FMT, SF32, D, n, C::W, C::WPE, false>),     \
+                           dim3((unsigned)n_groups), dim3(64 * C::W), 0, stream, p);        \
+      break;                                                                                \
+    } else {                                                                                \
+      return hipErrorInvalidValue;                                                          \
+    }                                                                                       \
   }
     TGE_DEC(1)
     TGE_DEC(2)
@@ -1050,14 +1061,16 @@ int decode_blocks_d(int row_groups, bool sparse) {
   switch (row_groups) {
 #define TGE_DOCC(r)                                                                        \
   case r: {                                                                                \
-    using C = DecodeCfg<FMT, SF32, D, r, false>;                                           \
-    using CS = DecodeCfg<FMT, SF32, D, r, true>;                                           \
-    e = sparse ? hipOccupancyMaxActiveBlocksPerMultiprocessor(                             \
-                     &n, paged_decode_kernel<FMT, SF32, D, r, CS::W, CS::WPE, true>,       \
-                     64 * CS::W, 0)                                                        \
-               : hipOccupancyMaxActiveBlocksPerMultiprocessor(                             \
-                     &n, paged_decode_kernel<FMT, SF32, D, r, C::W, C::WPE, false>,        \
-                     64 * C::W, 0);                                                        \
+    if constexpr (r <= max_row_groups<D>()) {                                              \
+      using C = DecodeCfg<FMT, SF32, D, r, false>;                                         \
+      using CS = DecodeCfg<FMT, SF32, D, r, true>;                                         \
+      e = sparse ? hipOccupancyMaxActiveBlocksPerMultiprocessor(                           \
+                       &n, paged_decode_kernel<FMT, SF32, D, r, CS::W, CS::WPE, true>,     \
+                       64 * CS::W, 0)                                                      \
+                 : hipOccupancyMaxActiveBlocksPerMultiprocessor(                           \
+                       &n, paged_decode_kernel<FMT, SF32, D, r, C::W, C::WPE, false>,      \
+                       64 * C::W, 0);                                                      \
+    }                                                                                      \
     break;                                                                                 \
   }
     TGE_DOCC(1)
@@ -1071,34 +1084,39 @@ int decode_blocks_d(int row_groups, bool sparse) {
   return e == hipSuccess ? n : 0;
 }
 
+// Calls f.template operator()<FMT, SF32, D>() for a pool's format, scale
+// format and block width (64, 128 or 256); `bad` for any other.
+template <class R, class F>
+R with_variant(int format, int scale_f32, int head_dim, R bad, F&& f) {
+  if (format == kF16) {
+    if (head_dim == 64) return f.template operator()<kF16, false, 64>();
+    if (head_dim == 128) return f.template operator()<kF16, false, 128>();
+    if (head_dim == 256) return f.template operator()<kF16, false, 256>();
+  } else if (format == kI8) {
+    if (head_dim == 64)
+      return scale_f32 ? f.template operator()<kI8, true, 64>() : f.template operator()<kI8, false, 64>();
+    if (head_dim == 128)
+      return scale_f32 ? f.template operator()<kI8, true, 128>() : f.template operator()<kI8, false, 128>();
+    if (head_dim == 256)
+      return scale_f32 ? f.template operator()<kI8, true, 256>() : f.template operator()<kI8, false, 256>();
+  }
+  return bad;
+}
+
 hipError_t launch_decode(int format, int scale_f32, int head_dim, int row_groups, int n_groups,
                          const AttnParams& p, hipStream_t stream) {
   if (n_groups <= 0) return hipSuccess;
   if (!p.wg_first) return hipErrorInvalidValue;
-  if (format == kF16) {
-    if (head_dim == 64) return launch_decode_d<kF16, false, 64>(row_groups, n_groups, p, stream);
-    if (head_dim == 128) return launch_decode_d<kF16, false, 128>(row_groups, n_groups, p, stream);
-  } else if (format == kI8) {
-    if (head_dim == 64)
-      return scale_f32 ? launch_decode_d<kI8, true, 64>(row_groups, n_groups, p, stream)
-                       : launch_decode_d<kI8, false, 64>(row_groups, n_groups, p, stream);
-    if (head_dim == 128)
-      return scale_f32 ? launch_decode_d<kI8, true, 128>(row_groups, n_groups, p, stream)
-                       : launch_decode_d<kI8, false, 128>(row_groups, n_groups, p, stream);
-  }
-  return hipErrorInvalidValue;
+  return with_variant(format, scale_f32, head_dim, hipErrorInvalidValue,
+                      [&]<int FMT, bool SF32, int D>() {
+                        return launch_decode_d<FMT, SF32, D>(row_groups, n_groups, p, stream);
+                      });
 }
 
 int decode_blocks_per_cu(int format, int scale_f32, int head_dim, int row_groups, bool sparse) {
-  if (format == kF16) {
-    return head_dim == 64 ? decode_blocks_d<kF16, false, 64>(row_groups, sparse)
-                          : decode_blocks_d<kF16, false, 128>(row_groups, sparse);
-  }
-  if (head_dim == 64)
-    return scale_f32 ? decode_blocks_d<kI8, true, 64>(row_groups, sparse)
-                     : decode_blocks_d<kI8, false, 64>(row_groups, sparse);
-  return scale_f32 ? decode_blocks_d<kI8, true, 128>(row_groups, sparse)
-                   : decode_blocks_d<kI8, false, 128>(row_groups, sparse);
+  return with_variant(format, scale_f32, head_dim, 0, [&]<int FMT, bool SF32, int D>() {
+    return decode_blocks_d<FMT, SF32, D>(row_groups, sparse);
+  });
 }
 
 template <int FMT, int D>
@@ -1129,10 +1147,20 @@ hipError_t launch_mixed_d(int row_groups, int n_dec, int n_pf, const AttnParams&
                           const AttnParams& pf, hipStream_t stream) {
   const dim3 grid((unsigned)(n_dec + n_pf)), block(256);
   switch (row_groups) {
-    case 1: hipLaunchKernelGGL((paged_mixed_kernel<FMT, SF32, D, 1>), grid, block, 0, stream, dec, pf, n_dec); break;
-    case 2: hipLaunchKernelGGL((paged_mixed_kernel<FMT, SF32, D, 2>), grid, block, 0, stream, dec, pf, n_dec); break;
-    case 3: hipLaunchKernelGGL((paged_mixed_kernel<FMT, SF32, D, 3>), grid, block, 0, stream, dec, pf, n_dec); break;
-    case 4: hipLaunchKernelGGL((paged_mixed_kernel<FMT, SF32, D, 4>), grid, block, 0, stream, dec, pf, n_dec); break;
+#define TGE_MIX(n)                                                                                \
+  case n:                                                                                         \
+    if constexpr (n <= max_row_groups<D>()) {                                                     \
+      hipLaunchKernelGGL((paged_mixed_kernel<FMT, SF32, D, n>), grid, block, 0, stream, dec, pf,  \
+                         n_dec);                                                                  \
+      break;                                                                                      \
+    } else {                                                                                      \
+      return hipErrorInvalidValue;                                                                \
+    }
+    TGE_MIX(1)
+    TGE_MIX(2)
+    TGE_MIX(3)
+    TGE_MIX(4)
+#undef TGE_MIX
     default: return hipErrorInvalidValue;
   }
   return hipGetLastError();
@@ -1142,18 +1170,10 @@ hipError_t launch_mixed(int format, int scale_f32, int head_dim, int row_groups,
                         int n_pf, const AttnParams& dec, const AttnParams& pf, hipStream_t stream) {
   if (n_dec + n_pf <= 0) return hipSuccess;
   if (!dec.wg_first || !dec.counters || !pf.counters) return hipErrorInvalidValue;
-  if (format == kF16) {
-    if (head_dim == 64) return launch_mixed_d<kF16, false, 64>(row_groups, n_dec, n_pf, dec, pf, stream);
-    if (head_dim == 128) return launch_mixed_d<kF16, false, 128>(row_groups, n_dec, n_pf, dec, pf, stream);
-  } else if (format == kI8) {
-    if (head_dim == 64)
-      return scale_f32 ? launch_mixed_d<kI8, true, 64>(row_groups, n_dec, n_pf, dec, pf, stream)
-                       : launch_mixed_d<kI8, false, 64>(row_groups, n_dec, n_pf, dec, pf, stream);
-    if (head_dim == 128)
-      return scale_f32 ? launch_mixed_d<kI8, true, 128>(row_groups, n_dec, n_pf, dec, pf, stream)
-                       : launch_mixed_d<kI8, false, 128>(row_groups, n_dec, n_pf, dec, pf, stream);
-  }
-  return hipErrorInvalidValue;
+  return with_variant(format, scale_f32, head_dim, hipErrorInvalidValue,
+                      [&]<int FMT, bool SF32, int D>() {
+                        return launch_mixed_d<FMT, SF32, D>(row_groups, n_dec, n_pf, dec, pf, stream);
+                      });
 }
 
 template <int FMT, bool SF32, int D>
@@ -1161,61 +1181,59 @@ int mixed_blocks_d(int row_groups) {
   int n = 0;
   hipError_t e = hipErrorInvalidValue;
   switch (row_groups) {
-    case 1: e = hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, paged_mixed_kernel<FMT, SF32, D, 1>, 256, 0); break;
-    case 2: e = hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, paged_mixed_kernel<FMT, SF32, D, 2>, 256, 0); break;
-    case 3: e = hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, paged_mixed_kernel<FMT, SF32, D, 3>, 256, 0); break;
-    case 4: e = hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, paged_mixed_kernel<FMT, SF32, D, 4>, 256, 0); break;
+#define TGE_MOCC(r)                                                                                    \
+  case r:                                                                                              \
+    if constexpr (r <= max_row_groups<D>())                                                            \
+      e = hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, paged_mixed_kernel<FMT, SF32, D, r>, 256, 0); \
+    break;
+    TGE_MOCC(1)
+    TGE_MOCC(2)
+    TGE_MOCC(3)
+    TGE_MOCC(4)
+#undef TGE_MOCC
     default: break;
   }
   return e == hipSuccess ? n : 0;
 }
 
 int mixed_blocks_per_cu(int format, int scale_f32, int head_dim, int row_groups) {
-  if (format == kF16) {
-    return head_dim == 64 ? mixed_blocks_d<kF16, false, 64>(row_groups)
-                          : mixed_blocks_d<kF16, false, 128>(row_groups);
-  }
-  if (head_dim == 64)
-    return scale_f32 ? mixed_blocks_d<kI8, true, 64>(row_groups) : mixed_blocks_d<kI8, false, 64>(row_groups);
-  return scale_f32 ? mixed_blocks_d<kI8, true, 128>(row_groups) : mixed_blocks_d<kI8, false, 128>(row_groups);
+  return with_variant(format, scale_f32, head_dim, 0, [&]<int FMT, bool SF32, int D>() {
+    return mixed_blocks_d<FMT, SF32, D>(row_groups);
+  });
 }
 
 int prefill_halves(int format, int head_dim) {
-  if (format == kF16) return head_dim == 64 ? halves_for_wpe<prefill_wpe<kF16, 64>()>()
-                                            : halves_for_wpe<prefill_wpe<kF16, 128>()>();
-  return head_dim == 64 ? halves_for_wpe<prefill_wpe<kI8, 64>()>()
-                        : halves_for_wpe<prefill_wpe<kI8, 128>()>();
+  return with_variant(format, 0, head_dim, 1, [&]<int FMT, bool SF32, int D>() {
+    return halves_for_wpe<prefill_wpe<FMT, D>()>();
+  });
 }
 
 hipError_t launch_prefill(int format, int scale_f32, int head_dim, int n_units,
                           const AttnParams& p, hipStream_t stream) {
   if (n_units <= 0) return hipSuccess;
-  if (format == kF16) {
-    if (head_dim == 64) return launch_prefill_d<kF16, false, 64>(n_units, p, stream);
-    if (head_dim == 128) return launch_prefill_d<kF16, false, 128>(n_units, p, stream);
-  } else if (format == kI8) {
-    if (head_dim == 64)
-      return scale_f32 ? launch_prefill_d<kI8, true, 64>(n_units, p, stream)
-                       : launch_prefill_d<kI8, false, 64>(n_units, p, stream);
-    if (head_dim == 128)
-      return scale_f32 ? launch_prefill_d<kI8, true, 128>(n_units, p, stream)
-                       : launch_prefill_d<kI8, false, 128>(n_units, p, stream);
-  }
-  return hipErrorInvalidValue;
+  return with_variant(format, scale_f32, head_dim, hipErrorInvalidValue,
+                      [&]<int FMT, bool SF32, int D>() {
+                        return launch_prefill_d<FMT, SF32, D>(n_units, p, stream);
+                      });
 }
 
 template <int D>
 hipError_t launch_reduce_d(int n_items, int max_parts, const ReduceParams& p, hipStream_t stream) {
-  // Slots per row: one per batch of 8 splits (one round of loads), at most 8.
+  // Slots per row: one per batch of 8 splits (one round of loads), at most 8
+  // (4 at 256 dims: a row's 64 (4-dim) lanes times the slots fill the 256
+  // threads).
+  constexpr int kMaxSlots = D > 128 ? 4 : 8;
   const int want = (max_parts + 7) / 8;
-  const int slots = want <= 1 ? 1 : (want <= 2 ? 2 : (want <= 4 ? 4 : 8));
+  const int slots = want <= 1 ? 1 : (want <= 2 ? 2 : (want <= 4 || kMaxSlots == 4 ? 4 : 8));
   const int rpb = 256 / (D / 4 * slots);
   const dim3 grid((unsigned)n_items, (unsigned)((p.rows_cap + rpb - 1) / rpb)), block(256);
   switch (slots) {
     case 1: hipLaunchKernelGGL((split_reduce_kernel<D, 1>), grid, block, 0, stream, p); break;
     case 2: hipLaunchKernelGGL((split_reduce_kernel<D, 2>), grid, block, 0, stream, p); break;
     case 4: hipLaunchKernelGGL((split_reduce_kernel<D, 4>), grid, block, 0, stream, p); break;
-    default: hipLaunchKernelGGL((split_reduce_kernel<D, 8>), grid, block, 0, stream, p); break;
+    default:
+      if constexpr (kMaxSlots == 8) hipLaunchKernelGGL((split_reduce_kernel<D, 8>), grid, block, 0, stream, p);
+      break;
   }
   return hipGetLastError();
 }
@@ -1225,6 +1243,7 @@ hipError_t launch_reduce(int head_dim, int n_items, int max_parts, const ReduceP
   if (n_items == 0) return hipSuccess;
   if (head_dim == 64) return launch_reduce_d<64>(n_items, max_parts, p, stream);
   if (head_dim == 128) return launch_reduce_d<128>(n_items, max_parts, p, stream);
+  if (head_dim == 256) return launch_reduce_d<256>(n_items, max_parts, p, stream);
   return hipErrorInvalidValue;
 }
 

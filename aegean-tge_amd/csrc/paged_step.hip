@@ -520,7 +520,12 @@ hipError_t launch_step_d(int row_groups, int n, const StepParams& p, hipStream_t
   constexpr bool I8 = FMT == kI8;
   switch (row_groups) {
     case 1: hipLaunchKernelGGL((paged_step_kernel<FMT, SF32, D, 1>), grid, block, 0, st, p); break;
-    case 2: hipLaunchKernelGGL((paged_step_kernel<FMT, SF32, D, 2>), grid, block, 0, st, p); break;
+    case 2:
+      if constexpr (step_fits(I8, SF32, D, 32)) {
+        hipLaunchKernelGGL((paged_step_kernel<FMT, SF32, D, 2>), grid, block, 0, st, p);
+        break;
+      }
+      return hipErrorInvalidValue;
     case 3:
       if constexpr (step_fits(I8, SF32, D, 48)) {
         hipLaunchKernelGGL((paged_step_kernel<FMT, SF32, D, 3>), grid, block, 0, st, p);
@@ -544,6 +549,7 @@ hipError_t launch_step(int format, int scale_f32, int head_dim, int row_groups, 
   if (format == kF16) {
     if (head_dim == 64) return launch_step_d<kF16, false, 64>(row_groups, n_recs, p, stream);
     if (head_dim == 128) return launch_step_d<kF16, false, 128>(row_groups, n_recs, p, stream);
+    if (head_dim == 256) return launch_step_d<kF16, false, 256>(row_groups, n_recs, p, stream);
   } else if (format == kI8) {
     if (head_dim == 64)
       return scale_f32 ? launch_step_d<kI8, true, 64>(row_groups, n_recs, p, stream)
@@ -551,6 +557,9 @@ hipError_t launch_step(int format, int scale_f32, int head_dim, int row_groups, 
     if (head_dim == 128)
       return scale_f32 ? launch_step_d<kI8, true, 128>(row_groups, n_recs, p, stream)
                        : launch_step_d<kI8, false, 128>(row_groups, n_recs, p, stream);
+    if (head_dim == 256)
+      return scale_f32 ? launch_step_d<kI8, true, 256>(row_groups, n_recs, p, stream)
+                       : launch_step_d<kI8, false, 256>(row_groups, n_recs, p, stream);
   }
   return hipErrorInvalidValue;
 }

@@ -244,8 +244,8 @@ int tge_kv_pool_create(const tge_kv_pool_desc* desc, tge_kv_pool** out) {
     return fail(TGE_ERR_INVALID, "kv_pool_create: unknown format");
   if (tge::block_dims_for(d.head_dim, d.format) == 0)
     return fail(TGE_ERR_INVALID, d.format == TGE_KV_I8
-                                     ? "kv_pool_create: int8 head_dim must be 32, 64, 96 or 128"
-                                     : "kv_pool_create: head_dim must be a multiple of 16 up to 128");
+                                     ? "kv_pool_create: int8 head_dim must be a multiple of 32 up to 256"
+                                     : "kv_pool_create: head_dim must be a multiple of 16 up to 256");
   if (d.format == TGE_KV_I8 && d.scale_format != TGE_SCALE_F16 &&
       d.scale_format != TGE_SCALE_F32)
     return fail(TGE_ERR_INVALID, "kv_pool_create: unknown scale format");
@@ -478,7 +478,7 @@ int tge_batch_plan(tge_batch* b, const tge_kv_pool* pool, const tge_batch_desc* 
   b->off_rows = o_rows;
   // Decode lists are built eagerly when the rows fit a decode unit (the
   // common case: one upload per step serves every layer).
-  if (st.max_rows <= tge::kMaxRows) {
+  if (st.max_rows <= tge::max_unit_rows(st.block_dims)) {
     s = build_decode_plan(b, pool, b->decode, 0, hs);
     if (s != TGE_OK) return s;
   }
@@ -730,7 +730,7 @@ int tge_decode_attention(const tge_batch* b, const tge_kv_pool* p, int layer,
   if (s != TGE_OK) return s;
   if (!q || !out) return fail(TGE_ERR_INVALID, "decode_attention: null q/out");
   if (!b->decode.built)
-    return fail(TGE_ERR_INVALID, "decode_attention: n_new * group exceeds 64 rows");
+    return fail(TGE_ERR_INVALID, "decode_attention: n_new * group exceeds a decode unit (64 rows, 48 at head_dim > 128)");
   if (b->decode.sparse != (b->sp_stride > 0)) {
     // the sparse setting changed after planning: rebalance for its kernel
     s = build_decode_plan(const_cast<tge_batch*>(b), p, const_cast<tge_batch*>(b)->decode, 0,
@@ -746,7 +746,7 @@ int tge_decode_step(const tge_batch* b, tge_kv_pool* p, int layer, const float* 
   if (s != TGE_OK) return s;
   if (!q || !k || !v || !out) return fail(TGE_ERR_INVALID, "decode_step: null q/k/v/out");
   if (!b->decode.built)
-    return fail(TGE_ERR_INVALID, "decode_step: n_new * group exceeds 64 rows");
+    return fail(TGE_ERR_INVALID, "decode_step: n_new * group exceeds a decode unit (64 rows, 48 at head_dim > 128)");
   if (!b->small.built || b->sp_stride > 0) {
     // a large step (or a static sparse one): the append, then the decode
     // kernel and its split merge
@@ -929,8 +929,8 @@ int tge_decode_attention_static(const tge_batch_desc* d, const tge_kv_pool* p, i
   s = tge::plan::build_step(step, d->n_sessions, d->ctx, d->n_new, d->table_offsets, d->page_ids,
                             d->q_heads, p->desc.kv_heads, hd, p->desc.pages, &msg);
   if (s != TGE_OK) return fail(s, std::string(msg ? msg : "invalid description"));
-  if (step.max_rows > tge::kMaxRows)
-    return fail(TGE_ERR_INVALID, "decode_attention_static: n_new * group exceeds 64 rows");
+  if (step.max_rows > tge::max_unit_rows(step.block_dims))
+    return fail(TGE_ERR_INVALID, "decode_attention_static: n_new * group exceeds a decode unit (64 rows, 48 at head_dim > 128)");
   const int f = p->desc.format, sf32 = p->desc.scale_format == TGE_SCALE_F32;
   const int rg = std::max(1, std::min(4, (step.max_rows + 15) / 16));
   const int bd = p->bd;

@@ -28,13 +28,14 @@ struct BlockGeom {
 };
 
 // Width of the page blocks for a head size: heads of up to 64 dims are
-// stored in 64-dim blocks, up to 128 in 128-dim blocks, the dims from
-// head_dim on holding zeros (so scores and values are those of the head's
-// own dims). A head size must be a positive multiple of 16 (int8: of 32,
-// the quantizer's block) of at most 128; 0 for any other.
+// stored in 64-dim blocks, up to 128 in 128-dim blocks, up to 256 in
+// 256-dim blocks, the dims from head_dim on holding zeros (so scores and
+// values are those of the head's own dims). A head size must be a positive
+// multiple of 16 (int8: of 32, the quantizer's block) of at most 256; 0 for
+// any other.
 __host__ __device__ inline int block_dims_for(int head_dim, int format) {
-  if (head_dim <= 0 || head_dim > 128 || head_dim % (format == kI8 ? 32 : 16) != 0) return 0;
-  return head_dim <= 64 ? 64 : 128;
+  if (head_dim <= 0 || head_dim > 256 || head_dim % (format == kI8 ? 32 : 16) != 0) return 0;
+  return head_dim <= 64 ? 64 : head_dim <= 128 ? 128 : 256;
 }
 
 __host__ __device__ inline BlockGeom block_geom(int format, int head_dim, int scale_f32) {

@@ -10,7 +10,14 @@ namespace tge {
 constexpr int kPageTokens = 16;   // block_table.hpp:19 kBlockTokens
 constexpr int kWaves = 4;         // waves per block-prefill workgroup
 constexpr int kMaxRows = 64;      // query rows (n_new * group) per decode unit
+// Query rows of one decode unit at a block width: 64, or 48 in 256-dim
+// blocks (three row groups: their Q^T table and two 16 KB ring slots per
+// wave fill the CU's LDS).
+constexpr int max_unit_rows(int block_dims) { return block_dims > 128 ? 48 : kMaxRows; }
 constexpr int kPrefillRows = 128; // rows of one block-prefill work item (4 waves x 32)
+// Rows of a block-prefill tile at a block width: 4 waves x 32 rows, or x 16
+// rows in 256-dim blocks (a wave's accumulators for 32 rows would not fit).
+constexpr int prefill_tile_rows(int block_dims) { return block_dims > 128 ? 64 : kPrefillRows; }
 
 struct SessionRec {
   int ctx;        // positions cached before this step
@@ -90,12 +97,12 @@ constexpr int step_batch_pages(bool i8, bool scale_f32, int head_dim, int row_gr
   const int np = head_dim / 32;
   const int kw = i8 ? 2 * np : 4 * np;
   const int sw = i8 ? (scale_f32 ? 4 * np : 2 * np) : 0;
-  return row_groups >= 3 ? 1 : (2 * kw + 2 * sw <= 16 ? 4 : 2);
+  return row_groups >= 3 || head_dim > 128 ? 1 : (2 * kw + 2 * sw <= 16 ? 4 : 2);
 }
 
 // Steps the one-kernel step takes: rows per unit that fit its registers.
 constexpr bool step_fits(bool i8, bool scale_f32, int head_dim, int rows) {
-  return rows <= kMaxRows && (head_dim <= 64 || rows <= (i8 && scale_f32 ? 32 : 48));
+  return rows <= kMaxRows && (head_dim <= 64 || rows <= (head_dim > 128 ? 16 : (i8 && scale_f32 ? 32 : 48)));
 }
 
 struct RowRec {  // one new token: destination page and slot, logical position

@@ -97,8 +97,8 @@ int build_step(Step& step, int ns, const int* ctx, const int* n_new, const int* 
   if (q_heads <= 0 || kv_heads <= 0 || q_heads % kv_heads != 0)
     return bad("batch_plan: q_heads must be a multiple of kv_heads");
   const int group = q_heads / kv_heads;
-  if (group > kPrefillRows)
-    return bad("batch_plan: more than 128 query heads per KV head");
+  if (group > prefill_tile_rows(head_dim <= 128 ? 128 : 256))
+    return bad("batch_plan: more than 128 query heads per KV head (64 at head_dim > 128)");
   if (table_offsets[0] != 0) return bad("batch_plan: table_offsets[0] must be 0");
   const int n_entries = table_offsets[ns];
   if (n_entries < 0) return bad("batch_plan: negative table size");
@@ -135,7 +135,7 @@ int build_step(Step& step, int ns, const int* ctx, const int* n_new, const int* 
   }
   step.kv_heads = kv_heads;
   step.head_dim = head_dim;
-  step.block_dims = head_dim <= 64 ? 64 : 128;
+  step.block_dims = head_dim <= 64 ? 64 : head_dim <= 128 ? 128 : 256;
   step.q_heads = q_heads;
   step.group = group;
   step.pages = pool_pages;
@@ -143,7 +143,9 @@ int build_step(Step& step, int ns, const int* ctx, const int* n_new, const int* 
   return TGE_OK;
 }
 
-bool decode_session(const Step& s, const SessionRec& r) { return r.n_new * s.group <= kMaxRows; }
+bool decode_session(const Step& s, const SessionRec& r) {
+  return r.n_new * s.group <= max_unit_rows(s.block_dims);
+}
 
 bool take_session(const Step& s, const SessionRec& r, int only) {
   return only == 0 || (only == 1) == decode_session(s, r);
@@ -343,7 +345,7 @@ void build_prefill(const Step& b, int cus, AttnLists& pl, int only, int halves) 
   pl.groups = 0;
   pl.parts = pl.max_splits = 0;
   pl.row_groups = kPrefillRows / 16;
-  const int tq = std::max(1, kPrefillRows / b.group);
+  const int tq = std::max(1, prefill_tile_rows(b.block_dims) / b.group);
   // Page-split size: enough items for about two rounds of two four-wave
   // workgroups on each compute unit (of one eight-wave workgroup with two
   // halves), at least 32 pages (eight tiles of four) per half.
@@ -392,7 +394,7 @@ constexpr int kStepUnsplitBatches = 3;
 
 bool build_step_lists(const Step& b, bool i8, bool scale_f32, StepLists& out) {
   out = StepLists{};
-  if (b.max_rows > kMaxRows || b.sessions.empty()) return false;
+  if (b.max_rows > max_unit_rows(b.block_dims) || b.sessions.empty()) return false;
   long blocks = 0;
   int max_pages = 0;
   for (const auto& sr : b.sessions) {

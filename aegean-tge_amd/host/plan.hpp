@@ -67,7 +67,7 @@ struct Step {
   std::vector<RowRec> rows;
   int kv_heads = 0;
   int head_dim = 0;
-  int block_dims = 0;  // width of the page blocks: 64 (head_dim <= 64) or 128
+  int block_dims = 0;  // width of the page blocks: 64, 128 or 256 (block_dims_for)
   int q_heads = 0;
   int group = 1;
   int pages = 0;     // pages of the pool

@@ -78,9 +78,9 @@ const char* tge_backend_arch(void);
 /* ---------------------------------------------------------------------------
  * Page pool. Device memory for `layers` x `pages` x `kv_heads` page blocks.
  * Each page block holds TGE_PAGE_TOKENS tokens of one KV head at the block
- * width W = 64 (head_dim <= 64) or 128 (head_dim <= 128), dims from head_dim
- * on stored as zeros, its parts back to back (one contiguous run of memory
- * per block):
+ * width W = 64 (head_dim <= 64), 128 (head_dim <= 128) or 256 (head_dim <=
+ * 256), dims from head_dim on stored as zeros, its parts back to back (one
+ * contiguous run of memory per block):
  *   K part, then V part: 16 * W elements each (f16 bits or int8 codes)
  *   I8 only, K scales, then V scales: 16 * W/32 scales each (f16 bits or
  *   fp32)
@@ -88,10 +88,10 @@ const char* tge_backend_arch(void);
  * Element (token t, dim d) of a block's part sits at:
  *   K: tge_kv_k_index(t, d, W)      V: tge_kv_v_index(t, d, W)
  *   scale of (t, block b = d/32): tge_kv_scale_index(t, b, W)
- * head_dim: a multiple of 16 up to 128 (F16) or of 32 up to 128 (I8, whose
+ * head_dim: a multiple of 16 up to 256 (F16) or of 32 up to 256 (I8, whose
  * scales cover 32-dim blocks). The reference takes any head_dim > 0
- * (attention_scalar.cpp:11-14; int8 % 32, qwen2.cpp:406-409); wider heads
- * (e.g. 256) are not supported here. q, k, v and out rows always have the
+ * (attention_scalar.cpp:11-14; int8 % 32, qwen2.cpp:406-409); heads wider
+ * than 256 are not supported here. q, k, v and out rows always have the
  * model's head_dim.
  * ------------------------------------------------------------------------ */
 typedef struct tge_kv_pool tge_kv_pool;
@@ -115,7 +115,7 @@ typedef struct {
   size_t kv_block_bytes;    /* bytes of one K (or V) part */
   size_t scale_block_bytes; /* bytes of one scale part (0 for F16) */
   size_t block_bytes;       /* bytes of a whole page block: the block stride */
-  int block_dims;           /* the block width W (64 or 128) */
+  int block_dims;           /* the block width W (64, 128 or 256) */
 } tge_kv_layer_view;
 
 int tge_kv_pool_create(const tge_kv_pool_desc* desc, tge_kv_pool** out);
@@ -132,7 +132,7 @@ int tge_kv_copy_page(tge_kv_pool* pool, int src_page, int dst_page, void* stream
 
 /* In-page element index of (token, dim) for K and V blocks, and of the
  * scale of (token, 32-dim block), for blocks of width W (the third
- * argument, 64 or 128; the pool's tge_kv_layer_view.block_dims). With
+ * argument, 64, 128 or 256; the pool's tge_kv_layer_view.block_dims). With
  * NP = W/32:
  *   K:     ((((d/4)&3)*16 + t)*NP + d/32)*8 + ((d/16)&1)*4 + (d&3)
  *   V:     ((t/4*16 + (d&15))*NP + d/32)*8 + ((d/16)&1)*4 + (t&3)
@@ -164,7 +164,8 @@ typedef struct {
   const int* table_offsets; /* host [n_sessions+1] */
   const int* page_ids;      /* host [table_offsets[n_sessions]] */
   int q_heads;              /* multiple of the pool's kv_heads, at most 128
-                               query heads per KV head */
+                               query heads per KV head (64 at head_dim
+                               > 128) */
 } tge_batch_desc;
 
 int tge_batch_create(tge_batch** out);
@@ -282,8 +283,8 @@ int tge_decode_attention_static(const tge_batch_desc* desc, const tge_kv_pool* p
  * prior page and the chunk itself, on f16 MFMA (Q rounded to f16 as in
  * decode; I8 pools run the same kernel where the reference takes its
  * per-token i8 path, qwen2.cpp:1535-1538). Tiles of up to 128
- * (query, head) rows of one KV head's query group; long prefixes are split
- * and merged like decode.
+ * (query, head) rows of one KV head's query group (64 at head_dim > 128);
+ * long prefixes are split and merged like decode.
  */
 int tge_prefill_attention(const tge_batch* batch, const tge_kv_pool* pool,
                           int layer, const float* q, float* out, void* stream);

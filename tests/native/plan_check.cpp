@@ -288,7 +288,7 @@ void random_plans(int cases) {
     const Residency res{cus * (1 + (int)(rng() % 2)), cus};
     for (int only = 0; only < 3; ++only) {
       AttnLists dec, pf;
-      if (only != 2 && st.max_rows <= kMaxRows) {
+      if (only != 2 && st.max_rows <= max_unit_rows(st.block_dims)) {
         build_decode(st, res, dec, only);
         check_lists(st, dec, only, false);
         REQUIRE(dec.groups <= res.groups, "more workgroups than resident");

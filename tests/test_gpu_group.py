@@ -57,6 +57,8 @@ CASES = {
     # head sizes the pool pads to the block width
     "f16_d80_g7": (14, 2, 80, tk.KV_F16, 0, 500, [(0, 500), (33, 100)]),
     "i8_d96_g4_f32scales": (16, 4, 96, tk.KV_I8, tk.SCALE_F32, 400, [(0, 400), (7, 64)]),
+    "f16_d256_g8": (16, 2, 256, tk.KV_F16, 0, 300, [(0, 300), (40, 90)]),
+    "i8_d256_g4": (8, 2, 256, tk.KV_I8, tk.SCALE_F16, 300, [(0, 300), (5, 70)]),
 }
 
 

@@ -28,7 +28,7 @@ def raw_pool_rows(case, layer, s, count):
     view = case.pool.layer(layer)
     pages = case.pool.pages
     W = view.block_dims
-    assert W == (64 if case.hd <= 64 else 128)
+    assert W == (64 if case.hd <= 64 else 128 if case.hd <= 128 else 256)
     elem = np.uint16 if case.fmt == tk.KV_F16 else np.int8
     esz = np.dtype(elem).itemsize
     bb = view.block_bytes
@@ -454,6 +454,11 @@ def test_prefill_i8_matches_oracle(gpu):
     (tk.KV_F16, tk.SCALE_F16, 2, 80, True),
     (tk.KV_I8, tk.SCALE_F16, 2, 96, False),
     (tk.KV_F16, tk.SCALE_F16, 1, 48, False),
+    # 7 q heads x 6 lanes: Q lanes that end a row off a 4-lane boundary
+    (tk.KV_I8, tk.SCALE_F16, 1, 96, True),
+    # 256-dim blocks
+    (tk.KV_F16, tk.SCALE_F16, 2, 256, True),
+    (tk.KV_I8, tk.SCALE_F32, 1, 160, False),
 ])
 def test_append_rope_bitexact(gpu, fmt, sf, kvh, hd, fma):
     """Fused bias + RoPE + append (tge_kv_append_rope): the pool contents and
@@ -713,6 +718,11 @@ HEAD_SIZES = {
     "f16_d16": (4, 2, 16, tk.KV_F16, 0),
     "i8_d96_f16scales": (12, 2, 96, tk.KV_I8, tk.SCALE_F16),
     "i8_d32_f32scales": (8, 4, 32, tk.KV_I8, tk.SCALE_F32),
+    # 256-dim blocks (one wave per SIMD in decode and prefill)
+    "f16_d256_g8": (16, 2, 256, tk.KV_F16, 0),
+    "f16_d192_g4": (8, 2, 192, tk.KV_F16, 0),
+    "i8_d256_f16scales": (8, 2, 256, tk.KV_I8, tk.SCALE_F16),
+    "i8_d160_f32scales_g8": (8, 1, 160, tk.KV_I8, tk.SCALE_F32),
 }
 
 
@@ -720,7 +730,7 @@ HEAD_SIZES = {
 @pytest.mark.parametrize("kind", ["decode", "step", "prefill", "mixed"])
 def test_head_sizes_between_block_widths(gpu, name, kind):
     """Decode (the decode kernel and the one-launch step), block prefill and
-    a mixed step at head sizes the pool pads to 64 or 128 dims: attention
+    a mixed step at head sizes the pool pads to 64, 128 or 256 dims: attention
     against the oracle at the model's head_dim, the stored rows bit-exact
     (gather and raw layout, padding zero)."""
     qh, kvh, hd, fmt, sf = HEAD_SIZES[name]

@@ -64,6 +64,14 @@ def test_static_decode_equals_allocating_decode(gpu):
     s3, a3, _ = run_both(pad)
     assert np.array_equal(bits(s3), bits(a3)), "static and allocating decode differ (call 3)"
     assert_attention_close(s3, pad.oracle_out(), "static decode call 3")
+    # fourth call: 256-dim blocks (int8, split contexts)
+    say("static decode: fourth call (head_dim 256, int8)")
+    wide = PagedCase(16, 2, 256, tk.KV_I8, [3000, 20], 2, seed=74, outlier_frac=0.01)
+    wide.fill()
+    s4, a4, _ = run_both(wide)
+    assert np.array_equal(bits(s4), bits(a4)), "static and allocating decode differ (call 4)"
+    assert_attention_close(s4, wide.oracle_out(), "static decode call 4")
+    wide.close()
     pad.close()
     small.close()
     big.close()
