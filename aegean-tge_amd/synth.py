@@ -42,6 +42,9 @@ class Shape:
 QWEN2_0_5B = Shape("Qwen2-0.5B", 24, 14, 2, 64)
 QWEN2_1_5B = Shape("Qwen2-1.5B", 28, 12, 2, 128)
 QWEN2_7B = Shape("Qwen2-7B", 28, 28, 4, 128)
+# Attention shape of a 256-dim-head model (Gemma-2-9B: 16 query heads, 8 KV
+# heads); 8 layers are enough for per-layer figures.
+WIDE_HEADS = Shape("16/8 heads x 256 dims, 8 layers", 8, 16, 8, 256)
 
 
 @dataclass
@@ -87,6 +90,24 @@ def configs():
                      churn_context=2048, fragmented=False, seed=5,
                      note="64 sessions log-uniform 1k-32k, int8+f16 scales, 4-query verify, "
                           "churn 8 sessions / 16 steps"),
+    }
+
+
+def wide_head_configs():
+    """Two legs at head_dim 256 (256-dim page blocks), beside the
+    BASELINE configurations: a c5-like verify decode (32 sessions
+    log-uniform 1k-32k, int8 + f16 scales, 4 queries each) and a c4-like
+    prompt (2048 tokens in 4 causal chunks of 512, f16)."""
+    rng = np.random.default_rng(2026)
+    ctx = [int(round(math.exp(x))) for x in rng.uniform(math.log(1024), math.log(32768), 32)]
+    return {
+        "d256": Config("d256", WIDE_HEADS, tge_kv.KV_I8, ctx, steps=16, n_new=4, pool_pages=0,
+                       outlier_frac=0.01, fragmented=True, seed=6,
+                       note="head_dim 256: 32 sessions log-uniform 1k-32k, int8+f16 scales, "
+                            "4-query verify, fragmented pool"),
+        "p256": Config("p256", WIDE_HEADS, tge_kv.KV_F16, [0], steps=0, pool_pages=160,
+                       prefill_chunk=512, prompt=2048, bf16_inputs=True, seed=7,
+                       note="head_dim 256: 2048-token prompt in 4 causal chunks of 512, f16"),
     }
 
 

@@ -27,7 +27,10 @@ The other four configurations are measured briefly and reported under
 "configs" (they are parity cases, not the headline), each with its own
 "cpu_baseline": the reference's AVX2 kernels under the schedule the
 reference runs for that configuration (decode of one sequence, a batched
-step, block prefill per chunk), timed for a few seconds at most.
+step, block prefill per chunk), timed for a few seconds at most. Beside
+them: shared-prefix decode ("prefix"), a mixed verify + prefill step
+("mixed"), and 256-dim heads (synth.wide_head_configs: a verify decode
+"d256" and a chunked prompt "p256").
 
 Usage: python bench.py [--gpus 1] [--steps 32] [--warmup 4] [--no-others]
        [--no-cpu] [--cpu-seconds 10]
@@ -112,7 +115,8 @@ def parse():
     ap.add_argument("--cpu", dest="cpu", action="store_true", default=True)
     ap.add_argument("--no-cpu", dest="cpu", action="store_false")
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
-    ap.add_argument("--only", default="", help="run one config key (c1..c5, prefix, mixed) and print it")
+    ap.add_argument("--only", default="",
+                    help="run one config key (c1..c5, prefix, mixed, d256, p256) and print it")
     ap.add_argument("--calibrate-copy", action="store_true",
                     help="only time 1 GiB device-to-device copies (counter calibration)")
     ap.add_argument("--fragment-c5", action="store_true",
@@ -857,9 +861,10 @@ def main():
     import tge_kv as tk
     tk.require_gpu()
     cfgs = synth.configs()
+    cfgs.update(synth.wide_head_configs())
     others = {}
-    keys = [args.only] if args.only else (["c1", "c2", "c3", "c4", "prefix", "mixed"]
-                                          if args.others else [])
+    keys = [args.only] if args.only else (["c1", "c2", "c3", "c4", "prefix", "mixed", "d256",
+                                           "p256"] if args.others else [])
     for key in keys:
         if key == "c5":
             continue
@@ -876,13 +881,14 @@ def main():
         cfg = cfgs[key]
         log(f"[bench] {key}: {cfg.note}")
         cpu_s = min(2.0, args.cpu_seconds / 5) if args.cpu else 0.0
-        if key == "c4":
+        if key in ("c4", "p256"):
             others[key] = run_prefill(tk, synth, cfg)
             others[key]["cpu_baseline"] = cpu_baseline_prefill(synth, cfg, cpu_s)
         else:
             b = DecodeBench(tk, synth, cfg, cfg.steps + 4)
             r = b.run(cfg.steps, 4, 3)
             r["frac_attn"] = r["attn_gbs"] / HBM_PEAK_GBS
+            r["frac_attn_kernel"] = r["attn_kernel_gbs"] / HBM_PEAK_GBS
             b.model.close()
             r["cpu_baseline"] = cpu_baseline_decode(synth, cfg, cpu_s)
             others[key] = r
