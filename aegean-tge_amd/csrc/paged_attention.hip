@@ -601,7 +601,10 @@ void paged_decode_kernel(AttnParams p) {
 // never meet across waves, so each wave writes its rows (or its split's
 // partial) directly.
 // ---------------------------------------------------------------------------
-template <int FMT, bool SF32, int D, int WPE, int HALVES = 1>
+// NRGP: 16-row groups per wave (2, or 1 for 64-row tiles: the 256-dim
+// kernels, and the narrow 128-dim tiles of steps too small to fill the
+// compute units with 128-row tiles).
+template <int FMT, bool SF32, int D, int WPE, int HALVES = 1, int NRGP = (D > 128 ? 1 : 2)>
 struct PrefillShared {
   static constexpr int SLOT = Ring<FMT, SF32, D>::SLOT;
   static constexpr int TILE = kWaves * SLOT;  // four pages
@@ -609,7 +612,7 @@ struct PrefillShared {
   static constexpr int NB = NB_FIT > 4 ? 4 : NB_FIT;
   static_assert(NB >= 2, "the prefill ring needs two tiles");
   // one ring per half; afterwards the second half's states pass through it
-  static constexpr int NRG = D > 128 ? 1 : 2;  // row groups of 16 per wave
+  static constexpr int NRG = NRGP;  // row groups of 16 per wave
   static constexpr int XO = kWaves * NRG * (D / 16) * 64 * 16;  // accumulators (bytes)
   static constexpr int XS = kWaves * NRG * 3 * 64 * 4;          // base, sum, empty flag
   static_assert(HALVES == 1 || XO + XS <= HALVES * NB * TILE, "state exchange fits the rings");
@@ -646,13 +649,14 @@ __device__ __forceinline__ void half_barrier(int* ctr, int target) {
 
 // MERGE: split tiles are merged in the launch (the mixed-step kernel).
 // HALVES: 1 or 2 groups of four waves sharing the item's rows (see above).
-template <int FMT, bool SF32, int D, int WPE, bool SP, bool MERGE = false, int HALVES = 1>
+template <int FMT, bool SF32, int D, int WPE, bool SP, bool MERGE = false, int HALVES = 1,
+          int NRGP = (D > 128 ? 1 : 2)>
 __device__ __forceinline__ void prefill_body(const AttnParams& p,
-                                             PrefillShared<FMT, SF32, D, WPE, HALVES>& sh,
+                                             PrefillShared<FMT, SF32, D, WPE, HALVES, NRGP>& sh,
                                              const int item) {
   static_assert(HALVES == 1 || !MERGE, "the in-launch merge runs on four-wave workgroups");
-  using SH = PrefillShared<FMT, SF32, D, WPE, HALVES>;
-  constexpr int NRG = SH::NRG;  // 32 rows per wave (16 at 256 dims)
+  using SH = PrefillShared<FMT, SF32, D, WPE, HALVES, NRGP>;
+  constexpr int NRG = SH::NRG;  // 32 rows per wave (16 in 64-row tiles)
   using U = Unit<FMT, SF32, D, NRG>;
   using Regs = typename U::Regs;
   using RG = Ring<FMT, SF32, D>;
@@ -879,12 +883,12 @@ __device__ __forceinline__ void prefill_body(const AttnParams& p,
   }
 }
 
-template <int FMT, bool SF32, int D, int WPE, bool SP>
+template <int FMT, bool SF32, int D, int WPE, bool SP, int NRGP = (D > 128 ? 1 : 2)>
 __global__ __launch_bounds__(256 * halves_for_wpe<WPE>()) __attribute__((amdgpu_waves_per_eu(WPE, WPE)))
 void paged_prefill_kernel(AttnParams p) {
   constexpr int H = halves_for_wpe<WPE>();
-  __shared__ PrefillShared<FMT, SF32, D, WPE, H> sh;
-  prefill_body<FMT, SF32, D, WPE, SP, false, H>(p, sh, blockIdx.x);
+  __shared__ PrefillShared<FMT, SF32, D, WPE, H, NRGP> sh;
+  prefill_body<FMT, SF32, D, WPE, SP, false, H, NRGP>(p, sh, blockIdx.x);
 }
 
 // ---------------------------------------------------------------------------
@@ -1128,16 +1132,28 @@ constexpr int prefill_wpe() {
 #endif
 }
 
+// tile_rows: rows of the plan's tiles (128, or 64: one 16-row group per
+// wave; always 64 at 256 dims).
 template <int FMT, bool SF32, int D>
-hipError_t launch_prefill_d(int n_units, const AttnParams& p, hipStream_t stream) {
+hipError_t launch_prefill_d(int n_units, int tile_rows, const AttnParams& p, hipStream_t stream) {
   constexpr int wpe = prefill_wpe<FMT, D>();
-  const dim3 block(256 * halves_for_wpe<wpe>());
-  if (p.sp_stride > 0) {
-    hipLaunchKernelGGL((paged_prefill_kernel<FMT, SF32, D, wpe, true>), dim3((unsigned)n_units),
-                       block, 0, stream, p);
+  const dim3 block(256 * halves_for_wpe<wpe>()), grid((unsigned)n_units);
+  const bool sp = p.sp_stride > 0;
+  if (tile_rows == prefill_tile_rows(D)) {
+    if (sp) {
+      hipLaunchKernelGGL((paged_prefill_kernel<FMT, SF32, D, wpe, true>), grid, block, 0, stream, p);
+    } else {
+      hipLaunchKernelGGL((paged_prefill_kernel<FMT, SF32, D, wpe, false>), grid, block, 0, stream, p);
+    }
+  } else if constexpr (D == 128) {
+    if (tile_rows != 64) return hipErrorInvalidValue;
+    if (sp) {
+      hipLaunchKernelGGL((paged_prefill_kernel<FMT, SF32, D, wpe, true, 1>), grid, block, 0, stream, p);
+    } else {
+      hipLaunchKernelGGL((paged_prefill_kernel<FMT, SF32, D, wpe, false, 1>), grid, block, 0, stream, p);
+    }
   } else {
-    hipLaunchKernelGGL((paged_prefill_kernel<FMT, SF32, D, wpe, false>), dim3((unsigned)n_units),
-                       block, 0, stream, p);
+    return hipErrorInvalidValue;
   }
   return hipGetLastError();
 }
@@ -1208,12 +1224,12 @@ int prefill_halves(int format, int head_dim) {
   });
 }
 
-hipError_t launch_prefill(int format, int scale_f32, int head_dim, int n_units,
+hipError_t launch_prefill(int format, int scale_f32, int head_dim, int n_units, int tile_rows,
                           const AttnParams& p, hipStream_t stream) {
   if (n_units <= 0) return hipSuccess;
   return with_variant(format, scale_f32, head_dim, hipErrorInvalidValue,
                       [&]<int FMT, bool SF32, int D>() {
-                        return launch_prefill_d<FMT, SF32, D>(n_units, p, stream);
+                        return launch_prefill_d<FMT, SF32, D>(n_units, tile_rows, p, stream);
                       });
 }
 

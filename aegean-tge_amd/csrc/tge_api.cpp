@@ -622,7 +622,8 @@ int run_attention(const tge_batch* b, const tge_kv_pool* p, int layer, const flo
                                pl.lists.row_groups, pl.lists.groups, a, st));
   } else {
     TGE_HIP(tge::launch_prefill(p->desc.format, p->desc.scale_format == TGE_SCALE_F32,
-                                b->step.block_dims, (int)pl.lists.work.size(), a, st));
+                                b->step.block_dims, (int)pl.lists.work.size(), pl.lists.tile_rows,
+                                a, st));
   }
   if (ev) TGE_HIP(hipEventRecord((*ev)[1], st));
   if (!pl.lists.reduce.empty()) {

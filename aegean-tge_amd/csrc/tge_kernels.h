@@ -146,7 +146,8 @@ int mixed_blocks_per_cu(int format, int scale_f32, int head_dim, int row_groups)
 // item's pages are shared by both halves and the plan's items may be twice
 // as long.
 int prefill_halves(int format, int head_dim);
-hipError_t launch_prefill(int format, int scale_f32, int head_dim, int n_units,
+// tile_rows: the plan's tile rows (prefill_tile_rows, or 64 at 128 dims).
+hipError_t launch_prefill(int format, int scale_f32, int head_dim, int n_units, int tile_rows,
                           const AttnParams& p, hipStream_t stream);
 // Resident decode workgroups per CU (of the static sparse variant when
 // `sparse`).

@@ -345,20 +345,57 @@ void build_prefill(const Step& b, int cus, AttnLists& pl, int only, int halves) 
   pl.groups = 0;
   pl.parts = pl.max_splits = 0;
   pl.row_groups = kPrefillRows / 16;
-  const int tq = std::max(1, prefill_tile_rows(b.block_dims) / b.group);
-  // Page-split size: enough items for about two rounds of two four-wave
-  // workgroups on each compute unit (of one eight-wave workgroup with two
-  // halves), at least 32 pages (eight tiles of four) per half.
-  long pages_total = 0;
-  for (const auto& sr : b.sessions) {
-    if (!take_session(b, sr, only)) continue;
-    for (int a = 0; a < sr.n_new; a += tq)
-      pages_total += (long)((sr.ctx + std::min(sr.n_new, a + tq) + 15) / 16) * b.kv_heads;
-  }
   halves = halves == 2 ? 2 : 1;
+  // Page-split size for tiles of tq queries: enough items for about two
+  // rounds of two four-wave workgroups on each compute unit (of one
+  // eight-wave workgroup with two halves), at least 32 pages (eight tiles
+  // of four) per half. `pieces` counts the workgroups that gives.
   const long target_units = 2L * std::max(1, cus) * (halves == 2 ? 1 : 2);
-  const int pps = (int)std::max<long>((long)TGE_PREFILL_MIN_SPLIT * halves,
-                                      ((pages_total + target_units - 1) / target_units + 3) / 4 * 4);
+  auto split_size = [&](int tq, long* pieces) {
+    long pages_total = 0;
+    for (const auto& sr : b.sessions) {
+      if (!take_session(b, sr, only)) continue;
+      for (int a = 0; a < sr.n_new; a += tq)
+        pages_total += (long)((sr.ctx + std::min(sr.n_new, a + tq) + 15) / 16) * b.kv_heads;
+    }
+    const int pps = (int)std::max<long>((long)TGE_PREFILL_MIN_SPLIT * halves,
+                                        ((pages_total + target_units - 1) / target_units + 3) / 4 * 4);
+    if (pieces) {
+      *pieces = 0;
+      for (const auto& sr : b.sessions) {
+        if (!take_session(b, sr, only)) continue;
+        for (int a = 0; a < sr.n_new; a += tq)
+          *pieces += (long)(((sr.ctx + std::min(sr.n_new, a + tq) + 15) / 16 + pps - 1) / pps) *
+                     b.kv_heads;
+      }
+    }
+    return pps;
+  };
+  pl.tile_rows = prefill_tile_rows(b.block_dims);
+  int tq = std::max(1, pl.tile_rows / b.group);
+  int pps = split_size(tq, nullptr);
+  // Narrow tiles: a 128-dim step whose 128-row tiles would leave half the
+  // compute units idle (the two-halves kernel runs one workgroup per CU)
+  // takes 64-row tiles (one 16-row group per wave) instead: twice the
+  // workgroups, each with half the rows against the same pages.
+  if (halves == 2 && b.block_dims == 128 && b.group <= 64) {
+    long pieces = 0, items = 0;
+    split_size(tq, &pieces);
+    const int tq64 = std::max(1, 64 / b.group);
+    for (const auto& sr : b.sessions)
+      if (take_session(b, sr, only)) items += (long)((sr.n_new + tq64 - 1) / tq64) * b.kv_heads;
+    if (2 * pieces <= std::max(1, cus)) {
+      pl.tile_rows = 64;
+      tq = tq64;
+      pps = split_size(tq, nullptr);
+    } else if (items <= std::max(1, cus) && pieces > items / 2) {
+      // the split 128-row tiles need a merge launch; one round of unsplit
+      // 64-row tiles does not
+      pl.tile_rows = 64;
+      tq = tq64;
+      pps = 1 << 30;
+    }
+  }
   for (int s = 0; s < (int)b.sessions.size(); ++s) {
     const SessionRec& sr = b.sessions[(std::size_t)s];
     if (!take_session(b, sr, only)) continue;

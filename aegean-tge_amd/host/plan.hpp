@@ -88,6 +88,7 @@ struct AttnLists {
   std::vector<int> wg_first;  // [groups + 1] first item of each workgroup, or empty
   int groups = 0;             // workgroups of the launch
   int row_groups = 1;         // 16-row groups per unit
+  int tile_rows = 0;          // prefill: rows of a tile (prefill_tile_rows, or 64)
   int parts = 0;              // split-K partial slots
   int max_splits = 0;
 };

@@ -283,7 +283,8 @@ int tge_decode_attention_static(const tge_batch_desc* desc, const tge_kv_pool* p
  * prior page and the chunk itself, on f16 MFMA (Q rounded to f16 as in
  * decode; I8 pools run the same kernel where the reference takes its
  * per-token i8 path, qwen2.cpp:1535-1538). Tiles of up to 128
- * (query, head) rows of one KV head's query group (64 at head_dim > 128);
+ * (query, head) rows of one KV head's query group (64 at head_dim > 128,
+ * and for steps whose 128-row tiles would leave compute units idle);
  * long prefixes are split and merged like decode.
  */
 int tge_prefill_attention(const tge_batch* batch, const tge_kv_pool* pool,

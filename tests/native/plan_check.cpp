@@ -112,6 +112,9 @@ void check_lists(const Step& st, const AttnLists& l, int only, bool prefill) {
     REQUIRE(take_session(st, sr, only), "session %d should not be planned", w.session);
     REQUIRE(w.kv_head >= 0 && w.kv_head < st.kv_heads, "kv head %d", w.kv_head);
     REQUIRE(w.rows >= 1 && w.rows <= 16 * l.row_groups, "rows %d of %d", w.rows, 16 * l.row_groups);
+    if (prefill)
+      REQUIRE(w.rows <= std::max(l.tile_rows, st.group), "rows %d past the %d-row tile", w.rows,
+              l.tile_rows);
     REQUIRE(w.rows_per_query == st.group && w.head_base == w.kv_head * st.group, "row mapping");
     REQUIRE(w.rows % st.group == 0 && w.row_begin + w.rows / st.group <= sr.n_new, "row range");
     REQUIRE(w.ctx == sr.ctx && w.q_row == sr.q_row && w.table_off == sr.table_off, "copies");
@@ -125,7 +128,7 @@ void check_lists(const Step& st, const AttnLists& l, int only, bool prefill) {
     const SessionRec& sr = st.sessions[(std::size_t)s];
     if (!take_session(st, sr, only)) continue;
     for (int h = 0; h < st.kv_heads; ++h) {
-      const int tq = prefill ? std::max(1, kPrefillRows / st.group) : sr.n_new;
+      const int tq = prefill ? std::max(1, l.tile_rows / st.group) : sr.n_new;
       for (int a = 0; a < sr.n_new; a += tq) {
         const auto it = by.find({s, h, a});
         REQUIRE(it != by.end(), "session %d head %d tile %d has no work", s, h, a);
@@ -253,6 +256,7 @@ void check_step_lists(const Step& st, bool i8, bool sf32) {
 
 void random_plans(int cases) {
   std::mt19937 rng(12345);
+  int narrow_seen = 0, wide_seen = 0;
   for (int i = 0; i < cases; ++i) {
     const int kvh = 1 << (rng() % 4);
     const int group = (i % 17 == 0) ? 1 + (int)(rng() % 128) : 1 + (int)(rng() % 8);
@@ -295,6 +299,11 @@ void random_plans(int cases) {
       }
       const int halves = 1 + (int)(rng() % 2);
       build_prefill(st, cus, pf, only, halves);
+      REQUIRE(pf.tile_rows == prefill_tile_rows(st.block_dims) ||
+                  (pf.tile_rows == 64 && st.block_dims == 128 && halves == 2),
+              "tile rows %d at %d dims", pf.tile_rows, st.block_dims);
+      if (pf.tile_rows == 64 && st.block_dims == 128) narrow_seen++;
+      if (pf.tile_rows == 128 && halves == 2) wide_seen++;
       check_lists(st, pf, only, true);
       std::size_t ofr = 0, off = 0;
       const std::size_t bytes = image_layout(pf, &ofr, &off);
@@ -305,6 +314,8 @@ void random_plans(int cases) {
                 "image");
     }
   }
+  REQUIRE(narrow_seen > 0 && wide_seen > 0, "tile widths: %d narrow, %d wide", narrow_seen,
+          wide_seen);
 }
 
 void invalid_descriptions() {
