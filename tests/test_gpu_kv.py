@@ -392,6 +392,37 @@ def test_prefill_chunks_match_oracle(gpu):
     pool.close()
 
 
+# Block prefill at head_dim 128 in both tile widths: (q_heads, kv_heads,
+# format, contexts, n_new). On 256 compute units the planner takes 128-row
+# tiles for the "wide" cases (144 items; 280 as 64-row tiles), unsplit
+# 64-row tiles where the 128-row ones would be split and merged (136
+# pieces of 68 tiles; 136 narrow items) and 64-row tiles for a small step
+# (56 items).
+TILE_CASES = {
+    "wide_f16": (16, 8, tk.KV_F16, [0], [1100]),
+    "wide_i8": (16, 8, tk.KV_I8, [0], [1100]),
+    "narrow_unsplit_f16": (28, 4, tk.KV_F16, [1500], [300]),
+    "narrow_small_i8": (28, 4, tk.KV_I8, [200, 0], [150, 90]),
+}
+
+
+@pytest.mark.parametrize("name", list(TILE_CASES))
+def test_prefill_tile_widths(gpu, name):
+    """128-row and 64-row block-prefill tiles (the planner's choice by step
+    size) against the oracle, stored rows bit-exact."""
+    qh, kvh, fmt, contexts, n_new = TILE_CASES[name]
+    say(f"prefill tiles {name}: contexts {contexts} n_new {n_new}")
+    case = PagedCase(qh, kvh, 128, fmt, contexts, n_new, seed=7400 + len(name),
+                     outlier_frac=0.01 if fmt == tk.KV_I8 else 0)
+    case.fill()
+    got, b = case.step(kind="prefill")
+    err = assert_attention_close(got, case.oracle_out(), f"prefill tiles {name}")
+    say(f"  max abs err {err:.2e}")
+    b.close()
+    check_contents(case)
+    case.close()
+
+
 @pytest.mark.parametrize("fmt", [tk.KV_F16, tk.KV_I8])
 def test_pool_layer_beyond_4gib(gpu, fmt):
     """One layer's block array past 4 GiB: the kernels address each page
