@@ -163,6 +163,12 @@ __global__ __launch_bounds__(64 * kStepWaves) void paged_step_kernel(StepParams 
   const StepRec rec = load_step((const sconst_step*)p.recs + blockIdx.x);
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  // the first batch's page ids, requested with the record (no dependence on it)
+  static_assert(PB * W <= kStepFirstIds, "first-batch ids");
+  const sconst_int* fids = (const sconst_int*)(p.first_ids + (size_t)blockIdx.x * kStepFirstIds);
+  int first_ids[PB];
+#pragma unroll
+  for (int i = 0; i < PB; ++i) first_ids[i] = fids[i * W + wave];
   const int col = lane & 15;
   const int grp = lane >> 4;
   const int group = p.group;
@@ -259,12 +265,10 @@ __global__ __launch_bounds__(64 * kStepWaves) void paged_step_kernel(StepParams 
   const int j0 = rec.page_begin + wave;
   Regs r[PB];
   auto first_batch = [&]() __attribute__((always_inline)) {
-    int ids[PB];
-#pragma unroll
-    for (int i = 0; i < PB; ++i) ids[i] = table[min(j0 + i * W, rec.page_end - 1)];
 #pragma unroll
     for (int i = 0; i < PB; ++i)
-      load_page<FMT, SF32, D>(r[i], pool + ((size_t)ids[i] * kv_heads + rec.kv_head) * bb, lane, grp);
+      load_page<FMT, SF32, D>(r[i], pool + ((size_t)first_ids[i] * kv_heads + rec.kv_head) * bb, lane,
+                              grp);
   };
   // (an appending piece whose first batch ends before the new positions
   // issues it now as well)

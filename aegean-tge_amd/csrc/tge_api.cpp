@@ -426,9 +426,12 @@ int upload_step_plan(tge_batch* b, const tge_kv_pool* pool, hipStream_t st) {
                                    pool->desc.scale_format == TGE_SCALE_F32, sp.lists))
     return TGE_OK;
   const auto& L = sp.lists;
-  const size_t bytes = L.recs.size() * sizeof(tge::StepRec);
-  int s = sp.image.upload(g_mem, bytes, st, [&](char* h) {
-    std::memcpy(h, L.recs.data(), bytes);
+  // [ records | first-batch page ids ]
+  const size_t rbytes = L.recs.size() * sizeof(tge::StepRec);
+  const size_t ibytes = L.first_ids.size() * sizeof(int);
+  int s = sp.image.upload(g_mem, rbytes + ibytes, st, [&](char* h) {
+    std::memcpy(h, L.recs.data(), rbytes);
+    std::memcpy(h + rbytes, L.first_ids.data(), ibytes);
   });
   if (s != TGE_OK) return s;
   const size_t rows_cap = 16 * (size_t)L.row_groups;
@@ -769,6 +772,7 @@ int tge_decode_step(const tge_batch* b, tge_kv_pool* p, int layer, const float* 
   a.app.scale_f32 = p->desc.scale_format == TGE_SCALE_F32;
   a.app.q_heads = b->step.q_heads;
   a.recs = reinterpret_cast<const tge::StepRec*>(sp.image.dev);
+  a.first_ids = reinterpret_cast<const int*>(sp.image.dev + sp.lists.recs.size() * sizeof(tge::StepRec));
   a.tables = reinterpret_cast<const int*>(b->image.dev + b->off_tables);
   a.q = q;
   a.out = out;

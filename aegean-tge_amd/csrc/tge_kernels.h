@@ -91,6 +91,7 @@ struct ReduceParams {
 struct StepParams {
   AppendParams app;       // pool, geometry, k/v rows, scale format (rows unused)
   const StepRec* recs;    // one per workgroup
+  const int* first_ids;   // [workgroups][kStepFirstIds]: the first batch's page ids
   const int* tables;
   const float* q;         // [rows][q_heads*app.dims]
   float* out;

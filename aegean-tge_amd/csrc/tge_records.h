@@ -93,6 +93,11 @@ static_assert(sizeof(StepRec) == 16 * sizeof(int), "StepRec is read as 16 ints")
 // is a whole number of such batches.
 constexpr int kStepWaves = 8;
 constexpr int kStepMaxParts = 64;  // pieces of one (session, KV head) context
+// Page ids of a piece's first batch, stored beside its record so that the
+// kernel loads them with the record instead of after it: [i][wave] is the
+// i-th page of the wave's batch, page_begin + wave + i * kStepWaves, or the
+// piece's last page past its end (batches hold at most 4 pages per wave).
+constexpr int kStepFirstIds = 4 * kStepWaves;
 constexpr int step_batch_pages(bool i8, bool scale_f32, int head_dim, int row_groups) {
   const int np = head_dim / 32;
   const int kw = i8 ? 2 * np : 4 * np;

@@ -490,6 +490,14 @@ bool build_step_lists(const Step& b, bool i8, bool scale_f32, StepLists& out) {
         r.q_row = sr.q_row;
         r.table_off = sr.table_off;
         out.recs.push_back(r);
+        const int pb = batch / kStepWaves;
+        for (int i = 0; i < kStepFirstIds / kStepWaves; ++i)
+          for (int w = 0; w < kStepWaves; ++w) {
+            const int pg = std::min(r.page_begin + w + i * kStepWaves, r.page_end - 1);
+            out.first_ids.push_back(i < pb && pg >= 0
+                                        ? b.tables[(std::size_t)(r.table_off + pg)]
+                                        : 0);
+          }
       }
     }
   }

@@ -122,6 +122,7 @@ void build_prefill(const Step& s, int cus, AttnLists& out, int only, int halves 
 // consecutive partial slots and the segment's arrival counter.
 struct StepLists {
   std::vector<StepRec> recs;
+  std::vector<int> first_ids;  // [recs][kStepFirstIds]
   int row_groups = 1;
   int piece_pages = 0;  // pages of every piece but a segment's first
   int parts = 0;        // partial slots

@@ -206,6 +206,20 @@ void check_step_lists(const Step& st, bool i8, bool sf32) {
   const bool unsplit = step_pages <= 3 * batch;
   REQUIRE(sl.piece_pages >= batch && sl.piece_pages % batch == 0, "piece %d batch %d",
           sl.piece_pages, batch);
+  // the first batch's page ids beside each record: what the block table
+  // holds for the pages the waves load first (the piece's last page past
+  // its end)
+  REQUIRE(sl.first_ids.size() == sl.recs.size() * (std::size_t)kStepFirstIds, "first ids");
+  for (std::size_t r = 0; r < sl.recs.size(); ++r) {
+    const StepRec& rec = sl.recs[r];
+    for (int b = 0; b < batch / kStepWaves; ++b)
+      for (int w = 0; w < kStepWaves; ++w) {
+        const int pg = std::min(rec.page_begin + w + b * kStepWaves, rec.page_end - 1);
+        REQUIRE(sl.first_ids[r * kStepFirstIds + (std::size_t)(b * kStepWaves + w)] ==
+                    st.tables[(std::size_t)(rec.table_off + pg)],
+                "first id of record %zu, batch page %d, wave %d", r, b, w);
+      }
+  }
   REQUIRE(sl.piece_pages == batch || sl.max_pieces > kStepMaxParts / 2, "pieces longer than needed");
   std::vector<int> slot_used((std::size_t)sl.parts, 0);
   std::size_t i = 0;
