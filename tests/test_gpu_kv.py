@@ -785,6 +785,51 @@ def test_head_sizes_between_block_widths(gpu, name, kind):
     case.close()
 
 
+def _random_head_case(i):
+    """Seeded random head size for test_random_head_sizes: f16 any multiple
+    of 16 up to 256, int8 any multiple of 32; GQA group 1-8, 1-4 KV heads,
+    1-4 sessions; decode, the one-launch step, block prefill or a mixed
+    step, within the row limits of the head size's block width."""
+    r = np.random.default_rng(5000 + i)
+    fmt = int(r.choice([tk.KV_F16, tk.KV_I8]))
+    hd = int(16 * r.integers(1, 17)) if fmt == tk.KV_F16 else int(32 * r.integers(1, 9))
+    sf = int(r.choice([tk.SCALE_F16, tk.SCALE_F32])) if fmt == tk.KV_I8 else tk.SCALE_F16
+    kvh = int(r.choice([1, 2, 4]))
+    group = int(r.integers(1, 9))
+    unit = 48 if hd > 128 else 64  # rows of a decode unit
+    kind = ("decode", "step", "prefill", "mixed")[i % 4]
+    n_s = int(r.integers(1, 5))
+    contexts = [0 if r.integers(0, 4) == 0 else int(r.integers(1, 1800)) for _ in range(n_s)]
+    if kind in ("decode", "step"):
+        n_new = [int(r.integers(1, unit // group + 1)) for _ in range(n_s)]
+    elif kind == "mixed":
+        n_new = [int(r.integers(1, unit // group + 1)) if k % 2 == 0 else
+                 int(r.integers(unit // group + 1, 100)) for k in range(n_s)]
+    else:
+        n_new = [int(r.integers(1, 90)) for _ in range(n_s)]
+    return dict(qh=kvh * group, kvh=kvh, hd=hd, fmt=fmt, sf=sf, kind=kind, contexts=contexts,
+                n_new=n_new)
+
+
+@pytest.mark.parametrize("i", range(16))
+def test_random_head_sizes(gpu, i):
+    """Sixteen seeded random head sizes (16-256 dims, padded to 64-, 128-
+    or 256-dim blocks) over random shapes and step kinds against the
+    oracle, stored rows bit-exact."""
+    c = _random_head_case(i)
+    say(f"random head size case {i}: {c}")
+    case = PagedCase(c["qh"], c["kvh"], c["hd"], c["fmt"], c["contexts"], c["n_new"],
+                     scale_format=c["sf"], seed=6000 + i,
+                     outlier_frac=0.01 if c["fmt"] == tk.KV_I8 else 0)
+    case.fill()
+    got, b = case.step(kind=c["kind"])
+    err = assert_attention_close(got, case.oracle_out(), f"random head size case {i}")
+    say(f"  max abs err {err:.2e}")
+    b.close()
+    check_contents(case)
+    case.close()
+
+
 @pytest.mark.parametrize("kind", ["decode", "prefill", "mixed"])
 def test_head_size_96_int8_sparse(gpu, kind):
     """The static sparse subset at a padded head size (int8, 96 dims in
