@@ -798,7 +798,8 @@ int tge_prefill_attention(const tge_batch* b, const tge_kv_pool* p, int layer,
   tge_batch* mb = const_cast<tge_batch*>(b);
   if (!mb->prefill.built) {
     tge::plan::build_prefill(mb->step, device_cus(), mb->prefill.lists, 0,
-                             tge::prefill_halves(p->desc.format, b->step.block_dims));
+                             tge::prefill_halves(p->desc.format, b->step.block_dims),
+                             p->desc.format == TGE_KV_I8);
     s = upload_plan(mb->prefill, b->step.block_dims, static_cast<hipStream_t>(stream));
     if (s != TGE_OK) return s;
   }

@@ -338,7 +338,7 @@ void add_units(std::vector<WorkRec>& work, std::vector<ReduceRec>& red, int& par
 #define TGE_PREFILL_MIN_SPLIT 32
 #endif
 
-void build_prefill(const Step& b, int cus, AttnLists& pl, int only, int halves) {
+void build_prefill(const Step& b, int cus, AttnLists& pl, int only, int halves, bool i8) {
   pl.work.clear();
   pl.reduce.clear();
   pl.wg_first.clear();
@@ -377,7 +377,9 @@ void build_prefill(const Step& b, int cus, AttnLists& pl, int only, int halves) 
   // Narrow tiles: a 128-dim step whose 128-row tiles would leave half the
   // compute units idle (the two-halves kernel runs one workgroup per CU)
   // takes 64-row tiles (one 16-row group per wave) instead: twice the
-  // workgroups, each with half the rows against the same pages.
+  // workgroups, each with half the rows against the same pages. With f16
+  // pages, so does a step whose 128-row tiles would be split and merged
+  // while its 64-row tiles fit one round of workgroups unsplit.
   if (halves == 2 && b.block_dims == 128 && b.group <= 64) {
     long pieces = 0, items = 0;
     split_size(tq, &pieces);
@@ -388,9 +390,10 @@ void build_prefill(const Step& b, int cus, AttnLists& pl, int only, int halves) 
       pl.tile_rows = 64;
       tq = tq64;
       pps = split_size(tq, nullptr);
-    } else if (items <= std::max(1, cus) && pieces > items / 2) {
+    } else if (!i8 && items <= std::max(1, cus) && pieces > items / 2) {
       // the split 128-row tiles need a merge launch; one round of unsplit
-      // 64-row tiles does not
+      // 64-row tiles does not (f16 pages: with int8 ones the split
+      // 128-row tiles measure faster)
       pl.tile_rows = 64;
       tq = tq64;
       pps = 1 << 30;

@@ -114,8 +114,13 @@ void build_decode(const Step& s, Residency res, AttnLists& out, int only);
 // Block-prefill work: (session, KV head, query tile) x page splits sized so
 // the launch covers `cus` compute units about twice; longest items first.
 // `halves`: groups of four waves per workgroup (2: an item's pages are
-// shared by two halves, so items may be twice as long).
-void build_prefill(const Step& s, int cus, AttnLists& out, int only, int halves = 1);
+// shared by two halves, so items may be twice as long). At 128 dims with
+// two halves the tiles may be 64 rows (tile_rows) when 128-row tiles would
+// leave compute units idle; `i8`: int8 pages (whose dequantisation makes a
+// page read serve fewer rows at a higher cost, so unsplit 64-row tiles do
+// not replace split 128-row ones).
+void build_prefill(const Step& s, int cus, AttnLists& out, int only, int halves = 1,
+                   bool i8 = false);
 
 // A small decode step in one launch (paged_step_kernel): one workgroup per
 // piece of a (session, KV head) segment; pieces of a split segment own

@@ -312,7 +312,8 @@ void random_plans(int cases) {
         REQUIRE(dec.groups <= res.groups, "more workgroups than resident");
       }
       const int halves = 1 + (int)(rng() % 2);
-      build_prefill(st, cus, pf, only, halves);
+      const bool pf_i8 = rng() % 2;
+      build_prefill(st, cus, pf, only, halves, pf_i8);
       REQUIRE(pf.tile_rows == prefill_tile_rows(st.block_dims) ||
                   (pf.tile_rows == 64 && st.block_dims == 128 && halves == 2),
               "tile rows %d at %d dims", pf.tile_rows, st.block_dims);

@@ -396,12 +396,13 @@ def test_prefill_chunks_match_oracle(gpu):
 # format, contexts, n_new). On 256 compute units the planner takes 128-row
 # tiles for the "wide" cases (144 items; 280 as 64-row tiles), unsplit
 # 64-row tiles where the 128-row ones would be split and merged (136
-# pieces of 68 tiles; 136 narrow items) and 64-row tiles for a small step
-# (56 items).
+# pieces of 68 tiles; 136 narrow items; f16 only: int8 keeps the split
+# 128-row tiles) and 64-row tiles for a small step (56 items).
 TILE_CASES = {
     "wide_f16": (16, 8, tk.KV_F16, [0], [1100]),
     "wide_i8": (16, 8, tk.KV_I8, [0], [1100]),
     "narrow_unsplit_f16": (28, 4, tk.KV_F16, [1500], [300]),
+    "wide_split_i8": (28, 4, tk.KV_I8, [1500], [300]),
     "narrow_small_i8": (28, 4, tk.KV_I8, [200, 0], [150, 90]),
 }
 
