@@ -854,7 +854,7 @@ def main():
         return
     if args.gpus != 1:
         print(f"bench.py runs on one GPU only: this build measures the single-GPU hot path "
-              f"(asked for --gpus {args.gpus}); how it would shard is described in DESIGN.md.",
+              f"(asked for --gpus {args.gpus}); multi-GPU runs are not part of it.",
               file=sys.stderr)
         sys.exit(2)
     import synth

@@ -172,8 +172,8 @@ def test_quantize_multiply_then_add_is_not_fused():
 
 
 def test_quantize_codes_use_the_fp32_scale():
-    # the f16-scale format stores float_to_half(scale) but its
-    # codes come from the fp32 scale. Each value sits a margin above a
+    # The f16-scale format stores float_to_half(scale) but its codes come
+    # from the fp32 scale (quantize_kv_block / store_kv_q8, qwen2.cpp:88-120). Each value sits a margin above a
     # half-integer multiple of the fp32 scale and below it for the (larger)
     # f16-rounded scale, so codes derived from the stored f16 scale would be
     # one smaller in magnitude on every non-maximum slot.
