@@ -463,9 +463,18 @@ struct Unit {
   // (wave-uniform). sp_stride 0: off.
   int sp_sink, sp_stride, sp_hi;
   int mid[NRG];
+  // the phase's modulo without a division per page (Lemire's fastmod:
+  // sp_m = 2^64 / stride rounded up; (p0 + sp_off) mod stride equals
+  // (p0 - sink) mod stride with a non-negative left side)
+  uint64_t sp_m;
+  int sp_off;
 
   __device__ __forceinline__ void set_sparse(int sink, int window, int stride, int span_max) {
     sp_sink = sink;
+    if (stride > 0) {
+      sp_m = ~0ull / (uint64_t)stride + 1;
+      sp_off = stride - sink % stride;
+    }
     sp_stride = stride;
     sp_hi = span_max > sink + window ? span_max - window : sink;
 #pragma unroll
@@ -482,8 +491,11 @@ struct Unit {
   // stride in [0, stride), also when p0 < sink (a lane's 4 positions may
   // straddle sink).
   __device__ __forceinline__ int sparse_phase(int p0) const {
-    const int r = (p0 - sp_sink) % sp_stride;
-    return r < 0 ? r + sp_stride : r;
+    const uint32_t a = (uint32_t)(p0 + sp_off);
+    const uint64_t low = sp_m * a;
+    const uint64_t s = (uint64_t)(uint32_t)(low >> 32) * (uint32_t)sp_stride +
+                       __umulhi((uint32_t)low, (uint32_t)sp_stride);
+    return (int)(s >> 32);
   }
   // Drop the lane's 4 positions p0..p0+3 of row group rg that fall between
   // sink and the row's window off the stride; `ph` = sparse_phase(p0).
