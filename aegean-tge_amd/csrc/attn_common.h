@@ -468,6 +468,12 @@ struct Unit {
   // (p0 - sink) mod stride with a non-negative left side)
   uint64_t sp_m;
   int sp_off;
+  // Strides up to 28: bit x of sp_on is set for x in {0, stride, 2*stride}
+  // (a position's phase plus its index in the lane's run is below 32), and
+  // sp_lo is the smallest window start over the wave's valid rows, so a
+  // page in [sink, sp_lo) is wholly inside every row's strided middle.
+  uint32_t sp_on;
+  int sp_lo;
 
   __device__ __forceinline__ void set_sparse(int sink, int window, int stride, int span_max) {
     sp_sink = sink;
@@ -477,11 +483,17 @@ struct Unit {
     }
     sp_stride = stride;
     sp_hi = span_max > sink + window ? span_max - window : sink;
+    int lo = 0x7fffffff;
 #pragma unroll
     for (int rg = 0; rg < NRG; ++rg) {
       const int span = lim[rg] + 1;
       mid[rg] = span > sink + window ? span - window : sink;
+      if (lim[rg] >= 0) lo = min(lo, mid[rg]);
     }
+#pragma unroll
+    for (int off = 32; off >= 1; off >>= 1) lo = min(lo, __shfl_xor(lo, off));
+    sp_lo = stride > 0 && stride <= 28 ? lo : sink;  // (sink: no page takes the fast path)
+    sp_on = stride > 0 && stride <= 28 ? (1u | (1u << stride) | (stride <= 15 ? 1u << (2 * stride) : 0u)) : 0u;
   }
   // Whether page pi holds a position some row may drop (wave-uniform).
   __device__ __forceinline__ bool sparse_page(int pi) const {
@@ -758,6 +770,11 @@ struct Unit {
 
     const bool sp = SPARSE && sparse_page(pi);
     const int ph = sp ? sparse_phase(pi * 16 + 4 * grp) : 0;
+    // (wave-uniform) the page lies inside every row's strided middle: the
+    // lane's four positions are kept exactly where their phase is on the
+    // stride, the same for every row group
+    const bool inner = sp && pi * 16 >= sp_sink && pi * 16 + 16 <= sp_lo;
+    const uint32_t on4 = (sp_on >> ph) & 15u;
 #pragma unroll
     for (int rg = 0; rg < NRG; ++rg) {
       sacc[rg] -= base[rg];  // exact: base is an integer
@@ -767,7 +784,13 @@ struct Unit {
           if (pi * 16 + 4 * grp + e > lim[rg]) sacc[rg][e] = -INFINITY;
         }
       }
-      if (sp) sparse_mask(sacc[rg], pi * 16 + 4 * grp, ph, rg);
+      if (inner) {
+#pragma unroll
+        for (int e = 0; e < 4; ++e)
+          if (!((on4 >> e) & 1u)) sacc[rg][e] = -INFINITY;
+      } else if (sp) {
+        sparse_mask(sacc[rg], pi * 16 + 4 * grp, ph, rg);
+      }
       const float lmax = fmaxf(fmaxf(sacc[rg][0], sacc[rg][1]), fmaxf(sacc[rg][2], sacc[rg][3]));
       if (__builtin_expect(__any(lmax > thr[rg]), 0)) {
         // rare: some row passed its threshold; move that row's base
