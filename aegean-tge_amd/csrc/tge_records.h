@@ -90,7 +90,9 @@ static_assert(sizeof(StepRec) == 16 * sizeof(int), "StepRec is read as 16 ints")
 // holds in registers at once (page images of 2*KW + 2*SW dwords per lane
 // beside the unit's accumulators; KW dwords of K per lane = 16 tokens x
 // head_dim elements / 64 lanes, SW dwords of scales). A piece of a context
-// is a whole number of such batches.
+// is a whole number of such batches. int8 pages take two per wave even
+// where four fit: split contexts then have pieces half as long (the page
+// math of a piece, not its loads, sets its length).
 constexpr int kStepWaves = 8;
 constexpr int kStepMaxParts = 64;  // pieces of one (session, KV head) context
 // Page ids of a piece's first batch, stored beside its record so that the
@@ -102,7 +104,7 @@ constexpr int step_batch_pages(bool i8, bool scale_f32, int head_dim, int row_gr
   const int np = head_dim / 32;
   const int kw = i8 ? 2 * np : 4 * np;
   const int sw = i8 ? (scale_f32 ? 4 * np : 2 * np) : 0;
-  return row_groups >= 3 || head_dim > 128 ? 1 : (2 * kw + 2 * sw <= 16 ? 4 : 2);
+  return row_groups >= 3 || head_dim > 128 ? 1 : (2 * kw + 2 * sw <= 16 && !i8 ? 4 : 2);
 }
 
 // Steps the one-kernel step takes: rows per unit that fit its registers.
