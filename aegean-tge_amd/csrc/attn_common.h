@@ -746,9 +746,11 @@ struct Unit {
   template <bool SPARSE, class QF>
   __device__ __forceinline__ void score_phase(const Regs& r, int pi, int grp, bool masked,
                                               const QF& qf, half4_t (&pw)[NRG]) {
+    // The scores start at -base (exact: base is an integer), so they come
+    // out relative to the row bases with no subtraction pass.
     float4_t sacc[NRG];
 #pragma unroll
-    for (int rg = 0; rg < NRG; ++rg) sacc[rg] = float4_t{0, 0, 0, 0};
+    for (int rg = 0; rg < NRG; ++rg) sacc[rg] = float4_t{-base[rg], -base[rg], -base[rg], -base[rg]};
 #pragma unroll
     for (int pp = 0; pp < NP; ++pp) {
       const half8_t ka = k_operand<FMT, SF32, D>(r, pp);
@@ -777,7 +779,6 @@ struct Unit {
     const uint32_t on4 = (sp_on >> ph) & 15u;
 #pragma unroll
     for (int rg = 0; rg < NRG; ++rg) {
-      sacc[rg] -= base[rg];  // exact: base is an integer
       if (masked) {
 #pragma unroll
         for (int e = 0; e < 4; ++e) {

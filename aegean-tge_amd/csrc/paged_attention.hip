@@ -40,6 +40,11 @@
 #include "attn_common.h"
 
 namespace tge {
+
+// Bounded waits inside the kernels (half_barrier) that ran out since the
+// process started: a launch during which one expired may have wrong rows.
+__device__ unsigned int g_wait_expired;
+
 namespace {
 
 // ---------------------------------------------------------------------------
@@ -633,17 +638,22 @@ constexpr int halves_for_wpe() {
 // Tile barrier of one half's four waves (the two halves run their tile
 // loops independently): this wave's LDS reads are complete, it counts in,
 // and waits until all four have counted `target` arrivals in total. The
-// wait is bounded (about 0.2 s): past the bound the wave goes on and the
-// launch completes with wrong rows instead of hanging.
+// wait is bounded (about 0.2 s): past the bound the wave goes on, the
+// launch completes with wrong rows instead of hanging, and the expiry is
+// counted in g_wait_expired (tge_wait_expiries reads it).
 __device__ __forceinline__ void half_barrier(int* ctr, int target) {
   asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
   if ((threadIdx.x & 63) == 0) __hip_atomic_fetch_add(ctr, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
-  for (int spin = 0; spin < (1 << 21); ++spin) {
+  constexpr int kSpins = 1 << 21;
+  int spin = 0;
+  for (; spin < kSpins; ++spin) {
     const int seen = __builtin_amdgcn_readfirstlane(
         __hip_atomic_load(ctr, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP));
     if (seen >= target) break;
     __builtin_amdgcn_s_sleep(1);
   }
+  if (spin == kSpins && (threadIdx.x & 63) == 0)
+    __hip_atomic_fetch_add(&g_wait_expired, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
   __atomic_signal_fence(__ATOMIC_SEQ_CST);
 }
 
@@ -1252,6 +1262,11 @@ hipError_t launch_reduce_d(int n_items, int max_parts, const ReduceParams& p, hi
       break;
   }
   return hipGetLastError();
+}
+
+hipError_t read_wait_expiries(unsigned int* out) {
+  return hipMemcpyFromSymbol(out, HIP_SYMBOL(g_wait_expired), sizeof(unsigned int), 0,
+                             hipMemcpyDeviceToHost);
 }
 
 hipError_t launch_reduce(int head_dim, int n_items, int max_parts, const ReduceParams& p,

@@ -5,6 +5,7 @@
 #include <hip/hip_runtime.h>
 
 #include <algorithm>
+#include <climits>
 #include <cmath>
 #include <cstdlib>
 #include <cstring>
@@ -163,6 +164,9 @@ struct tge_batch {
   tge::plan::Step step;  // host copy of the plan
   StepPlan small;        // one-launch decode steps (tge_decode_step)
   bool planned = false;
+  // The pool's storage the plan was built for (the one-launch step's page
+  // batches depend on it).
+  int format = 0, scale_format = 0;
   AttnPlan decode, prefill;
   // Mixed steps (tge_batch_attention): the decode kernel over the sessions
   // whose rows fit a decode unit, the prefill kernel over the others.
@@ -461,6 +465,8 @@ int tge_batch_plan(tge_batch* b, const tge_kv_pool* pool, const tge_batch_desc* 
                                 pool->desc.pages, &msg);
   if (s != TGE_OK) return fail(s, msg ? msg : "batch_plan: invalid description");
   tge::plan::Step& st = b->step;
+  b->format = pool->desc.format;
+  b->scale_format = pool->desc.scale_format;
   b->prefill.built = false;
   b->decode.built = false;
   b->mix_built = false;
@@ -558,7 +564,8 @@ int check_use(const tge_batch* b, const tge_kv_pool* p, int layer, const char* w
   if (!b || !p) return fail(TGE_ERR_INVALID, std::string(who) + ": null argument");
   if (!b->planned) return fail(TGE_ERR_INVALID, std::string(who) + ": batch not planned");
   if (b->step.kv_heads != p->desc.kv_heads || b->step.head_dim != p->desc.head_dim ||
-      b->step.pages != p->desc.pages)
+      b->step.pages != p->desc.pages || b->format != p->desc.format ||
+      b->scale_format != p->desc.scale_format)
     return fail(TGE_ERR_INVALID, std::string(who) + ": batch planned for another pool");
   if (layer < 0 || layer >= p->desc.layers)
     return fail(TGE_ERR_INVALID, std::string(who) + ": layer out of range");
@@ -886,32 +893,27 @@ constexpr int kStaticDevices = 64;
 
 __device__ __align__(256) char scratch[kStaticScratchBytes];
 
-struct StaticScratch {
-  std::once_flag once;
-  char* ptr = nullptr;  // device address of `scratch` on this device
-  std::string error;
-};
-StaticScratch g_static[kStaticDevices];
+std::mutex g_static_mu;
+char* g_static[kStaticDevices] = {};  // device address of `scratch` per device
 
-// The device address of this device's `scratch`, looked up once per device
-// with that device current.
+// The device address of this device's `scratch`, looked up with that device
+// current on the first call that succeeds (a failed lookup is not kept: the
+// next call tries again).
 int static_scratch(char** out) {
   int dev = 0;
   TGE_HIP(hipGetDevice(&dev));
   if (dev < 0 || dev >= kStaticDevices)
     return fail(TGE_ERR_DEVICE, "decode_attention_static: device index beyond the table");
-  StaticScratch& s = g_static[dev];
-  std::call_once(s.once, [&s] {
+  std::lock_guard<std::mutex> lock(g_static_mu);
+  if (!g_static[dev]) {
     void* p = nullptr;
     const hipError_t e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
-    if (e == hipSuccess && p) {
-      s.ptr = static_cast<char*>(p);
-    } else {
-      s.error = std::string("hipGetSymbolAddress(scratch): ") + hipGetErrorString(e);
-    }
-  });
-  if (!s.ptr) return fail(TGE_ERR_DEVICE, s.error);
-  *out = s.ptr;
+    if (e != hipSuccess || !p)
+      return fail(TGE_ERR_DEVICE, std::string("hipGetSymbolAddress(scratch): ") +
+                                      hipGetErrorString(e));
+    g_static[dev] = static_cast<char*>(p);
+  }
+  *out = g_static[dev];
   return TGE_OK;
 }
 
@@ -926,6 +928,16 @@ int tge_decode_attention_static(const tge_batch_desc* d, const tge_kv_pool* p, i
     return fail(TGE_ERR_INVALID, "decode_attention_static: layer out of range");
   int s = backend_ready();
   if (s != TGE_OK) return fail(s, "decode_attention_static: backend unavailable");
+  {
+    // The plan is copied from host memory at each call: a captured copy
+    // would replay whatever the buffer holds later, so capture is refused.
+    hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
+    TGE_HIP(hipStreamIsCapturing(static_cast<hipStream_t>(stream), &cs));
+    if (cs != hipStreamCaptureStatusNone)
+      return fail(TGE_ERR_INVALID,
+                  "decode_attention_static: the stream is capturing (the plan is uploaded from "
+                  "host memory at each call, which a graph would replay stale)");
+  }
   // Host-side plan in per-thread buffers that keep their capacity.
   thread_local tge::plan::Step step;
   thread_local tge::plan::AttnLists lists;
@@ -1032,6 +1044,8 @@ int tge_attention_group(const tge_attention_group_args* a, void* stream) {
     return fail(TGE_ERR_INVALID, "attention_group: null pointer");
   if (a->first < 0 || a->count < 0)
     return fail(TGE_ERR_INVALID, "attention_group: first and count must be >= 0");
+  if (a->first > INT_MAX - a->count)
+    return fail(TGE_ERR_INVALID, "attention_group: first + count overflows int");
   if (a->group_heads < 1 || a->group_heads > tge::kPrefillRows)
     return fail(TGE_ERR_INVALID, "attention_group: group_heads must be 1..128");
   int s = backend_ready();
@@ -1088,6 +1102,42 @@ int tge_kv_gather(const tge_batch* b, const tge_kv_pool* p, int layer, int sessi
   g.k_scales = i8 ? k_scales : nullptr;
   g.v_scales = i8 ? v_scales : nullptr;
   TGE_HIP(tge::launch_kv_gather(p->desc.format, g, static_cast<hipStream_t>(stream)));
+  return TGE_OK;
+}
+
+int tge_wait_expiries(unsigned int* count) {
+  if (!count) return fail(TGE_ERR_INVALID, "wait_expiries: null argument");
+  int s = backend_ready();
+  if (s != TGE_OK) return fail(s, "wait_expiries: backend unavailable");
+  unsigned int n = 0;
+  TGE_HIP(tge::read_wait_expiries(&n));
+  *count = n;
+  return TGE_OK;
+}
+
+int tge_read_ceiling(const void* buf, size_t bytes, int pattern, int workgroups_per_cu,
+                     int block_bytes, void* stream) {
+  if (!buf) return fail(TGE_ERR_INVALID, "read_ceiling: null buffer");
+  if (workgroups_per_cu < 1 || workgroups_per_cu > 64)
+    return fail(TGE_ERR_INVALID, "read_ceiling: workgroups_per_cu must be 1..64");
+  if (pattern == TGE_READ_STREAM) {
+    if (bytes < 4096 || bytes % 4096 != 0)
+      return fail(TGE_ERR_INVALID, "read_ceiling: stream bytes must be a positive multiple of 4096");
+  } else if (pattern == TGE_READ_BLOCKS) {
+    if (block_bytes < 16 || block_bytes > 17 * 1024 || block_bytes % 16 != 0)
+      return fail(TGE_ERR_INVALID, "read_ceiling: block_bytes must be a multiple of 16 in 16..17408");
+    if (bytes < (size_t)block_bytes || bytes / (size_t)block_bytes > 0x7fffffffu)
+      return fail(TGE_ERR_INVALID, "read_ceiling: 1..2^31-1 blocks");
+  } else {
+    return fail(TGE_ERR_INVALID, "read_ceiling: unknown pattern");
+  }
+  int s = backend_ready();
+  if (s != TGE_OK) return fail(s, "read_ceiling: backend unavailable");
+  int dev = 0, cus = 0;
+  TGE_HIP(hipGetDevice(&dev));
+  TGE_HIP(hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev));
+  TGE_HIP(tge::launch_read_ceiling(buf, bytes, pattern, cus * workgroups_per_cu, block_bytes,
+                                   static_cast<hipStream_t>(stream)));
   return TGE_OK;
 }
 

@@ -155,5 +155,12 @@ hipError_t launch_prefill(int format, int scale_f32, int head_dim, int n_units, 
 int decode_blocks_per_cu(int format, int scale_f32, int head_dim, int row_groups, bool sparse);
 hipError_t launch_reduce(int head_dim, int n_items, int max_parts, const ReduceParams& p,
                          hipStream_t stream);
+// Expiries of the kernels' bounded waits since the process started (a
+// synchronous read of the device counter).
+hipError_t read_wait_expiries(unsigned int* out);
+// Read-only streaming of `bytes` (pattern 0: 4 KiB chunks over the grid;
+// 1: scattered blocks of block_bytes <= 17 KiB, one wave each).
+hipError_t launch_read_ceiling(const void* buf, size_t bytes, int pattern, int workgroups,
+                               int block_bytes, hipStream_t stream);
 
 }  // namespace tge

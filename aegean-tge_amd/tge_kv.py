@@ -160,6 +160,8 @@ SIGNATURES = [
     ("tge_qwen2_kv_remember_prefix", _I, [_VP, _I, _PI, _I]),
     ("tge_qwen2_kv_shared_prefix_len", _I, [_VP, _PI, _I]),
     ("tge_qwen2_kv_attach_prefix", _I, [_VP, _I, _PI, _I]),
+    ("tge_read_ceiling", _I, [_VP, C.c_size_t, _I, _I, _I, _VP]),
+    ("tge_wait_expiries", _I, [C.POINTER(C.c_uint)]),
 ]
 
 
@@ -482,6 +484,13 @@ def batch_desc(sessions, q_heads):
         offs.append(len(ids))
     keep = (_ints(ctx), _ints(n_new), _ints(offs), _ints(ids))
     return BatchDesc(len(sessions), keep[0], keep[1], keep[2], keep[3], q_heads), keep
+
+
+def wait_expiries():
+    """tge_wait_expiries: bounded in-kernel waits that ran out so far."""
+    n = C.c_uint()
+    check(lib().tge_wait_expiries(C.byref(n)), "wait_expiries")
+    return n.value
 
 
 def decode_attention_static(pool, sessions, q_heads, layer, q, out, stream=None):

@@ -119,6 +119,8 @@ def parse():
                     help="run one config key (c1..c5, prefix, mixed, d256, p256) and print it")
     ap.add_argument("--calibrate-copy", action="store_true",
                     help="only time 1 GiB device-to-device copies (counter calibration)")
+    ap.add_argument("--read-ceiling", action="store_true",
+                    help="only run the HBM read-ceiling sweep (tge_read_ceiling) and print it")
     ap.add_argument("--fragment-c5", action="store_true",
                     help="shuffle the c5 pool's free list before the sessions fill it")
     return ap.parse_args()
@@ -825,6 +827,44 @@ def copy_peak(nbytes=1 << 30, reps=5):
     return 2 * nbytes / (best * 1e-3) / 1e9
 
 
+def read_peak(nbytes=4 << 30, block_bytes=4352, reps=3):
+    """HBM read ceiling of this GPU by hand-written read-only kernels
+    (tge_read_ceiling): every byte of a 4 GiB buffer read once per launch
+    (16x the 256 MB last-level cache), swept over workgroups per CU, best of
+    `reps` launches per shape, timed with HIP events on the launch stream.
+    "stream": 4 KiB chunks over the grid, 16 B per lane; "blocks": scattered
+    page blocks of `block_bytes` (the c5 pool's 4352 B), one wave per block,
+    the decode kernel's access shape."""
+    import tge_kv as tk
+    hip = tk.hip()
+    lib = tk.lib()
+    buf = hip.malloc(nbytes)
+    hip.memset(buf, 1, nbytes)
+    hip.sync()
+    e0, e1 = hip.event(), hip.event()
+    out = {"bytes": nbytes, "reps": reps, "kernel": "tge_read_ceiling (read_ceiling.hip)"}
+    for name, pattern, sweep in (("stream", 0, (1, 2, 3, 4, 6, 8)), ("blocks", 1, (1, 2, 3, 4, 6, 8))):
+        size = nbytes if pattern == 0 else (nbytes // block_bytes) * block_bytes
+        best = {}
+        for wpc in sweep:
+            ms_best = None
+            for _ in range(reps + 1):  # (the first launch warms up)
+                hip.record(e0)
+                tk.check(lib.tge_read_ceiling(buf, size, pattern, wpc, block_bytes, None), "read_ceiling")
+                hip.record(e1)
+                ms = hip.elapsed_ms(e0, e1)
+                ms_best = ms if ms_best is None else min(ms_best, ms)
+            best[wpc] = size / (ms_best * 1e-3) / 1e9
+        top = max(best, key=best.get)
+        out[name] = {"gbs": round(best[top], 1), "workgroups_per_cu": top,
+                     "waves_per_cu": 4 * top,
+                     "sweep_gbs": {str(k): round(v, 1) for k, v in best.items()}}
+        if pattern == 1:
+            out[name]["block_bytes"] = block_bytes
+    hip.free(buf)
+    return out
+
+
 def calibrate_copy(nbytes=1 << 30, reps=3):
     """Device-to-device copies of a known size: the reference point that
     scales FETCH_SIZE / WRITE_SIZE readings to bytes (run under rocprofv3)."""
@@ -851,6 +891,11 @@ def main():
     args = parse()
     if args.calibrate_copy:
         calibrate_copy()
+        return
+    if args.read_ceiling:
+        import tge_kv as tk
+        tk.require_gpu()
+        print(json.dumps(read_peak()), flush=True)
         return
     if args.gpus != 1:
         print(f"bench.py runs on one GPU only: this build measures the single-GPU hot path "
@@ -898,6 +943,8 @@ def main():
         return
     copy_gbs = copy_peak()
     log(f"[bench] device-to-device copy: {copy_gbs:.0f} GB/s read + write")
+    ceiling = read_peak()
+    log(f"[bench] read ceiling: {json.dumps(ceiling)}")
     if args.others and not args.only and not args.fragment_c5:
         # c5 on a fragmented pool (free list shuffled before the sessions
         # allocate, so no session's pages are adjacent), a shorter run
@@ -971,6 +1018,11 @@ def main():
             "algorithmic_bytes": r["attn_bytes_per_launch"],
             "measured_copy_peak": round(copy_gbs, 1),
             "frac_of_measured_copy_peak": round(r["attn_kernel_gbs"] / copy_gbs, 4),
+            "measured_read_peak": ceiling["stream"]["gbs"],
+            "frac_of_measured_read_peak": round(r["attn_kernel_gbs"] / ceiling["stream"]["gbs"], 4),
+            "measured_block_read_peak": ceiling["blocks"]["gbs"],
+            "frac_of_measured_block_read_peak": round(r["attn_kernel_gbs"] / ceiling["blocks"]["gbs"], 4),
+            "read_ceiling": ceiling,
         },
         "cpu_baseline": cpu,
         "configs": others,

@@ -259,9 +259,12 @@ int tge_decode_step(const tge_batch* batch, tge_kv_pool* pool, int layer, const 
 int tge_batch_step_info(const tge_batch* batch, int* workgroups, int* max_pieces);
 
 /*
- * tge_decode_attention for callers that cannot allocate memory (code under
- * HIP graph capture, tight serving loops, harnesses that forbid hipMalloc).
- * No counterpart in the reference. It plans the step from `desc` on the
+ * tge_decode_attention for callers that cannot allocate memory (tight
+ * serving loops, harnesses that forbid hipMalloc). No counterpart in the
+ * reference. Not for stream capture: the plan is built on the host and
+ * copied from host memory at each call, so a captured copy would replay
+ * stale contents; a call on a stream that is capturing returns
+ * TGE_ERR_INVALID before anything is enqueued. It plans the step from `desc` on the
  * host (the decode plan of tge_batch_plan; dense attention, no sparse
  * subset) and runs the same kernels, so its output equals that of
  * tge_batch_plan + tge_decode_attention on the same description bit for
@@ -523,6 +526,33 @@ int tge_qwen2_kv_attach_prefix(tge_qwen2_kv* model, int sequence,
  * Lets a caller pre-shape the free list before the first step; pages held by
  * sequences must not be released through it. */
 tge_block_table* tge_qwen2_kv_table(tge_qwen2_kv* model);
+
+/*
+ * Health check, with no counterpart in the reference: the number of bounded
+ * in-kernel waits that ran out since the process started (the block-prefill
+ * kernel's tile barrier between its two halves of waves, bounded at about
+ * 0.2 s so that a launch can never hang). Non-zero means some launch
+ * finished with wrong rows. Synchronous (waits for the device counter).
+ */
+int tge_wait_expiries(unsigned int* count);
+
+/* ---------------------------------------------------------------------------
+ * Measurement helper, with no counterpart in the reference: the HBM read
+ * ceiling of this GPU, beside the 8 TB/s specification. One launch reads
+ * every byte of the device buffer `buf` once and writes nothing:
+ *   TGE_READ_STREAM  4 KiB chunks dealt round-robin to the workgroups
+ *                    (256 threads, `workgroups_per_cu` per compute unit,
+ *                    1..64), 16 B per lane, eight chunks in flight per
+ *                    workgroup (bytes: a multiple of 4096);
+ *   TGE_READ_BLOCKS  bytes / block_bytes blocks of `block_bytes` (16..17408,
+ *                    a multiple of 16; a pool's page-block size), one wave
+ *                    per block, in a scattered order, two blocks in flight
+ *                    per wave (the decode kernel's access shape).
+ * The caller times the launch (e.g. events on `stream`).
+ */
+enum tge_read_pattern { TGE_READ_STREAM = 0, TGE_READ_BLOCKS = 1 };
+int tge_read_ceiling(const void* buf, size_t bytes, int pattern, int workgroups_per_cu,
+                     int block_bytes, void* stream);
 
 #ifdef __cplusplus
 }

@@ -6,6 +6,11 @@ import numpy as np
 ATOL = 2e-3
 RTOL = 1e-3
 
+# Worst error-to-bound ratio per full-size check, printed at the end of the
+# session (conftest.pytest_terminal_summary): name -> (outputs, max abs err,
+# max err / bound).
+MARGINS = {}
+
 
 def make_values(count, seed):
     """The reference tests' input generator (test_attention.cpp:12-21): a

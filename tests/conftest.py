@@ -21,6 +21,17 @@ def pytest_configure(config):
     config.addinivalue_line("markers", "gpu: needs a gfx950 GPU (MI355X)")
 
 
+def pytest_terminal_summary(terminalreporter, exitstatus, config):
+    """One line per full-size parity check that ran: its outputs, worst
+    absolute error and worst ratio of error to the bound (2e-3 + 1e-3|ref|),
+    so the margins appear in the tail of a quiet run."""
+    from _util import MARGINS
+    if MARGINS:
+        terminalreporter.write_line(
+            "parity margins (outputs, max abs err, max err/bound): " +
+            "; ".join(f"{k} {n} {e:.2e} {r:.3f}" for k, (n, e, r) in MARGINS.items()))
+
+
 @pytest.fixture(scope="session")
 def tk():
     import tge_kv

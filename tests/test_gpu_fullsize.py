@@ -29,7 +29,7 @@ import pytest
 import oracle as O
 import synth
 import tge_kv as tk
-from _util import ATOL, RTOL, bits
+from _util import ATOL, MARGINS, RTOL, bits
 
 pytestmark = pytest.mark.gpu
 
@@ -63,6 +63,7 @@ class Margin:
     def report(self):
         say(f"  {self.name}: {self.checked} outputs, max abs err {self.err:.3e}, "
             f"max err/bound {self.ratio:.3f}")
+        MARGINS[self.name] = (self.checked, self.err, self.ratio)
 
 
 def flat_cache(fmt, k, v):
@@ -153,9 +154,13 @@ class Serving:
         dv = tk.DeviceArray.from_numpy(np.concatenate([v[c:c + n] for v, c in zip(self.v, self.ctx)]))
         dq = tk.DeviceArray.from_numpy(q)
         out = tk.DeviceArray(q.shape, np.float32).zero()
-        b.append(self.pool, 0, dk, dv)
-        getattr(b, kind)(self.pool, 0, dq, out)
+        if kind == "step":  # tge_decode_step: append + attention in one call
+            b.decode_step(self.pool, 0, dq, dk, dv, out)
+        else:
+            b.append(self.pool, 0, dk, dv)
+            getattr(b, kind)(self.pool, 0, dq, out)
         tk.hip().sync()
+        self.last_step_info = b.step_info()
         got = out.numpy()
         sh = self.sh
         wants = oracle_outputs(self.fc, q, self.ctx, n, sh)
@@ -223,6 +228,30 @@ def test_c3_full_size(gpu):
     sv.close()
 
 
+@pytest.mark.parametrize("name", ["c1", "c2", "c3"])
+def test_small_step_kernel_full_run(gpu, name):
+    """C1-C3 through tge_decode_step, the path the driver's layer call and
+    the bench time for these configurations: one kernel per layer-step
+    (paged_step_kernel) that stores the step's rows, attends and merges its
+    split contexts in the launch, re-arming its arrival counters for the
+    next step. Every step of the configuration's whole run is checked
+    against the oracle and the pool holds every stored row bit for bit at
+    the end."""
+    cfg = synth.configs()[name]
+    say(f"{name} full run through the one-kernel step")
+    seed = {"c1": 111, "c2": 112, "c3": 113}[name]
+    pool_pages = 128 if name == "c1" else cfg.pool_pages
+    table_seed = None if name == "c2" else cfg.seed
+    sv = Serving(cfg, cfg.contexts, cfg.steps, 1, pool_pages, table_seed=table_seed, seed=seed)
+    sv.fill()
+    m = Margin(f"{name}_step")
+    for i in range(cfg.steps):
+        sv.step(m, kind="step", check_store=(i == cfg.steps - 1))
+        assert sv.last_step_info[0] > 0, f"step {i} did not run as one kernel: {sv.last_step_info}"
+    m.report()
+    sv.close()
+
+
 def test_c4_full_size(gpu):
     """C4: a 2048-token prompt (bf16-representable inputs) in four causal
     chunks of 512; each chunk is appended, then block-attended over every
@@ -257,6 +286,7 @@ def test_c4_full_size(gpu):
             a.close()
         b.close()
     m.report()
+    assert tk.wait_expiries() == 0, "a bounded in-kernel wait ran out"
     pool.close()
     table.close()
 

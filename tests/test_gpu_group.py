@@ -97,4 +97,8 @@ def test_attention_group_empty_chunk_and_bad_page(gpu):
     with pytest.raises(tk.TgeError) as e:
         tk.attention_group(case.pool, 0, 2, case.pages[0], 0, 40, q)  # kv_head 2 of 2
     assert e.value.status == tk.ERR_INVALID
+    with pytest.raises(tk.TgeError) as e:  # first + count past INT_MAX
+        tk.attention_group(case.pool, 0, 0, case.pages[0], 2**31 - 10, 20, q)
+    assert e.value.status == tk.ERR_INVALID
+    assert "overflow" in tk.lib().tge_last_error().decode()
     case.close()

@@ -419,6 +419,7 @@ def test_prefill_tile_widths(gpu, name):
     got, b = case.step(kind="prefill")
     err = assert_attention_close(got, case.oracle_out(), f"prefill tiles {name}")
     say(f"  max abs err {err:.2e}")
+    assert tk.wait_expiries() == 0, "a bounded in-kernel wait ran out"
     b.close()
     check_contents(case)
     case.close()

@@ -129,3 +129,34 @@ def test_step_large_falls_back(gpu):
     b.close()
     check_contents(case)
     case.close()
+
+
+def test_batch_planned_for_another_format_is_refused(gpu):
+    """A batch planned on an int8 pool and used on an f16 pool of the same
+    shape (or with the other scale format) is refused: the one-launch step's
+    page batches depend on the storage format."""
+    say("step: batch planned for another format")
+    qh, kvh, hd = 14, 2, 64
+    p_i8 = tk.KvPool(1, 8, kvh, hd, tk.KV_I8, tk.SCALE_F16)
+    p_i8f32 = tk.KvPool(1, 8, kvh, hd, tk.KV_I8, tk.SCALE_F32)
+    p_f16 = tk.KvPool(1, 8, kvh, hd, tk.KV_F16)
+    q = tk.DeviceArray((1, qh * hd), np.float32).zero()
+    k = tk.DeviceArray((1, kvh * hd), np.float32).zero()
+    v = tk.DeviceArray((1, kvh * hd), np.float32).zero()
+    out = tk.DeviceArray((1, qh * hd), np.float32).zero()
+    b = tk.Batch().plan(p_i8, [tk.Session(40, 1, [0, 1, 2])], qh)
+    L = tk.lib()
+    for other in (p_f16, p_i8f32):
+        st = L.tge_decode_step(b.h, other.h, 0, q.ptr, k.ptr, v.ptr, out.ptr, None)
+        assert st == tk.ERR_INVALID, st
+        assert "another pool" in L.tge_last_error().decode()
+        assert L.tge_kv_append(b.h, other.h, 0, k.ptr, v.ptr, None) == tk.ERR_INVALID
+    # the pool it was planned for still works
+    assert L.tge_decode_step(b.h, p_i8.h, 0, q.ptr, k.ptr, v.ptr, out.ptr, None) == tk.OK
+    tk.hip().sync()
+    assert np.all(np.isfinite(out.numpy()))
+    b.close()
+    for a in (q, k, v, out):
+        a.close()
+    for pl in (p_i8, p_i8f32, p_f16):
+        pl.close()

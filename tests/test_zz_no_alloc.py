@@ -5,8 +5,11 @@ Two calls in a row, the second on a smaller step, must each equal the
 allocating entry point bit for bit (same plan, same kernels), and match the
 oracle within the attention tolerance. A step whose plan exceeds the static
 array is refused with TGE_ERR_CAPACITY before anything runs, and a later
-call still works.
+call still works. A call on a stream that is capturing a graph is refused
+with TGE_ERR_INVALID (its plan is uploaded from host memory at each call,
+which a captured graph would replay stale), with nothing captured.
 """
+import ctypes as C
 import sys
 
 import numpy as np
@@ -93,6 +96,43 @@ def test_static_decode_rejects_oversized_plans(gpu):
     tk.decode_attention_static(pool, [tk.Session(20, 1, [1, 2])], 14, 0, q, out)
     tk.hip().sync()
     assert np.all(np.isfinite(out.numpy()))
+    for a in (q, out):
+        a.close()
+    pool.close()
+
+
+def test_static_decode_refuses_a_capturing_stream(gpu):
+    say("static decode: call on a capturing stream")
+    hip = tk.hip()
+    h = hip.h
+    h.hipStreamBeginCapture.argtypes = [C.c_void_p, C.c_int]
+    h.hipStreamEndCapture.argtypes = [C.c_void_p, C.POINTER(C.c_void_p)]
+    h.hipGraphDestroy.argtypes = [C.c_void_p]
+    h.hipStreamSynchronize.argtypes = [C.c_void_p]
+    st = C.c_void_p()
+    hip.ok(h.hipStreamCreate(C.byref(st)), "hipStreamCreate")
+    pool = tk.KvPool(1, 4, 2, 64, tk.KV_F16)
+    q = tk.DeviceArray((1, 14 * 64), np.float32).zero()
+    out = tk.DeviceArray((1, 14 * 64), np.float32).zero()
+    hip.sync()
+    hip.ok(h.hipStreamBeginCapture(st, 2), "hipStreamBeginCapture")  # relaxed mode
+    err = None
+    try:
+        tk.decode_attention_static(pool, [tk.Session(20, 1, [1, 2])], 14, 0, q, out, stream=st.value)
+    except tk.TgeError as e:
+        err = e
+    finally:
+        graph = C.c_void_p()
+        hip.ok(h.hipStreamEndCapture(st, C.byref(graph)), "hipStreamEndCapture")
+        if graph.value:
+            h.hipGraphDestroy(graph)
+    assert err is not None and err.status == tk.ERR_INVALID, err
+    assert "capturing" in tk.lib().tge_last_error().decode()
+    # the same stream decodes normally once the capture has ended
+    tk.decode_attention_static(pool, [tk.Session(20, 1, [1, 2])], 14, 0, q, out, stream=st.value)
+    hip.ok(h.hipStreamSynchronize(st), "hipStreamSynchronize")
+    assert np.all(np.isfinite(out.numpy()))
+    h.hipStreamDestroy(st)
     for a in (q, out):
         a.close()
     pool.close()
