@@ -154,7 +154,6 @@ struct StepPlan {
     image.release(g_mem);
     part_o.release(g_mem);
     part_ml.release(g_mem);
-    counters.release(g_mem);
   }
 };
 
@@ -188,6 +187,7 @@ struct tge_batch {
   // and after the merge. Triples are created on demand and reused.
   bool profiling = false;
   std::vector<std::array<hipEvent_t, 3>> prof;
+  std::vector<char> prof_merged;  // whether the call launched the split merge kernel
   size_t prof_used = 0;
 
   ~tge_batch() {
@@ -548,7 +548,7 @@ int tge_batch_kernel_times(const tge_batch* b, int* calls, float* attention_us,
     TGE_HIP(hipEventSynchronize(t[2]));
     float x = 0.0f, y = 0.0f;
     TGE_HIP(hipEventElapsedTime(&x, t[0], t[1]));
-    TGE_HIP(hipEventElapsedTime(&y, t[1], t[2]));
+    if (b->prof_merged[i]) TGE_HIP(hipEventElapsedTime(&y, t[1], t[2]));
     att += x;
     mrg += y;
   }
@@ -614,7 +614,9 @@ int profile_events(tge_batch* b, std::array<hipEvent_t, 3>** ev) {
       }
     }
     b->prof.push_back(t);
+    b->prof_merged.push_back(0);
   }
+  b->prof_merged[b->prof_used] = 0;
   *ev = &b->prof[b->prof_used++];
   return TGE_OK;
 }
@@ -627,6 +629,7 @@ int run_attention(const tge_batch* b, const tge_kv_pool* p, int layer, const flo
   const int ps = profile_events(const_cast<tge_batch*>(b), &ev);
   if (ps != TGE_OK) return ps;
   if (ev) TGE_HIP(hipEventRecord((*ev)[0], st));
+  const bool merge_kernel = !pl.lists.reduce.empty();
   if (decode) {
     TGE_HIP(tge::launch_decode(p->desc.format, p->desc.scale_format == TGE_SCALE_F32, b->step.block_dims,
                                pl.lists.row_groups, pl.lists.groups, a, st));
@@ -635,8 +638,11 @@ int run_attention(const tge_batch* b, const tge_kv_pool* p, int layer, const flo
                                 b->step.block_dims, (int)pl.lists.work.size(), pl.lists.tile_rows,
                                 a, st));
   }
-  if (ev) TGE_HIP(hipEventRecord((*ev)[1], st));
-  if (!pl.lists.reduce.empty()) {
+  if (ev) {
+    TGE_HIP(hipEventRecord((*ev)[1], st));
+    const_cast<tge_batch*>(b)->prof_merged[b->prof_used - 1] = merge_kernel;
+  }
+  if (merge_kernel) {
     tge::ReduceParams r{};
     r.items = reinterpret_cast<const tge::ReduceRec*>(pl.image.dev + pl.off_reduce);
     r.part_o = reinterpret_cast<const float*>(pl.part_o.dev);

@@ -190,9 +190,10 @@ int tge_batch_info(const tge_batch* batch, int* rows, int* work_items,
  * on its stream before the paged attention kernel, between it and the split
  * merge kernel, and after the merge. tge_batch_kernel_times waits for every
  * recorded call and returns their number and the summed durations in
- * microseconds (a call without splits adds only the gap between its two
- * events to merge_us). Calls issued back to back keep the launch latency of
- * the host out of the bracketed intervals. */
+ * microseconds; merge_us sums only the calls that launched the split merge
+ * kernel (a call whose plan has no split pieces adds nothing to it). Calls
+ * issued back to back keep the launch latency of the host out of the
+ * bracketed intervals. */
 int tge_batch_set_profiling(tge_batch* batch, int enable);
 
 /* Static sparse attention for the batch's attention calls (SparseConfig,
