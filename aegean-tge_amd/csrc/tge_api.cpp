@@ -154,6 +154,7 @@ struct StepPlan {
     image.release(g_mem);
     part_o.release(g_mem);
     part_ml.release(g_mem);
+    counters.release(g_mem);
   }
 };
 
