@@ -186,6 +186,49 @@ __device__ __forceinline__ void read_page(PageRegs<FMT, SF32, D>& r, const char*
   read_half<FMT, SF32, D, true>(r, slot, lane, grp);
 }
 
+typedef const __attribute__((address_space(4))) WorkRec sconst_work;
+
+// A work record read through the scalar cache.
+__device__ __forceinline__ WorkRec load_work(const sconst_work* w) {
+  const sconst_int* q = (const sconst_int*)w;
+  WorkRec r;
+  r.session = q[0];
+  r.kv_head = q[1];
+  r.page_begin = q[2];
+  r.page_end = q[3];
+  r.part = q[4];
+  r.row_begin = q[5];
+  r.rows = q[6];
+  r.rows_per_query = q[7];
+  r.head_base = q[8];
+  r.ctx = q[9];
+  r.q_row = q[10];
+  r.table_off = q[11];
+  r.red = q[12];
+  return r;
+}
+
+// Barrier of a group of a workgroup's waves through an LDS counter: this
+// wave's LDS reads are complete, it counts in, and waits until `target`
+// arrivals have been counted in total. The wait is bounded (about 0.2 s):
+// past the bound the wave goes on (the launch completes with wrong rows
+// instead of hanging) and the expiry is counted in *expired.
+__device__ __forceinline__ void bounded_barrier(int* ctr, int target, unsigned int* expired) {
+  asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+  if ((threadIdx.x & 63) == 0) __hip_atomic_fetch_add(ctr, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+  constexpr int kSpins = 1 << 21;
+  int spin = 0;
+  for (; spin < kSpins; ++spin) {
+    const int seen = __builtin_amdgcn_readfirstlane(
+        __hip_atomic_load(ctr, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP));
+    if (seen >= target) break;
+    __builtin_amdgcn_s_sleep(1);
+  }
+  if (spin == kSpins && (threadIdx.x & 63) == 0)
+    __hip_atomic_fetch_add(expired, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  __atomic_signal_fence(__ATOMIC_SEQ_CST);
+}
+
 // s_waitcnt vmcnt(n) (other counters untouched), n <= 63.
 template <int N>
 __device__ __forceinline__ void wait_vmcnt() {

@@ -134,8 +134,6 @@ struct DecodeShared {
   int flag;  // arrival broadcast of the in-kernel split merge
 };
 
-typedef const __attribute__((address_space(4))) WorkRec sconst_work;
-
 // Wait for this wave's outstanding LDS and scalar-memory operations; a
 // compiler barrier for memory accesses.
 __device__ __forceinline__ void lgkm_wait_all() {
@@ -151,25 +149,6 @@ __device__ __forceinline__ void lds_barrier() {
   asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
 }
 
-// A work record read through the scalar cache.
-__device__ __forceinline__ WorkRec load_work(const sconst_work* w) {
-  const sconst_int* q = (const sconst_int*)w;
-  WorkRec r;
-  r.session = q[0];
-  r.kv_head = q[1];
-  r.page_begin = q[2];
-  r.page_end = q[3];
-  r.part = q[4];
-  r.row_begin = q[5];
-  r.rows = q[6];
-  r.rows_per_query = q[7];
-  r.head_base = q[8];
-  r.ctx = q[9];
-  r.q_row = q[10];
-  r.table_off = q[11];
-  r.red = q[12];
-  return r;
-}
 
 // Share indices of the pages in a wave's ring, oldest first (a FIFO of at
 // most N wave-uniform values; the constant-index loops keep it in scalar
@@ -642,19 +621,7 @@ constexpr int halves_for_wpe() {
 // launch completes with wrong rows instead of hanging, and the expiry is
 // counted in g_wait_expired (tge_wait_expiries reads it).
 __device__ __forceinline__ void half_barrier(int* ctr, int target) {
-  asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
-  if ((threadIdx.x & 63) == 0) __hip_atomic_fetch_add(ctr, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
-  constexpr int kSpins = 1 << 21;
-  int spin = 0;
-  for (; spin < kSpins; ++spin) {
-    const int seen = __builtin_amdgcn_readfirstlane(
-        __hip_atomic_load(ctr, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP));
-    if (seen >= target) break;
-    __builtin_amdgcn_s_sleep(1);
-  }
-  if (spin == kSpins && (threadIdx.x & 63) == 0)
-    __hip_atomic_fetch_add(&g_wait_expired, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-  __atomic_signal_fence(__ATOMIC_SEQ_CST);
+  bounded_barrier(ctr, target, &g_wait_expired);
 }
 
 // MERGE: split tiles are merged in the launch (the mixed-step kernel).
