@@ -76,7 +76,9 @@ def test_pool_argument_checks(tk):
                  (1, 4, 1, 272, 1, 0), (1, 4, 1, 512, 1, 0), (1, 4, 1, 0, 1, 0),
                  (1, 4, 1, -16, 1, 0), (1, 4, 1, 80, 2, 0), (1, 4, 1, 48, 2, 1),
                  (1, 4, 1, 240, 2, 0), (1, 4, 1, 64, 7, 0), (1, 4, 1, 64, 2, 9),
-                 (1, -1, 1, 64, 1, 0)]:
+                 (1, -1, 1, 64, 1, 0),
+                 # no f32 tier: any format code but f16 (1) and int8 (2)
+                 (1, 4, 1, 64, 0, 0), (1, 4, 1, 64, 3, 0)]:
         d = tk.PoolDesc(*desc)
         assert tk.lib().tge_kv_pool_create(C.byref(d), C.byref(h)) == tk.ERR_INVALID, desc
         assert h.value is None
@@ -319,3 +321,19 @@ def test_attention_group_argument_checks(tk):
     assert L.tge_attention_group(None, None) == tk.ERR_INVALID
     a = tk.AttentionGroupArgs()
     assert L.tge_attention_group(C.byref(a), None) == tk.ERR_INVALID  # no pool
+
+
+def test_measurement_helpers_argument_checks(tk):
+    # tge_read_ceiling and tge_wait_expiries validate before touching a device
+    L = tk.lib()
+    buf = C.c_void_p(0x1000)
+    assert L.tge_read_ceiling(None, 4096, 0, 1, 4352, None) == tk.ERR_INVALID
+    assert L.tge_read_ceiling(buf, 4095, 0, 1, 4352, None) == tk.ERR_INVALID  # not whole chunks
+    assert L.tge_read_ceiling(buf, 4096, 0, 0, 4352, None) == tk.ERR_INVALID  # workgroups per CU
+    assert L.tge_read_ceiling(buf, 4096, 0, 65, 4352, None) == tk.ERR_INVALID
+    assert L.tge_read_ceiling(buf, 1 << 20, 1, 1, 8, None) == tk.ERR_INVALID  # block too small
+    assert L.tge_read_ceiling(buf, 1 << 20, 1, 1, 17424, None) == tk.ERR_INVALID  # block too large
+    assert L.tge_read_ceiling(buf, 1 << 20, 1, 1, 4350, None) == tk.ERR_INVALID  # not 16-byte units
+    assert L.tge_read_ceiling(buf, 100, 1, 1, 4352, None) == tk.ERR_INVALID  # no whole block
+    assert L.tge_read_ceiling(buf, 1 << 20, 2, 1, 4352, None) == tk.ERR_INVALID  # unknown pattern
+    assert L.tge_wait_expiries(None) == tk.ERR_INVALID
