@@ -1028,6 +1028,39 @@ def main():
         "configs": others,
     }
     print(json.dumps(line), flush=True)
+    log(summary_line(line))
+
+
+def summary_line(line):
+    """One compact line with every configuration's headline figures (the
+    tail of the run's stderr): us per layer-step (decode) or per layer-chunk
+    (prefill), tokens/s, fraction of the HBM (decode) or f16 MFMA (prefill)
+    peak, and the CPU baseline beside it."""
+    parts = []
+    cfgs = line.get("configs") or {}
+    for key in ("c1", "c2", "c3"):
+        r = cfgs.get(key)
+        if not r:
+            continue
+        cpu = r.get("cpu_baseline") or {}
+        parts.append(f"{key} {r['us_per_layer_step']:.2f}us/layer-step {r['tokens_per_s']:.0f}tok/s "
+                     f"step-kernel {r['step_launch_us']:.2f}us {r['step_gbs']:.0f}GB/s "
+                     f"frac {r['step_gbs'] / HBM_PEAK_GBS:.3f} "
+                     f"cpu {cpu.get('us_per_layer_step', float('nan')):.0f}us")
+    r = cfgs.get("c4")
+    if r:
+        cpu = r.get("cpu_baseline") or {}
+        parts.append(f"c4 {'/'.join(f'{x:.1f}' for x in r['us_per_layer_chunk'])}us/layer-chunk "
+                     f"{r['tokens_per_s']:.0f}tok/s {r['tflops']:.0f}TF/s mfma {r['mfma_util']:.3f} "
+                     f"(kernel {r['attn_kernel_mfma_util']:.3f}) cpu {cpu.get('value', float('nan')):.2f}TF/s")
+    c = line["config"]
+    cpu = line.get("cpu_baseline") or {}
+    parts.append(f"c5 {c['us_per_layer_step']:.1f}us/layer-step {c['tokens_per_s']:.0f}tok/s "
+                 f"{line['value']:.0f}GB/s step {c['frac_of_hbm_peak']:.3f} kernel "
+                 f"{line['roofline']['frac']:.3f} of 8TB/s, "
+                 f"{line['roofline'].get('frac_of_measured_block_read_peak', float('nan')):.3f} of the "
+                 f"measured block-read ceiling; cpu {cpu.get('value', float('nan')):.2f}GB/s")
+    return "[bench] summary: " + " | ".join(parts)
 
 
 if __name__ == "__main__":
