@@ -11,40 +11,28 @@
 namespace tge {
 namespace {
 
-// Store one lane's 8 values of a 32-value block (dims 32b + 8*quarter ..)
-// of K (which = 0) or V row `rr` of KV head h. f16: each lane converts its 8
-// values with the reference's float_to_half recipe. int8: the four lanes of
-// the block (adjacent, aligned to 4 in the wave) combine their absmax runs
-// in order (see FoldRun), then each computes the block's scale and inverse
-// exactly as quantize_kv_block does (correctly rounded fp32 division) and
-// quantizes its 8 values. Dead lanes (`live` false) take part in the
-// shuffles and store nothing.
-template <int FMT>
-__device__ __forceinline__ void store_lane(const AppendParams& p, const float (&x)[8], const RowRec rr,
-                                           int which, int h, int b, int quarter, bool live) {
-  const int nb = p.head_dim >> 5;
-  char* const blk = static_cast<char*>(p.pool) + ((size_t)rr.page * p.kv_heads + h) * p.geom.block_bytes;
-  const int t = rr.slot;
-  const int d0 = 32 * b + 8 * quarter;  // first dim of this lane
-  // K chunk of (token t, dims d0..d0+3) and (d0+4..d0+7): 4 contiguous
-  // elements each (k_index_np is contiguous in d&3).
-  const int k0 = k_index_np(t, d0, nb);
-  const int k1 = k_index_np(t, d0 + 4, nb);
+// One lane's 8 values of a 32-value block (dims 32b + 8*quarter ..) of a K
+// or V row in stored form: f16, 8 halves (w[0..3], pairs low first); int8,
+// 8 codes (w[0..1], bytes in dim order) and the block's scale.
+struct LaneCodes {
+  uint32_t w[4];
+  float scale;
+};
 
+// Encode one lane's 8 values. f16: each value with the reference's
+// float_to_half recipe. int8: the four lanes of the block (adjacent,
+// aligned to 4 in the wave) combine their absmax runs in order (see
+// FoldRun), then each computes the block's scale and inverse exactly as
+// quantize_kv_block does (correctly rounded fp32 division) and quantizes
+// its 8 values. Every lane of the wave takes part (the shuffles); lanes
+// whose values are not stored still compute.
+template <int FMT>
+__device__ __forceinline__ LaneCodes encode_lane(const float (&x)[8]) {
+  LaneCodes c{{0, 0, 0, 0}, 0.0f};
   if (FMT == kF16) {
-    uint16_t hx[8];
 #pragma unroll
-    for (int i = 0; i < 8; ++i) hx[i] = float_to_half_ref(x[i]);
-    if (!live) return;
-    if (which == 0) {
-      uint16_t* dst = reinterpret_cast<uint16_t*>(blk);
-      *reinterpret_cast<uint2*>(dst + k0) = make_uint2(hx[0] | ((uint32_t)hx[1] << 16), hx[2] | ((uint32_t)hx[3] << 16));
-      *reinterpret_cast<uint2*>(dst + k1) = make_uint2(hx[4] | ((uint32_t)hx[5] << 16), hx[6] | ((uint32_t)hx[7] << 16));
-    } else {
-      uint16_t* dst = reinterpret_cast<uint16_t*>(blk + p.geom.v_off());
-#pragma unroll
-      for (int i = 0; i < 8; ++i) dst[v_index_np(t, d0 + i, nb)] = hx[i];
-    }
+    for (int i = 0; i < 4; ++i)
+      c.w[i] = float_to_half_ref(x[2 * i]) | ((uint32_t)float_to_half_ref(x[2 * i + 1]) << 16);
   } else {
     // the block's absmax: lane runs joined in lane order
     const FoldRun mine = fold_run(x);
@@ -58,34 +46,85 @@ __device__ __forceinline__ void store_lane(const AppendParams& p, const float (&
     const float maximum = all.v;
     const float scale = __fdiv_rn(maximum, 127.0f);
     const float inverse = scale != 0.0f ? __fdiv_rn(1.0f, scale) : 0.0f;
-    uint32_t packed[2] = {0, 0};
 #pragma unroll
     for (int i = 0; i < 8; ++i) {
       const float scaled = __fmul_rn(x[i], inverse);
       const float rounded = scaled >= 0.0f ? __fadd_rn(scaled, 0.5f) : __fadd_rn(scaled, -0.5f);
-      int c = trunc_to_int_x86(rounded);
-      c = c > 127 ? 127 : (c < -127 ? -127 : c);
-      packed[i >> 2] |= (uint32_t)(uint8_t)(int8_t)c << (8 * (i & 3));
+      int q = trunc_to_int_x86(rounded);
+      q = q > 127 ? 127 : (q < -127 ? -127 : q);
+      c.w[i >> 2] |= (uint32_t)(uint8_t)(int8_t)q << (8 * (i & 3));
     }
-    if (!live) return;
-    if (which == 0) {
-      int8_t* dst = reinterpret_cast<int8_t*>(blk);
-      *reinterpret_cast<uint32_t*>(dst + k0) = packed[0];
-      *reinterpret_cast<uint32_t*>(dst + k1) = packed[1];
+    c.scale = scale;
+  }
+  return c;
+}
+
+// Write one lane's encoded values of token slot t into a page block through
+// `put` (byte offset in the block, value, bytes: 1, 2, 4 or 8; a write never
+// crosses a 16-byte boundary): K, two runs of 4 dims (k_index_np is
+// contiguous in d&3); V, 8 single elements; int8, the block's scale from
+// the quarter-0 lane.
+template <int FMT, typename Put>
+__device__ __forceinline__ void write_lane(Put&& put, const BlockGeom& g, int nb, bool scale_f32,
+                                           const LaneCodes& c, int t, int which, int b, int quarter) {
+  const int d0 = 32 * b + 8 * quarter;  // first dim of this lane
+  constexpr int E = FMT == kF16 ? 2 : 1;  // element bytes
+  if (which == 0) {
+    const int k0 = k_index_np(t, d0, nb) * E;
+    const int k1 = k_index_np(t, d0 + 4, nb) * E;
+    if (FMT == kF16) {
+      put(k0, (uint64_t)c.w[0] | ((uint64_t)c.w[1] << 32), 8);
+      put(k1, (uint64_t)c.w[2] | ((uint64_t)c.w[3] << 32), 8);
     } else {
-      int8_t* dst = reinterpret_cast<int8_t*>(blk + p.geom.v_off());
-#pragma unroll
-      for (int i = 0; i < 8; ++i) dst[v_index_np(t, d0 + i, nb)] = (int8_t)(packed[i >> 2] >> (8 * (i & 3)));
+      put(k0, c.w[0], 4);
+      put(k1, c.w[1], 4);
     }
-    if (quarter == 0) {
-      char* sp = blk + (which ? p.geom.vs_off() : p.geom.ks_off());
-      if (p.scale_f32) {
-        reinterpret_cast<float*>(sp)[scale_index_np(t, b, nb)] = scale;
-      } else {
-        reinterpret_cast<uint16_t*>(sp)[scale_index_np(t, b, nb)] = float_to_half_ref(scale);
-      }
+  } else {
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      const int off = g.v_off() + v_index_np(t, d0 + i, nb) * E;
+      if (FMT == kF16)
+        put(off, (c.w[i >> 1] >> (16 * (i & 1))) & 0xffffu, 2);
+      else
+        put(off, (c.w[i >> 2] >> (8 * (i & 3))) & 0xffu, 1);
     }
   }
+  if (FMT != kF16 && quarter == 0) {
+    const int sp = which ? g.vs_off() : g.ks_off();
+    if (scale_f32)
+      put(sp + scale_index_np(t, b, nb) * 4, __float_as_uint(c.scale), 4);
+    else
+      put(sp + scale_index_np(t, b, nb) * 2, float_to_half_ref(c.scale), 2);
+  }
+}
+
+// Stores to global memory at `blk`.
+struct GlobalPut {
+  char* blk;
+  __device__ __forceinline__ void operator()(int off, uint64_t v, int bytes) const {
+    char* d = blk + off;
+    if (bytes == 8)
+      *reinterpret_cast<uint2*>(d) = make_uint2((uint32_t)v, (uint32_t)(v >> 32));
+    else if (bytes == 4)
+      *reinterpret_cast<uint32_t*>(d) = (uint32_t)v;
+    else if (bytes == 2)
+      *reinterpret_cast<uint16_t*>(d) = (uint16_t)v;
+    else
+      *reinterpret_cast<uint8_t*>(d) = (uint8_t)v;
+  }
+};
+
+// Store one lane's 8 values of a 32-value block (dims 32b + 8*quarter ..)
+// of K (which = 0) or V row `rr` of KV head h (encode_lane, then
+// write_lane to the pool). Dead lanes (`live` false) take part in the
+// shuffles and store nothing.
+template <int FMT>
+__device__ __forceinline__ void store_lane(const AppendParams& p, const float (&x)[8], const RowRec rr,
+                                           int which, int h, int b, int quarter, bool live) {
+  const LaneCodes c = encode_lane<FMT>(x);
+  if (!live) return;
+  char* const blk = static_cast<char*>(p.pool) + ((size_t)rr.page * p.kv_heads + h) * p.geom.block_bytes;
+  write_lane<FMT>(GlobalPut{blk}, p.geom, p.head_dim >> 5, p.scale_f32 != 0, c, rr.slot, which, b, quarter);
 }
 
 __device__ __forceinline__ void load8(float (&x)[8], const float* src) {

@@ -37,6 +37,7 @@
 // is bit-reproducible); units of a split context write partial
 // (max, sum, acc) for the reduction kernel.
 
+#include "append_common.h"
 #include "attn_common.h"
 
 namespace tge {
@@ -52,9 +53,10 @@ namespace {
 // workgroups per CU for up to 32 rows per unit), each covering a contiguous
 // share of the plan's page sequence (its work items in order).
 //
-// Within a unit the waves take pages round-robin (wave w: pages w, w+W,
-// ...; with a static sparse subset that skips pages, the unit's kept pages
-// instead). Each wave streams its pages through a private LDS ring of NB
+// Within a unit the waves take pages round-robin (wave w: the unit's pages
+// j with (j + item) mod W = w, item the unit's index in the plan, so the
+// last pages of a share's units spread over the waves; with a static sparse
+// subset that skips pages, the unit's kept pages, from wave 0). Each wave streams its pages through a private LDS ring of NB
 // slots (NB-1 page blocks in flight while it consumes one) and crosses unit
 // boundaries without draining: the next unit's first pages are already in
 // flight while the current unit is merged. The Q^T operands of the share's
@@ -119,6 +121,12 @@ struct DecodeCfg {
   static constexpr int LEFT = LDS - merge_bytes(W) - W * NB * SLOT;
   static constexpr int MAXU = LEFT / QBYTES > 4 ? 4 : LEFT / QBYTES;
   static_assert(NB >= 2 && MAXU >= 1, "decode LDS plan");
+  static_assert((W & (W - 1)) == 0, "the page split takes indices mod W");
+  // The dense variants of up to 128 dims and 32 rows per unit can store a
+  // decode step's new rows (their register budget holds a wave's encoded
+  // rows through the page loop); rows per wave they hold: APP_ROWS.
+  static constexpr bool kApp = !SP && !MIX && !kBig;
+  static constexpr int APP_ROWS = decode_app_rows(D);
   // a merge pass stages 8 rows of D floats (row stride D+4) in one ring slot
   static_assert(8 * (D + 4) * 4 <= SLOT, "merge staging fits a slot");
 };
@@ -171,7 +179,59 @@ struct PageFifo {
   __device__ __forceinline__ int front() const { return t[0]; }
 };
 
-template <int FMT, bool SF32, int D, int NRG, int W, int WPE, bool SP, bool MIX>
+// Where fetch_page lands byte `off` of a page block in the ring slot: the K
+// and V parts in 16-byte pieces interleaved over the lanes (piece i of lane
+// l at i*1024 + l*16), the scales in place. Elements that lie 16 pieces
+// apart in a part (a K row's two runs of 4 dims) land 256 bytes apart, and
+// ones a piece apart (a V column's 8 dims) 16 bytes apart.
+template <int FMT, bool SF32, int D>
+__device__ __forceinline__ int ring_slot_offset(int off) {
+  using RG = Ring<FMT, SF32, D>;
+  static_assert(RG::KV_BYTES == 16 * D * (FMT == kF16 ? 2 : 1), "ring slot holds one block");
+  if (off >= 2 * RG::KV_BYTES) return off;
+  const int part = off >= RG::KV_BYTES ? RG::KV_BYTES : 0;
+  const int g = off - part;
+  return part + ((g >> 4) % RG::PIECES) * 1024 + (g / (16 * RG::PIECES)) * 16 + (g & 15);
+}
+
+// Write one lane's encoded values (write_lane's pieces) into a landed page's
+// ring slot: `offs` from ring_slot_offset (bits 0-15: the K run or first V
+// element, 16 up: the scale), `rest` = the lane's index within its row.
+template <int FMT, bool SF32, int D>
+__device__ __forceinline__ void patch_slot(char* slot, const LaneCodes& c, int offs, int rest, int np) {
+  constexpr int E = FMT == kF16 ? 2 : 1;
+  // the layouts the fixed strides assume (k_index_np, v_index_np; a piece
+  // per lane chunk of 16 * PIECES bytes)
+  static_assert(16 * 8 * (D / 32) * E == 16 * 16 * Ring<FMT, SF32, D>::PIECES, "K runs 16 pieces apart");
+  static_assert(8 * (D / 32) * E == 16 * Ring<FMT, SF32, D>::PIECES, "V dims one piece apart");
+  char* const d = slot + (offs & 0xffff);
+  if ((rest >> 2) / np == 0) {  // K
+    if (FMT == kF16) {
+      *reinterpret_cast<uint2*>(d) = make_uint2(c.w[0], c.w[1]);
+      *reinterpret_cast<uint2*>(d + 256) = make_uint2(c.w[2], c.w[3]);
+    } else {
+      *reinterpret_cast<uint32_t*>(d) = c.w[0];
+      *reinterpret_cast<uint32_t*>(d + 256) = c.w[1];
+    }
+  } else {
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      if (FMT == kF16)
+        *reinterpret_cast<uint16_t*>(d + 16 * i) = (uint16_t)(c.w[i >> 1] >> (16 * (i & 1)));
+      else
+        *reinterpret_cast<uint8_t*>(d + 16 * i) = (uint8_t)(c.w[i >> 2] >> (8 * (i & 3)));
+    }
+  }
+  if (FMT != kF16 && (rest & 3) == 0) {
+    char* const s = slot + (offs >> 16);
+    if (SF32)
+      *reinterpret_cast<uint32_t*>(s) = __float_as_uint(c.scale);
+    else
+      *reinterpret_cast<uint16_t*>(s) = float_to_half_ref(c.scale);
+  }
+}
+
+template <int FMT, bool SF32, int D, int NRG, int W, int WPE, bool SP, bool MIX, bool APP = false>
 __device__ __forceinline__ void decode_body(const AttnParams& p,
                                             DecodeShared<FMT, SF32, D, NRG, SP, MIX>& sh,
                                             const int group) {
@@ -198,6 +258,58 @@ __device__ __forceinline__ void decode_body(const AttnParams& p,
   const int q_stride = p.q_heads * p.dims;
 
   char* ring = sh.ring + wave * NB * RG::SLOT;
+
+  // ---- the step's new K/V rows (APP: the launch of tge_decode_step) --------
+  // Each wave handles the new rows of the pages it reads itself (the plan
+  // lists them per wave, at most APP_ROWS): their values are loaded beside
+  // the Q table and encoded as the append encodes them; when such a page
+  // lands in the ring, the wave writes the rows into the slot before reading
+  // it (the page in memory does not hold them yet); after its last page the
+  // wave stores them into the pool. No other wave or workgroup reads those
+  // pages in this launch. Row r takes RL lanes: four per 32-value block of
+  // the K row, then of the V row (encode_lane's lane order).
+  constexpr bool kApp = APP;
+  static_assert(!APP || CFG::kApp, "a variant that stores new rows");
+  constexpr int RL = 8 * NP;
+  constexpr int RJ = 64 / RL;                         // rows per 64-lane job
+  constexpr int AJ = kApp ? CFG::APP_ROWS / RJ : 1;  // jobs
+  static_assert(CFG::APP_ROWS <= kAppPad && CFG::APP_ROWS % RJ == 0, "app rows");
+  // A job's state through the page loop: the encoded values, the lane's
+  // slot offsets (K: first run, the second 256 bytes on; V: first element,
+  // the next ones 16 bytes apart; bits 16 up: the scale, quarter-0 lanes)
+  // and the row's key (work item << 16 | its page mod 2^16; -1: no row).
+  struct AppJob {
+    LaneCodes c;
+    int offs;
+    int key;
+  };
+  AppJob jobs[AJ];
+#pragma unroll
+  for (int a = 0; a < AJ; ++a) jobs[a].key = -1;
+  int app_n = 0, app_off = 0;  // this wave's rows, its first record
+  int arec[kApp ? CFG::APP_ROWS * kAppRecInts : 1];
+  auto read_recs = [&]() __attribute__((always_inline)) -> void {
+    // (records past the wave's own are the next wave's, or the zero padding
+    // after the last list: never used)
+    const sconst_int* rec = (const sconst_int*)p.app_recs + (size_t)app_off * kAppRecInts;
+#pragma unroll
+    for (int e = 0; e < (kApp ? CFG::APP_ROWS * kAppRecInts : 1); ++e) arec[e] = rec[e];
+  };
+  // record field e of the lane's row in job a
+  auto rec_field = [&](int a, int e) __attribute__((always_inline)) -> int {
+    int v = arec[(a * RJ) * kAppRecInts + e];
+#pragma unroll
+    for (int c = 1; c < RJ; ++c) v = lane / RL == c ? arec[(a * RJ + c) * kAppRecInts + e] : v;
+    return v;
+  };
+  if constexpr (kApp) {
+    // (read at kernel start: the scalar round trips end before the page ids
+    // of the first fetches return)
+    const sconst_int* af = (const sconst_int*)p.app_first + group * W + wave;
+    app_off = af[0];
+    app_n = af[1] - app_off;
+    read_recs();
+  }
 
   // ---- Q^T operands of units [qfirst, qfirst + MAXU) in LDS ----------------
   // Entry (u, rg, pp, l): lane l = 16g + c of row group rg holds row c, dims
@@ -275,9 +387,10 @@ __device__ __forceinline__ void decode_body(const AttnParams& p,
   // ---- issue side: this wave's next page, its block, its fetch -------------
   // Cursor over the share's units: unit `ik` covers share pages
   // [ibase, ibase + its page count); `jn` is this wave's next page in it
-  // (wave w takes the unit's pages w, w+W, ...: a fixed split, so results
-  // are bit-reproducible and independent of where the pages sit).
-  int ik = first, ibase = 0, jn = wave;
+  // (wave w takes the unit's pages j = w - ik, w - ik + W, ... mod W: a
+  // fixed split, so results are bit-reproducible and independent of where
+  // the pages sit).
+  int ik = first, ibase = 0, jn = (wave - first) & (W - 1);
   WorkRec iw = load_work(work + first);
   WorkRec iw_next = load_work(work + (first + 1 < last ? first + 1 : first));
   // Next page to fetch: share index (-1: none), page id and KV head. The id
@@ -343,7 +456,7 @@ __device__ __forceinline__ void decode_body(const AttnParams& p,
         } else {
           ibase += iw.page_end - iw.page_begin;
           ++ik;
-          jn = wave;
+          jn = (wave - ik) & (W - 1);
           iw = iw_next;
           iw_next = load_work(work + (ik + 1 < last ? ik + 1 : ik));
         }
@@ -518,7 +631,38 @@ __device__ __forceinline__ void decode_body(const AttnParams& p,
       }
     }
   }
+  float app_x[AJ][8];
+  if constexpr (kApp) {
+    if (app_n > 0) {
+      const int rest = lane % RL;
+      const int which = (rest >> 2) / NP, b = (rest >> 2) % NP, quarter = rest & 3;
+      const int d0 = 32 * b + 8 * quarter;
+      const float* src = which ? p.app_v : p.app_k;
+      constexpr int E = FMT == kF16 ? 2 : 1;
+      const BlockGeom geom = block_geom(FMT, D, SF32 ? 1 : 0);
+#pragma unroll
+      for (int a = 0; a < AJ; ++a) {
+        const bool live = a * RJ + lane / RL < app_n;
+        const int pos = rec_field(a, 1), kvrow = rec_field(a, 2), item = rec_field(a, 3);
+        const int t = pos & 15;
+        const int run = which ? geom.v_off() + v_index_np(t, d0, NP) * E : k_index_np(t, d0, NP) * E;
+        const int sc = (which ? geom.vs_off() : geom.ks_off()) + scale_index_np(t, b, NP) * (SF32 ? 4 : 2);
+        jobs[a].offs = ring_slot_offset<FMT, SF32, D>(run) | (sc << 16);
+        jobs[a].key = live ? (item << 16) | ((pos >> 4) & 0xffff) : -1;
+#pragma unroll
+        for (int i = 0; i < 8; ++i) app_x[a][i] = 0.0f;  // (dims past the head's own store zeros)
+        if (live && d0 < p.dims) load8(app_x[a], src + (size_t)kvrow * p.dims + d0);
+      }
+    }
+  }
   fill_q_start(qfirst);
+  if constexpr (kApp) {
+    if (app_n > 0) {
+#pragma unroll
+      for (int a = 0; a < AJ; ++a)
+        if (a * RJ < app_n) jobs[a].c = encode_lane<FMT>(app_x[a]);  // (wave-uniform: shuffles)
+    }
+  }
   reset_unit();
   __syncthreads();  // the Q table is written
   // Close every unit that ends before this wave's next page (all of them
@@ -549,6 +693,15 @@ __device__ __forceinline__ void decode_body(const AttnParams& p,
     }
     const int g = fifo.front();
     const int pi = cw.page_begin + (g - cbase);
+    if constexpr (kApp) {
+      if (pi >= (cw.ctx >> 4)) {  // a page with new rows (a lane's key matches: its row)
+        const int key = (ck << 16) | (pi & 0xffff);
+        char* const slot = ring + head * RG::SLOT;
+#pragma unroll
+        for (int a = 0; a < AJ; ++a)
+          if (jobs[a].key == key) patch_slot<FMT, SF32, D>(slot, jobs[a].c, jobs[a].offs, lane % RL, NP);
+      }
+    }
     const half8_t* qt = sh.q + (ck - qfirst) * QUNIT + lane;
     u.template consume_slot<SP>(
         ring + head * RG::SLOT, lane, pi, grp, pi >= unmasked,
@@ -566,13 +719,39 @@ __device__ __forceinline__ void decode_body(const AttnParams& p,
     fifo.pop();
     close_units();  // the slot just read is free
   }
+  if constexpr (kApp) {
+    // the rows into the pool (for the launches after this one); the list
+    // bounds and records are read again (the empty asm keeps the compiler
+    // from holding the first reads' registers through the page loop)
+    int gw = group * W + wave;
+    asm volatile("" : "+s"(gw));
+    const sconst_int* af = (const sconst_int*)p.app_first + gw;
+    app_off = af[0];
+    app_n = af[1] - app_off;
+    if (app_n > 0) {
+      read_recs();
+      const int rest = lane % RL;
+      const BlockGeom geom = block_geom(FMT, D, SF32 ? 1 : 0);
+      char* const pool = static_cast<char*>(const_cast<void*>(p.pool));
+#pragma unroll
+      for (int a = 0; a < AJ; ++a) {
+        const int page = rec_field(a, 0), pos = rec_field(a, 1), kvrow = rec_field(a, 2);
+        if (a * RJ + lane / RL < app_n)
+          write_lane<FMT>(GlobalPut{pool + ((size_t)page * p.kv_heads + kvrow % p.kv_heads) * p.block_bytes},
+                          geom, NP, SF32, jobs[a].c, pos & 15, (rest >> 2) / NP, (rest >> 2) % NP, rest & 3);
+      }
+    }
+  }
 }
 
-template <int FMT, bool SF32, int D, int NRG, int W, int WPE, bool SP>
+
+// APP: the launch also encodes, attends to and stores the step's new rows
+// (p.app_k, tge_decode_step).
+template <int FMT, bool SF32, int D, int NRG, int W, int WPE, bool SP, bool APP = false>
 __global__ __launch_bounds__(64 * W) __attribute__((amdgpu_waves_per_eu(WPE, WPE)))
 void paged_decode_kernel(AttnParams p) {
   __shared__ DecodeShared<FMT, SF32, D, NRG, SP> sh;
-  decode_body<FMT, SF32, D, NRG, W, WPE, SP, false>(p, sh, blockIdx.x);
+  decode_body<FMT, SF32, D, NRG, W, WPE, SP, false, APP>(p, sh, blockIdx.x);
 }
 
 // ---------------------------------------------------------------------------
@@ -1013,12 +1192,20 @@ hipError_t launch_decode_d(int row_groups, int n_groups, const AttnParams& p, hi
     if constexpr (n <= max_row_groups<D>()) {                                               \
       using C = DecodeCfg<FMT, SF32, D, n, false>;                                          \
       using CS = DecodeCfg<FMT, SF32, D, n, true>;                                          \
-      if (p.sp_stride > 0)                                                                  \
+      if (p.sp_stride > 0) {                                                                \
         hipLaunchKernelGGL((paged_decode_kernel<FMT, SF32, D, n, CS::W, CS::WPE, true>),    \
                            dim3((unsigned)n_groups), dim3(64 * CS::W), 0, stream, p);       \
-      else                                                                                  \
+      } else if (p.app_k) {                                                                 \
+        if constexpr (C::kApp)                                                              \
+          hipLaunchKernelGGL((paged_decode_kernel<FMT, SF32, D, n, C::W, C::WPE, false,     \
+                                                  C::kApp>),                                \
+                             dim3((unsigned)n_groups), dim3(64 * C::W), 0, stream, p);      \
+        else                                                                                \
+          return hipErrorInvalidValue;                                                      \
+      } else {                                                                              \
         hipLaunchKernelGGL((paged_decode_kernel<FMT, SF32, D, n, C::W, C::WPE, false>),     \
                            dim3((unsigned)n_groups), dim3(64 * C::W), 0, stream, p);        \
+      }                                                                                     \
       break;                                                                                \
     } else {                                                                                \
       return hipErrorInvalidValue;                                                          \
@@ -1097,6 +1284,28 @@ hipError_t launch_decode(int format, int scale_f32, int head_dim, int row_groups
 int decode_blocks_per_cu(int format, int scale_f32, int head_dim, int row_groups, bool sparse) {
   return with_variant(format, scale_f32, head_dim, 0, [&]<int FMT, bool SF32, int D>() {
     return decode_blocks_d<FMT, SF32, D>(row_groups, sparse);
+  });
+}
+
+template <int FMT, bool SF32, int D, int R>
+constexpr int decode_app_waves_r() {
+  if constexpr (R <= max_row_groups<D>()) {
+    using C = DecodeCfg<FMT, SF32, D, R>;
+    return C::kApp ? C::W : 0;
+  } else {
+    return 0;
+  }
+}
+
+int decode_app_waves(int format, int scale_f32, int head_dim, int row_groups) {
+  return with_variant(format, scale_f32, head_dim, 0, [&]<int FMT, bool SF32, int D>() {
+    switch (row_groups) {
+      case 1: return decode_app_waves_r<FMT, SF32, D, 1>();
+      case 2: return decode_app_waves_r<FMT, SF32, D, 2>();
+      case 3: return decode_app_waves_r<FMT, SF32, D, 3>();
+      case 4: return decode_app_waves_r<FMT, SF32, D, 4>();
+      default: return 0;
+    }
   });
 }
 

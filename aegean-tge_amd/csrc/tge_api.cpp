@@ -133,6 +133,7 @@ struct AttnPlan {
   tge::plan::Staged image;  // work | reduce | wg_first
   size_t off_reduce = 0;
   size_t off_first = 0;
+  size_t off_app = 0;  // app_first, then app_recs (decode plans that store the new rows)
   tge::plan::Scratch part_o;   // [parts][rows_cap][block width] fp32
   tge::plan::Scratch part_ml;  // [parts][rows_cap][2] fp32
   ~AttnPlan() {
@@ -336,9 +337,9 @@ namespace {
 // (rows of the page blocks' width).
 int upload_plan(AttnPlan& pl, int block_dims, hipStream_t st) {
   pl.built = false;
-  const size_t total = tge::plan::image_layout(pl.lists, &pl.off_reduce, &pl.off_first);
+  const size_t total = tge::plan::image_layout(pl.lists, &pl.off_reduce, &pl.off_first, &pl.off_app);
   int s = pl.image.upload(g_mem, total, st, [&](char* h) {
-    tge::plan::write_image(pl.lists, pl.off_reduce, pl.off_first, h);
+    tge::plan::write_image(pl.lists, pl.off_reduce, pl.off_first, h, pl.off_app);
   });
   if (s != TGE_OK) return s;
   const size_t rows_cap = 16 * (size_t)pl.lists.row_groups;
@@ -414,6 +415,12 @@ int build_decode_plan(tge_batch* b, const tge_kv_pool* p, AttnPlan& pl, int only
                           mixed ? resident_groups_mixed(p->desc.format, sf32, b->step.block_dims, rg)
                                 : resident_groups(p->desc.format, sf32, b->step.block_dims, rg, sparse),
                           pl.lists, only);
+  // (the dense decode kernel of tge_decode_step stores the step's new rows
+  // where its variant can)
+  if (!mixed && !sparse)
+    tge::plan::build_decode_appends(b->step, pl.lists,
+                                    tge::decode_app_waves(p->desc.format, sf32, b->step.block_dims, rg),
+                                    tge::decode_app_rows(b->step.block_dims));
   pl.sparse = sparse;
   return upload_plan(pl, b->step.block_dims, st);
 }
@@ -514,6 +521,12 @@ int tge_batch_step_info(const tge_batch* b, int* workgroups, int* max_pieces) {
   const bool one = b->small.built;
   if (workgroups) *workgroups = one ? (int)b->small.lists.recs.size() : 0;
   if (max_pieces) *max_pieces = one ? b->small.lists.max_pieces : 0;
+  return TGE_OK;
+}
+
+int tge_batch_decode_stores_rows(const tge_batch* b, int* stores) {
+  if (!b || !b->planned || !stores) return fail(TGE_ERR_INVALID, "batch_decode_stores_rows: batch not planned");
+  *stores = !b->small.built && b->sp_stride == 0 && b->decode.built && b->decode.lists.app_waves > 0;
   return TGE_OK;
 }
 
@@ -622,10 +635,19 @@ int profile_events(tge_batch* b, std::array<hipEvent_t, 3>** ev) {
   return TGE_OK;
 }
 
+// app_k/app_v (dense decode only): the step's new K/V rows, stored by the
+// decode launch itself (tge_decode_step).
 int run_attention(const tge_batch* b, const tge_kv_pool* p, int layer, const float* q,
-                  float* out, void* stream, const AttnPlan& pl, bool decode) {
+                  float* out, void* stream, const AttnPlan& pl, bool decode,
+                  const float* app_k = nullptr, const float* app_v = nullptr) {
   hipStream_t st = static_cast<hipStream_t>(stream);
-  const tge::AttnParams a = attn_params(b, p, layer, q, out, pl);
+  tge::AttnParams a = attn_params(b, p, layer, q, out, pl);
+  if (app_k) {
+    a.app_k = app_k;
+    a.app_v = app_v;
+    a.app_first = reinterpret_cast<const int*>(pl.image.dev + pl.off_app);
+    a.app_recs = a.app_first + pl.lists.app_first.size();
+  }
   std::array<hipEvent_t, 3>* ev = nullptr;
   const int ps = profile_events(const_cast<tge_batch*>(b), &ev);
   if (ps != TGE_OK) return ps;
@@ -765,12 +787,27 @@ int tge_decode_step(const tge_batch* b, tge_kv_pool* p, int layer, const float* 
   if (!q || !k || !v || !out) return fail(TGE_ERR_INVALID, "decode_step: null q/k/v/out");
   if (!b->decode.built)
     return fail(TGE_ERR_INVALID, "decode_step: n_new * group exceeds a decode unit (64 rows, 48 at head_dim > 128)");
-  if (!b->small.built || b->sp_stride > 0) {
-    // a large step (or a static sparse one): the append, then the decode
-    // kernel and its split merge
+  if (b->sp_stride > 0) {
+    // a static sparse step: the append, then the sparse decode kernel and
+    // its split merge
     s = tge_kv_append(b, p, layer, k, v, stream);
     if (s != TGE_OK) return s;
     return tge_decode_attention(b, p, layer, q, out, stream);
+  }
+  if (!b->small.built) {
+    // a large step: the decode kernel, which writes the new rows into the
+    // pages it reads as they land and stores them into the pool, then its
+    // split merge
+    if (b->decode.sparse) {
+      s = build_decode_plan(const_cast<tge_batch*>(b), p, const_cast<tge_batch*>(b)->decode, 0,
+                            static_cast<hipStream_t>(stream));
+      if (s != TGE_OK) return s;
+    }
+    if (b->decode.lists.app_waves > 0)
+      return run_attention(b, p, layer, q, out, stream, b->decode, true, k, v);
+    s = tge_kv_append(b, p, layer, k, v, stream);  // (no new-row lists: the variant or rows per wave)
+    if (s != TGE_OK) return s;
+    return run_attention(b, p, layer, q, out, stream, b->decode, true);
   }
   const StepPlan& sp = b->small;
   tge_kv_layer_view view{};

@@ -75,6 +75,16 @@ struct AttnParams {
   // each (zero at launch; each record's last piece re-arms it).
   const ReduceRec* reduce;
   int* counters;
+  // The step's new K/V rows, [rows][kv_heads*dims] in q's row order, which
+  // the launch attends to and stores into the pool (decode variants that
+  // can, decode_app_waves; null: the rows are already in the pool). Wave w
+  // of workgroup g handles the rows of records [app_first[g*W + w],
+  // app_first[g*W + w + 1]) of app_recs: {page id, position, k/v row *
+  // kv_heads + KV head, work item} (the plan's build_decode_appends).
+  const float* app_k;
+  const float* app_v;
+  const int* app_first;
+  const int* app_recs;
 };
 
 struct ReduceParams {
@@ -153,6 +163,10 @@ hipError_t launch_prefill(int format, int scale_f32, int head_dim, int n_units, 
 // Resident decode workgroups per CU (of the static sparse variant when
 // `sparse`).
 int decode_blocks_per_cu(int format, int scale_f32, int head_dim, int row_groups, bool sparse);
+// Waves per workgroup of the dense decode variant if it can store a step's
+// new rows (AttnParams::app_k), else 0; decode_app_rows: rows per wave it holds.
+int decode_app_waves(int format, int scale_f32, int head_dim, int row_groups);
+constexpr int decode_app_rows(int block_dims) { return block_dims <= 64 ? 16 : 8; }
 hipError_t launch_reduce(int head_dim, int n_items, int max_parts, const ReduceParams& p,
                          hipStream_t stream);
 // Expiries of the kernels' bounded waits since the process started (a

@@ -112,6 +112,13 @@ constexpr bool step_fits(bool i8, bool scale_f32, int head_dim, int rows) {
   return rows <= kMaxRows && (head_dim <= 64 || rows <= (head_dim > 128 ? 16 : (i8 && scale_f32 ? 32 : 48)));
 }
 
+// New-row records of a decode launch that stores the step's rows: ints per
+// record ({page id, position, k/v row * kv_heads + KV head, work item}),
+// and the zero records after the last list (a wave reads kAppPad records
+// from its first).
+constexpr int kAppRecInts = 4;
+constexpr int kAppPad = 16;
+
 struct RowRec {  // one new token: destination page and slot, logical position
   int page;
   int slot;

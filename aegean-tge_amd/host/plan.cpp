@@ -183,6 +183,9 @@ void build_decode(const Step& b, Residency res, AttnLists& pl, int only) {
   pl.work.clear();
   pl.reduce.clear();
   pl.wg_first.clear();
+  pl.app_first.clear();
+  pl.app_recs.clear();
+  pl.app_waves = 0;
   pl.parts = pl.max_splits = 0;
   int max_rows = 0;
   for (const auto& sr : b.sessions)
@@ -507,19 +510,68 @@ bool build_step_lists(const Step& b, bool i8, bool scale_f32, StepLists& out) {
   return true;
 }
 
-std::size_t image_layout(const AttnLists& pl, std::size_t* off_reduce, std::size_t* off_first) {
+std::size_t image_layout(const AttnLists& pl, std::size_t* off_reduce, std::size_t* off_first,
+                         std::size_t* off_app) {
   const std::size_t wbytes = pl.work.size() * sizeof(WorkRec);
   *off_reduce = align256(wbytes);
   *off_first = align256(*off_reduce + pl.reduce.size() * sizeof(ReduceRec));
-  return *off_first + pl.wg_first.size() * sizeof(int);
+  const std::size_t end = *off_first + pl.wg_first.size() * sizeof(int);
+  if (!off_app) return end;
+  *off_app = align256(end);
+  return *off_app + (pl.app_first.size() + pl.app_recs.size()) * sizeof(int);
 }
 
-void write_image(const AttnLists& pl, std::size_t off_reduce, std::size_t off_first, char* h) {
+void write_image(const AttnLists& pl, std::size_t off_reduce, std::size_t off_first, char* h,
+                 std::size_t off_app) {
   if (!pl.work.empty()) std::memcpy(h, pl.work.data(), pl.work.size() * sizeof(WorkRec));
   if (!pl.reduce.empty())
     std::memcpy(h + off_reduce, pl.reduce.data(), pl.reduce.size() * sizeof(ReduceRec));
   if (!pl.wg_first.empty())
     std::memcpy(h + off_first, pl.wg_first.data(), pl.wg_first.size() * sizeof(int));
+  if (off_app && !pl.app_first.empty()) {
+    std::memcpy(h + off_app, pl.app_first.data(), pl.app_first.size() * sizeof(int));
+    std::memcpy(h + off_app + pl.app_first.size() * sizeof(int), pl.app_recs.data(),
+                pl.app_recs.size() * sizeof(int));
+  }
+}
+
+void build_decode_appends(const Step& b, AttnLists& pl, int waves, int max_rows) {
+  pl.app_first.clear();
+  pl.app_recs.clear();
+  pl.app_waves = 0;
+  // (the kernel keys a row by its work item, below 2^15)
+  if (waves <= 0 || pl.work.size() >= (std::size_t)1 << 15) return;
+  const int groups = (int)pl.wg_first.size() - 1;
+  std::vector<std::vector<int>> per((std::size_t)waves);
+  for (int g = 0; g < groups; ++g) {
+    for (auto& v : per) v.clear();
+    for (int it = pl.wg_first[(std::size_t)g]; it < pl.wg_first[(std::size_t)g + 1]; ++it) {
+      const WorkRec& u = pl.work[(std::size_t)it];
+      const SessionRec& sr = b.sessions[(std::size_t)u.session];
+      const int j0 = std::max(0, 16 * u.page_begin - sr.ctx);
+      const int j1 = std::min(sr.n_new, 16 * u.page_end - sr.ctx);
+      for (int j = j0; j < j1; ++j) {
+        const int pos = sr.ctx + j;
+        auto& v = per[(std::size_t)((pos / 16 - u.page_begin + it) % waves)];
+        v.push_back(b.tables[(std::size_t)sr.table_off + (std::size_t)(pos / 16)]);
+        v.push_back(pos);
+        v.push_back((sr.q_row + j) * b.kv_heads + u.kv_head);
+        v.push_back(it);
+      }
+    }
+    for (const auto& v : per) {
+      if ((int)(v.size() / kAppRecInts) > max_rows) {  // more than a wave holds: no lists
+        pl.app_first.clear();
+        pl.app_recs.clear();
+        return;
+      }
+      pl.app_first.push_back((int)(pl.app_recs.size() / kAppRecInts));
+      pl.app_recs.insert(pl.app_recs.end(), v.begin(), v.end());
+    }
+  }
+  pl.app_first.push_back((int)(pl.app_recs.size() / kAppRecInts));
+  pl.app_recs.resize(pl.app_recs.size() + (std::size_t)kAppPad * kAppRecInts, 0);
+  pl.app_waves = waves;
 }
 
 }  // namespace tge::plan

@@ -91,7 +91,17 @@ struct AttnLists {
   int tile_rows = 0;          // prefill: rows of a tile (prefill_tile_rows, or 64)
   int parts = 0;              // split-K partial slots
   int max_splits = 0;
+  // Decode launches that store the step's new rows (build_decode_appends):
+  // the rows each wave stores, those of the pages it reads itself, as
+  // records {page id, position, k/v row * kv_heads + KV head, work item};
+  // wave w of workgroup g stores records [app_first[g*app_waves + w],
+  // app_first[g*app_waves + w + 1]). kAppPad zero records follow the last.
+  // app_waves 0: no lists (the launch cannot store the rows).
+  std::vector<int> app_first;
+  std::vector<int> app_recs;
+  int app_waves = 0;
 };
+
 
 // Resident workgroups of the decode launch and the device's compute units;
 // workgroup g is the (g / cus)-th to land on its compute unit.
@@ -110,6 +120,13 @@ bool take_session(const Step& s, const SessionRec& r, int only);
 // workgroup (balanced by pages, per-piece cost and dispatch rank); a
 // segment cut into several items is merged by the split reduction.
 void build_decode(const Step& s, Residency res, AttnLists& out, int only);
+
+// The new-row records of a decode plan whose launch of `waves` waves per
+// workgroup stores the rows: page j (from page_begin) of work item `item`
+// is read by wave (j + item) mod waves, which stores the new rows that page
+// holds. No lists
+// (app_waves 0) when `waves` is 0 or a wave would hold more than max_rows.
+void build_decode_appends(const Step& s, AttnLists& pl, int waves, int max_rows);
 
 // Block-prefill work: (session, KV head, query tile) x page splits sized so
 // the launch covers `cus` compute units about twice; longest items first.
@@ -147,7 +164,10 @@ bool build_step_lists(const Step& s, bool i8, bool scale_f32, StepLists& out);
 
 // The plan image of `lists` (work | reduce | wg_first, each 256-aligned):
 // total bytes and the offsets of the reduce and wg_first parts.
-std::size_t image_layout(const AttnLists& lists, std::size_t* off_reduce, std::size_t* off_first);
-void write_image(const AttnLists& lists, std::size_t off_reduce, std::size_t off_first, char* dst);
+// [ work | reduce | wg_first | app_first | app_recs ], each part 256-byte aligned.
+std::size_t image_layout(const AttnLists& lists, std::size_t* off_reduce, std::size_t* off_first,
+                         std::size_t* off_app = nullptr);
+void write_image(const AttnLists& lists, std::size_t off_reduce, std::size_t off_first, char* dst,
+                 std::size_t off_app = 0);
 
 }  // namespace tge::plan

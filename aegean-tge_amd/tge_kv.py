@@ -161,6 +161,7 @@ SIGNATURES = [
     ("tge_qwen2_kv_shared_prefix_len", _I, [_VP, _PI, _I]),
     ("tge_qwen2_kv_attach_prefix", _I, [_VP, _I, _PI, _I]),
     ("tge_read_ceiling", _I, [_VP, C.c_size_t, _I, _I, _I, _VP]),
+    ("tge_batch_decode_stores_rows", _I, [_VP, C.POINTER(C.c_int)]),
     ("tge_wait_expiries", _I, [C.POINTER(C.c_uint)]),
 ]
 
@@ -563,6 +564,13 @@ class Batch:
         w, m = C.c_int(), C.c_int()
         check(lib().tge_batch_step_info(self.h, C.byref(w), C.byref(m)), "batch_step_info")
         return w.value, m.value
+
+    def decode_stores_rows(self):
+        """tge_batch_decode_stores_rows: True when tge_decode_step runs the
+        current plan as one decode launch that also stores the new rows."""
+        x = C.c_int()
+        check(lib().tge_batch_decode_stores_rows(self.h, C.byref(x)), "batch_decode_stores_rows")
+        return bool(x.value)
 
     def decode_step(self, pool, layer, q, k, v, out, stream=None):
         """tge_decode_step: append the step's K/V rows, then decode attention

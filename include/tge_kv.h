@@ -245,10 +245,16 @@ int tge_decode_attention(const tge_batch* batch, const tge_kv_pool* pool,
  * most 48 rows per session at head_dim 128, at most 4096 page blocks in the
  * step, no static sparse subset) runs as one kernel: the workgroup that reads a segment's new positions stores the new
  * rows of its KV head first (the same bits as tge_kv_append), and a context
- * cut into several pieces is merged by the last piece to finish. Larger
- * steps run the append, the decode kernel and its merge. Outputs equal
- * those of the two calls within the attention tolerance (the same math,
- * other page splits).
+ * cut into several pieces is merged by the last piece to finish. A larger
+ * step runs the decode kernel and its merge, the decode kernel taking the
+ * new rows from k and v: each wave encodes the rows of the pages it reads
+ * (the same bits as tge_kv_append), writes them into its on-chip copy of
+ * such a page as it lands and stores them into the pool after its last
+ * page. Where its variant cannot (head_dim above 128, more than 32 rows per
+ * unit, more new rows on one wave's pages than it holds, a static sparse
+ * subset) the append runs first, as its own launch. Outputs equal those of
+ * the two calls within the attention tolerance (the same math, other page
+ * splits; bit for bit on a large step).
  */
 int tge_decode_step(const tge_batch* batch, tge_kv_pool* pool, int layer, const float* q,
                     const float* k, const float* v, float* out, void* stream);
@@ -258,6 +264,12 @@ int tge_decode_step(const tge_batch* batch, tge_kv_pool* pool, int layer, const 
  * into; 0 and 0 when the step runs the append and decode kernels. No
  * counterpart in the reference: for benchmarks and tests. */
 int tge_batch_step_info(const tge_batch* batch, int* workgroups, int* max_pieces);
+
+/* 1 in *stores when tge_decode_step runs the current plan (and sparse
+ * setting) as a decode launch that stores the new rows itself (no append
+ * launch), else 0. No counterpart in the reference: for benchmarks and
+ * tests. */
+int tge_batch_decode_stores_rows(const tge_batch* batch, int* stores);
 
 /*
  * tge_decode_attention for callers that cannot allocate memory (tight

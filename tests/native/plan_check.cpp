@@ -4,6 +4,8 @@
 //     page of every (session, KV head[, query tile]) exactly once, in order;
 //     split items own consecutive partial slots that one reduction record
 //     lists; workgroup ranges tile the work list; rows fit the units;
+//   - the decode lists' new-row records list every new row once, for the
+//     wave that reads its page;
 //   - the one-launch step lists are taken exactly when a step qualifies and
 //     tile each (session, KV head) in order with one appending last piece;
 //   - invalid descriptions are rejected and leave the step untouched;
@@ -268,9 +270,65 @@ void check_step_lists(const Step& st, bool i8, bool sf32) {
   for (int u : slot_used) REQUIRE(u == 1, "unused slot");
 }
 
+// New-row records of a decode plan (build_decode_appends): each new row of
+// every (session, KV head) once, in the list of the wave that reads its page
+// ((page - page_begin + item) mod waves), with its page id and k/v row; no
+// lists only when a wave would hold more than max_rows.
+void check_appends(const Step& st, const AttnLists& l, int waves, int max_rows) {
+  if (l.app_waves == 0) {
+    REQUIRE(l.app_first.empty() && l.app_recs.empty(), "no lists: empty");
+    // some wave holds more than max_rows
+    bool over = false;
+    for (int g = 0; g < l.groups && !over; ++g) {
+      std::vector<int> n((std::size_t)waves, 0);
+      for (int it = l.wg_first[(std::size_t)g]; it < l.wg_first[(std::size_t)g + 1]; ++it) {
+        const WorkRec& u = l.work[(std::size_t)it];
+        const SessionRec& sr = st.sessions[(std::size_t)u.session];
+        for (int j = 0; j < sr.n_new; ++j) {
+          const int pg = (sr.ctx + j) / 16;
+          if (pg >= u.page_begin && pg < u.page_end) ++n[(std::size_t)((pg - u.page_begin + it) % waves)];
+        }
+      }
+      for (int x : n) over = over || x > max_rows;
+    }
+    REQUIRE(over, "lists refused although every wave fits");
+    return;
+  }
+  REQUIRE(l.app_waves == waves, "waves");
+  REQUIRE(l.app_first.size() == (std::size_t)l.groups * waves + 1, "list bounds");
+  const int total = l.app_first.back();
+  REQUIRE(l.app_recs.size() == (std::size_t)(total + kAppPad) * kAppRecInts, "records and padding");
+  for (std::size_t k = (std::size_t)total * kAppRecInts; k < l.app_recs.size(); ++k)
+    REQUIRE(l.app_recs[k] == 0, "padding");
+  std::map<std::tuple<int, int, int>, int> seen;  // (session, head, position)
+  for (int g = 0; g < l.groups; ++g) {
+    for (int w = 0; w < waves; ++w) {
+      const int a = l.app_first[(std::size_t)(g * waves + w)], b = l.app_first[(std::size_t)(g * waves + w + 1)];
+      REQUIRE(a <= b && b - a <= max_rows, "wave list %d..%d", a, b);
+      for (int r = a; r < b; ++r) {
+        const int* rec = &l.app_recs[(std::size_t)r * kAppRecInts];
+        const int item = rec[3];
+        REQUIRE(item >= l.wg_first[(std::size_t)g] && item < l.wg_first[(std::size_t)g + 1], "item of the share");
+        const WorkRec& u = l.work[(std::size_t)item];
+        const SessionRec& sr = st.sessions[(std::size_t)u.session];
+        const int pos = rec[1], pg = pos / 16, j = pos - sr.ctx;
+        REQUIRE(j >= 0 && j < sr.n_new, "a new position");
+        REQUIRE(pg >= u.page_begin && pg < u.page_end, "a page of the item");
+        REQUIRE((pg - u.page_begin + item) % waves == w, "the wave that reads the page");
+        REQUIRE(rec[0] == st.tables[(std::size_t)(sr.table_off + pg)], "page id");
+        REQUIRE(rec[2] == (sr.q_row + j) * st.kv_heads + u.kv_head, "k/v row");
+        REQUIRE(seen.emplace(std::make_tuple(u.session, u.kv_head, pos), 1).second, "row listed twice");
+      }
+    }
+  }
+  std::size_t want = 0;
+  for (const auto& sr : st.sessions) want += (std::size_t)sr.n_new * st.kv_heads;
+  REQUIRE(seen.size() == want, "rows listed %zu of %zu", seen.size(), want);
+}
+
 void random_plans(int cases) {
   std::mt19937 rng(12345);
-  int narrow_seen = 0, wide_seen = 0;
+  int narrow_seen = 0, wide_seen = 0, appends_seen = 0;
   for (int i = 0; i < cases; ++i) {
     const int kvh = 1 << (rng() % 4);
     const int group = (i % 17 == 0) ? 1 + (int)(rng() % 128) : 1 + (int)(rng() % 8);
@@ -310,6 +368,19 @@ void random_plans(int cases) {
         build_decode(st, res, dec, only);
         check_lists(st, dec, only, false);
         REQUIRE(dec.groups <= res.groups, "more workgroups than resident");
+        if (only == 0) {
+          const int waves = (rng() % 2) ? 4 : 8, max_rows = (rng() % 2) ? 8 : 16;
+          build_decode_appends(st, dec, waves, max_rows);
+          check_appends(st, dec, waves, max_rows);
+          if (dec.app_waves) appends_seen++;
+          std::size_t ofr = 0, off = 0, oapp = 0;
+          const std::size_t bytes = image_layout(dec, &ofr, &off, &oapp);
+          std::vector<char> img(bytes);
+          write_image(dec, ofr, off, img.data(), oapp);
+          if (!dec.app_recs.empty())
+            REQUIRE(std::memcmp(img.data() + oapp + dec.app_first.size() * sizeof(int), dec.app_recs.data(),
+                                dec.app_recs.size() * sizeof(int)) == 0, "records in the image");
+        }
       }
       const int halves = 1 + (int)(rng() % 2);
       const bool pf_i8 = rng() % 2;
@@ -331,6 +402,7 @@ void random_plans(int cases) {
   }
   REQUIRE(narrow_seen > 0 && wide_seen > 0, "tile widths: %d narrow, %d wide", narrow_seen,
           wide_seen);
+  REQUIRE(appends_seen > 0, "no plan with new-row lists");
 }
 
 void invalid_descriptions() {

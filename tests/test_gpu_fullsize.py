@@ -161,6 +161,7 @@ class Serving:
             getattr(b, kind)(self.pool, 0, dq, out)
         tk.hip().sync()
         self.last_step_info = b.step_info()
+        self.last_stores_rows = b.decode_stores_rows()
         got = out.numpy()
         sh = self.sh
         wants = oracle_outputs(self.fc, q, self.ctx, n, sh)
@@ -297,8 +298,9 @@ def test_c5_full_size(gpu):
     4-query verify step over all of them; then the churn of the workload:
     8 sessions release their pages (logical order) and 8 new 2048-token
     sessions take them (LIFO reuse), and a second step runs over the
-    changed batch. Every output row is checked, and the pool contents of
-    the new sessions are bit-exact."""
+    changed batch through tge_decode_step (the decode launch attends to and
+    stores the new rows, as in the bench's layer call). Every output row is checked, and
+    the pool contents of the new sessions are bit-exact."""
     cfg = synth.configs()["c5"]
     say("C5 full size")
     sh = cfg.shape
@@ -322,7 +324,8 @@ def test_c5_full_size(gpu):
     reused = sum(p in set(freed) for s in churn for p in sv.pages[s])
     assert reused == sum(len(sv.pages[s]) for s in churn), "new sessions should reuse freed pages"
     sv.fill(only=set(churn))
-    rows, items, splits = sv.step(m)
+    rows, items, splits = sv.step(m, kind="step")
+    assert sv.last_step_info == (0, 0) and sv.last_stores_rows, "the decode launch stores the rows"
     say(f"  step 2 plan: {rows} rows, {items} work items, up to {splits} splits")
     b = tk.Batch().plan(sv.pool, [tk.Session(c - cfg.n_new, cfg.n_new, p)
                                   for c, p in zip(sv.ctx, sv.pages)], sh.q_heads)

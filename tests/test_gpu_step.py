@@ -160,3 +160,56 @@ def test_batch_planned_for_another_format_is_refused(gpu):
         a.close()
     for pl in (p_i8, p_i8f32, p_f16):
         pl.close()
+
+
+LARGE_STEP_CASES = {
+    # name: (q_heads, kv_heads, hd, fmt, sf, contexts, n_new, the decode
+    # launch stores the rows); each above 4096 page blocks, so
+    # tge_decode_step runs the persistent decode kernel: it writes the new
+    # rows of the pages each wave reads into the wave's copy of the page and
+    # stores them into the pool, or (head_dim 256, more than 32 rows per
+    # unit, too many rows on one wave's pages) the append runs first.
+    "verify_i8": (28, 4, 128, tk.KV_I8, 0, [9000, 37, 5000, 15, 3000, 300], 4, True),
+    "f16_d64_ragged": (6, 2, 64, tk.KV_F16, 0, [20000, 12000, 31, 16, 17, 2047], [9, 1, 2, 9, 3, 5],
+                       True),
+    # 63 rows per unit (four row groups): the append runs first
+    "f16_d64_wide_group": (14, 2, 64, tk.KV_F16, 0, [20000, 12000, 31, 16, 17, 2047], [9, 1, 2, 9, 3, 5],
+                           False),
+    "i8_f32_group1": (8, 8, 128, tk.KV_I8, 1, [9000, 1, 255, 40, 600], 8, True),
+    "short_sessions_first_pages": (28, 4, 128, tk.KV_I8, 0, [17000, 20, 3, 45, 0, 16], 4, True),
+    "d256_append_first": (12, 2, 256, tk.KV_F16, 0, [30000, 5000, 8, 100], 8, False),
+    # many short sessions: shares of many units; more rows on one wave's
+    # pages than it holds, so the append runs first
+    "many_short": (28, 4, 128, tk.KV_I8, 0, [int(x) for x in np.random.default_rng(5).integers(0, 60, 160)]
+                   + [12000], 4, None),
+}
+
+
+@pytest.mark.parametrize("name", list(LARGE_STEP_CASES))
+def test_large_step_stores_rows_in_decode(gpu, name):
+    """A large step through tge_decode_step: pool contents bit-exact against
+    the oracle, attention against the oracle, and outputs bit-identical to
+    the separate append followed by tge_decode_attention on a second pool of
+    the same case; the path taken is the one the case names."""
+    qh, kvh, hd, fmt, sf, ctx, nn, folds = LARGE_STEP_CASES[name]
+    say(f"large step case {name}")
+    out = {}
+    for kind in ("step", "decode"):
+        case = PagedCase(qh, kvh, hd, fmt, ctx, nn, scale_format=sf, seed=61,
+                         outlier_frac=0.01 if fmt == tk.KV_I8 else 0)
+        case.fill()
+        got, b = case.step(kind=kind)
+        assert b.step_info() == (0, 0), "a large step"
+        if kind == "step":
+            stores = b.decode_stores_rows()
+            say(f"  decode launch stores the rows: {stores}")
+            if folds is not None:
+                assert stores == folds
+        out[kind] = got
+        b.close()
+        if kind == "step":
+            err = assert_attention_close(got, case.oracle_out(), name)
+            say(f"  max abs err {err:.2e}")
+            check_contents(case)
+        case.close()
+    assert np.array_equal(bits(out["step"]), bits(out["decode"])), "fused and separate append differ"
