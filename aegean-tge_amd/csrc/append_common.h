@@ -61,7 +61,7 @@ __device__ __forceinline__ LaneCodes encode_lane(const float (&x)[8]) {
 
 // Write one lane's encoded values of token slot t into a page block through
 // `put` (byte offset in the block, value, bytes: 1, 2, 4 or 8; a write never
-// crosses a 16-byte boundary): K, two runs of 4 dims (k_index_np is
+// crosses a 16-byte boundary): K, two runs of 4 dims (k_index is
 // contiguous in d&3); V, 8 single elements; int8, the block's scale from
 // the quarter-0 lane.
 template <int FMT, typename Put>
@@ -70,8 +70,8 @@ __device__ __forceinline__ void write_lane(Put&& put, const BlockGeom& g, int nb
   const int d0 = 32 * b + 8 * quarter;  // first dim of this lane
   constexpr int E = FMT == kF16 ? 2 : 1;  // element bytes
   if (which == 0) {
-    const int k0 = k_index_np(t, d0, nb) * E;
-    const int k1 = k_index_np(t, d0 + 4, nb) * E;
+    const int k0 = k_index(t, d0, E) * E;
+    const int k1 = k_index(t, d0 + 4, E) * E;
     if (FMT == kF16) {
       put(k0, (uint64_t)c.w[0] | ((uint64_t)c.w[1] << 32), 8);
       put(k1, (uint64_t)c.w[2] | ((uint64_t)c.w[3] << 32), 8);
@@ -82,7 +82,7 @@ __device__ __forceinline__ void write_lane(Put&& put, const BlockGeom& g, int nb
   } else {
 #pragma unroll
     for (int i = 0; i < 8; ++i) {
-      const int off = g.v_off() + v_index_np(t, d0 + i, nb) * E;
+      const int off = g.v_off() + v_index(t, d0 + i, E) * E;
       if (FMT == kF16)
         put(off, (c.w[i >> 1] >> (16 * (i & 1))) & 0xffffu, 2);
       else

@@ -59,7 +59,7 @@ template <int FMT, bool SF32, int D, bool V>
 __device__ __forceinline__ float load_kv(const char* blk, int t, int d) {
   constexpr int NP = D / 32;
   constexpr int ESZ = FMT == kF16 ? 2 : 1;
-  const int i = V ? v_index_np(t, d, NP) : k_index_np(t, d, NP);
+  const int i = V ? v_index(t, d, ESZ) : k_index(t, d, ESZ);
   const char* part = blk + (V ? 16 * D * ESZ : 0);
   if constexpr (FMT == kF16) {
     return half_bits_to_float(reinterpret_cast<const uint16_t*>(part)[i]);

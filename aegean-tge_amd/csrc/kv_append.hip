@@ -180,8 +180,8 @@ __global__ __launch_bounds__(256) void kv_gather_kernel(GatherParams p) {
   const int page = p.table[pos >> 4], t = pos & 15;
   const int np = p.head_dim >> 5;
   const char* blk = static_cast<const char*>(p.pool) + ((size_t)page * p.kv_heads + h) * p.geom.block_bytes;
-  static_cast<T*>(p.k_rows)[idx] = reinterpret_cast<const T*>(blk)[k_index_np(t, d, np)];
-  static_cast<T*>(p.v_rows)[idx] = reinterpret_cast<const T*>(blk + p.geom.v_off())[v_index_np(t, d, np)];
+  static_cast<T*>(p.k_rows)[idx] = reinterpret_cast<const T*>(blk)[k_index(t, d, (int)sizeof(T))];
+  static_cast<T*>(p.v_rows)[idx] = reinterpret_cast<const T*>(blk + p.geom.v_off())[v_index(t, d, (int)sizeof(T))];
   if (p.k_scales && (d & 31) == 0) {
     const size_t o = (size_t)pos * (kv_dim >> 5) + (c >> 5);
     const int si = scale_index_np(t, d >> 5, np);

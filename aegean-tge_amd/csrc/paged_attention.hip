@@ -179,31 +179,14 @@ struct PageFifo {
   __device__ __forceinline__ int front() const { return t[0]; }
 };
 
-// Where fetch_page lands byte `off` of a page block in the ring slot: the K
-// and V parts in 16-byte pieces interleaved over the lanes (piece i of lane
-// l at i*1024 + l*16), the scales in place. Elements that lie 16 pieces
-// apart in a part (a K row's two runs of 4 dims) land 256 bytes apart, and
-// ones a piece apart (a V column's 8 dims) 16 bytes apart.
-template <int FMT, bool SF32, int D>
-__device__ __forceinline__ int ring_slot_offset(int off) {
-  using RG = Ring<FMT, SF32, D>;
-  static_assert(RG::KV_BYTES == 16 * D * (FMT == kF16 ? 2 : 1), "ring slot holds one block");
-  if (off >= 2 * RG::KV_BYTES) return off;
-  const int part = off >= RG::KV_BYTES ? RG::KV_BYTES : 0;
-  const int g = off - part;
-  return part + ((g >> 4) % RG::PIECES) * 1024 + (g / (16 * RG::PIECES)) * 16 + (g & 15);
-}
-
 // Write one lane's encoded values (write_lane's pieces) into a landed page's
-// ring slot: `offs` from ring_slot_offset (bits 0-15: the K run or first V
-// element, 16 up: the scale), `rest` = the lane's index within its row.
+// ring slot, which holds the block in its memory layout: `offs` = block byte
+// offsets (bits 0-15: the K run or first V element, 16 up: the scale),
+// `rest` = the lane's index within its row. A K row's second run of 4 dims
+// belongs to the lane 16 further on (256 bytes on in its piece), a V row's
+// next dim to the next lane (16 bytes on).
 template <int FMT, bool SF32, int D>
 __device__ __forceinline__ void patch_slot(char* slot, const LaneCodes& c, int offs, int rest, int np) {
-  constexpr int E = FMT == kF16 ? 2 : 1;
-  // the layouts the fixed strides assume (k_index_np, v_index_np; a piece
-  // per lane chunk of 16 * PIECES bytes)
-  static_assert(16 * 8 * (D / 32) * E == 16 * 16 * Ring<FMT, SF32, D>::PIECES, "K runs 16 pieces apart");
-  static_assert(8 * (D / 32) * E == 16 * Ring<FMT, SF32, D>::PIECES, "V dims one piece apart");
   char* const d = slot + (offs & 0xffff);
   if ((rest >> 2) / np == 0) {  // K
     if (FMT == kF16) {
@@ -645,9 +628,9 @@ __device__ __forceinline__ void decode_body(const AttnParams& p,
         const bool live = a * RJ + lane / RL < app_n;
         const int pos = rec_field(a, 1), kvrow = rec_field(a, 2), item = rec_field(a, 3);
         const int t = pos & 15;
-        const int run = which ? geom.v_off() + v_index_np(t, d0, NP) * E : k_index_np(t, d0, NP) * E;
+        const int run = which ? geom.v_off() + v_index(t, d0, E) * E : k_index(t, d0, E) * E;
         const int sc = (which ? geom.vs_off() : geom.ks_off()) + scale_index_np(t, b, NP) * (SF32 ? 4 : 2);
-        jobs[a].offs = ring_slot_offset<FMT, SF32, D>(run) | (sc << 16);
+        jobs[a].offs = run | (sc << 16);
         jobs[a].key = live ? (item << 16) | ((pos >> 4) & 0xffff) : -1;
 #pragma unroll
         for (int i = 0; i < 8; ++i) app_x[a][i] = 0.0f;  // (dims past the head's own store zeros)
@@ -845,8 +828,8 @@ __device__ __forceinline__ void prefill_body(const AttnParams& p,
     if (j < npages) {
       const char* blk = static_cast<const char*>(p.pool) +
                         ((size_t)table[j] * p.kv_heads + w.kv_head) * p.block_bytes;
-      fetch_page<FMT, SF32, D>(ring + (k % NB) * SH::TILE + wave * RG::SLOT, blk, p.block_bytes,
-                               lane);
+      fetch_page<FMT, SF32, D, kPageReusePolicy>(ring + (k % NB) * SH::TILE + wave * RG::SLOT, blk,
+                                                 p.block_bytes, lane);
     }
   };
   // The first tiles' fetches go out before the Q loads (both latencies overlap).

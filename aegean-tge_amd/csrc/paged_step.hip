@@ -118,8 +118,8 @@ __device__ __forceinline__ StepRec load_step(const sconst_step* s) {
 }
 
 // A page block straight from memory into the lane's registers: the same
-// image read_page takes from an LDS slot (lane l's chunk sits at
-// l * PIECES * 16 in each part; scales as stored).
+// image read_page takes from an LDS slot (piece i of lane l sits at
+// i * 1024 + l * 16 in each part; scales as stored).
 template <int FMT, bool SF32, int D>
 __device__ __forceinline__ void load_page(PageRegs<FMT, SF32, D>& r, const char* block, int lane,
                                           int grp) {
@@ -127,9 +127,8 @@ __device__ __forceinline__ void load_page(PageRegs<FMT, SF32, D>& r, const char*
   using R = PageRegs<FMT, SF32, D>;
 #pragma unroll
   for (int i = 0; i < RG::PIECES; ++i) {
-    const u32x4_t k = *reinterpret_cast<const u32x4_t*>(block + lane * RG::PIECES * 16 + i * 16);
-    const u32x4_t v =
-        *reinterpret_cast<const u32x4_t*>(block + RG::KV_BYTES + lane * RG::PIECES * 16 + i * 16);
+    const u32x4_t k = *reinterpret_cast<const u32x4_t*>(block + i * 1024 + lane * 16);
+    const u32x4_t v = *reinterpret_cast<const u32x4_t*>(block + RG::KV_BYTES + i * 1024 + lane * 16);
     r.k[4 * i] = k.x; r.k[4 * i + 1] = k.y; r.k[4 * i + 2] = k.z; r.k[4 * i + 3] = k.w;
     r.v[4 * i] = v.x; r.v[4 * i + 1] = v.y; r.v[4 * i + 2] = v.z; r.v[4 * i + 3] = v.w;
   }

@@ -9,7 +9,8 @@
 //                    c mod grid), UNROLL chunks in flight per lane;
 //   TGE_READ_BLOCKS  whole blocks of `block_bytes` (the page-block size of a
 //                    pool, e.g. 4352 for int8 at head_dim 128), one wave per
-//                    block, blocks taken in a scattered order (block
+//                    block, each load a contiguous KiB with the non-temporal
+//                    policy, blocks taken in a scattered order (block
 //                    i*stride mod n, stride coprime to n), two blocks in
 //                    flight per wave: the access shape of the decode kernel.
 // The loaded words are folded into one value that is stored only when it
@@ -67,7 +68,7 @@ __device__ __forceinline__ uint32_t load_block(const char* buf, size_t blk, uint
   const auto rs = rsrc(buf + blk * block_bytes, block_bytes);
 #pragma unroll
   for (int i = 0; i < PIECES; ++i)
-    r[i] = __builtin_bit_cast(u32x4_t, __builtin_amdgcn_raw_buffer_load_b128(rs, i * 1024 + lane * 16, 0, 0));
+    r[i] = __builtin_bit_cast(u32x4_t, __builtin_amdgcn_raw_buffer_load_b128(rs, i * 1024 + lane * 16, 0, 2));
   return 0;
 }
 

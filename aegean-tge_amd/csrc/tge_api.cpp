@@ -228,11 +228,13 @@ const char* tge_backend_arch(void) {
   return g_backend.arch.c_str();
 }
 
-int tge_kv_k_index(int token, int dim, int head_dim) {
-  return tge::k_index_np(token, dim, head_dim / 32);
+int tge_kv_k_index(int token, int dim, int format) {
+  if (format != TGE_KV_F16 && format != TGE_KV_I8) return -1;
+  return tge::k_index(token, dim, format == TGE_KV_F16 ? 2 : 1);
 }
-int tge_kv_v_index(int token, int dim, int head_dim) {
-  return tge::v_index_np(token, dim, head_dim / 32);
+int tge_kv_v_index(int token, int dim, int format) {
+  if (format != TGE_KV_F16 && format != TGE_KV_I8) return -1;
+  return tge::v_index(token, dim, format == TGE_KV_F16 ? 2 : 1);
 }
 int tge_kv_scale_index(int token, int block, int head_dim) {
   return tge::scale_index_np(token, block, head_dim / 32);

@@ -48,30 +48,37 @@ __host__ __device__ inline BlockGeom block_geom(int format, int head_dim, int sc
 
 // ---------------------------------------------------------------------------
 // Page layout. One page block = 16 tokens x head_dim (D) of one KV head; NP =
-// D/32. The in-block order is the register order of the CDNA4 matrix-core
-// operands, arranged so that each lane of a wave owns one contiguous chunk of
-// NP*8 elements (D=128: 64 B f16, 32 B int8) that it fetches with 16-byte
-// loads, and a wave's chunks tile the whole block:
+// D/32; E = element bytes (2 f16, 1 int8). The in-block order is the register
+// order of the CDNA4 matrix-core operands: each lane of a wave owns NP*8
+// elements of each part (D=128: 64 B f16, 32 B int8), cut into 16-byte
+// pieces, and piece i of lane l sits at byte i*1024 + l*16 of the part. So
+// the wave's 16-byte load i (one per piece) reads one contiguous KiB, whole
+// cache lines, and the direct-to-LDS copy of a block is the identity.
 //
+// A lane's elements, in its own order j = p*8 + h*4 + e (PE = 16/E elements
+// per piece; element j lies in piece j/PE at position j%PE):
 //  K (A operand of S^T = K.Q^T, row = token t):
 //    d -> pair p = d/32, half h = (d/16)&1, group g = (d/4)&3, e = d&3
-//    index = ((g*16 + t)*NP + p)*8 + h*4 + e
-//    lane (g, t) holds, per pair p, dims 32p+4g+e and 32p+16+4g+e: the
-//    v_mfma_f32_16x16x32_f16 A operand of the 32-dim block p (k = 8g + j).
+//    lane (g, t) = g*16 + t holds, per pair p, dims 32p+4g+e and 32p+16+4g+e:
+//    the v_mfma_f32_16x16x32_f16 A operand of the 32-dim block p (k = 8g + j).
 //  V (A operand of O^T = V^T.P^T, row = dim):
 //    tile j = d/16, pair p = j/2, h = j&1, dl = d&15, g = t/4, e = t&3
-//    index = ((g*16 + dl)*NP + p)*8 + h*4 + e
-//    lane (g, dl) holds tokens 4g..4g+3 of dims 32p+dl (h=0), 32p+16+dl
-//    (h=1): the v_mfma_f32_16x16x16_f16 A operand of tile j.
+//    lane (g, dl) = g*16 + dl holds tokens 4g..4g+3 of dims 32p+dl (h=0),
+//    32p+16+dl (h=1): the v_mfma_f32_16x16x16_f16 A operand of tile j.
+//    index = ((j/PE)*64 + lane)*PE + j%PE for both parts.
 //  Scales (I8), one per (token t, 32-dim block b):
 //    index = ((t/4)*NP + b)*4 + (t&3)
 //    lanes of group g read the 4*NP scales of their four tokens at once.
 // ---------------------------------------------------------------------------
-__host__ __device__ inline int k_index_np(int t, int d, int np) {
-  return ((((d >> 2) & 3) * 16 + t) * np + (d >> 5)) * 8 + (((d >> 4) & 1) << 2) + (d & 3);
+__host__ __device__ inline int piece_index(int lane, int j, int esz) {
+  const int pe = 16 / esz;  // elements per 16-byte piece
+  return ((j / pe) * 64 + lane) * pe + (j % pe);
 }
-__host__ __device__ inline int v_index_np(int t, int d, int np) {
-  return (((t >> 2) * 16 + (d & 15)) * np + (d >> 5)) * 8 + (((d >> 4) & 1) << 2) + (t & 3);
+__host__ __device__ inline int k_index(int t, int d, int esz) {
+  return piece_index(((d >> 2) & 3) * 16 + t, (d >> 5) * 8 + (((d >> 4) & 1) << 2) + (d & 3), esz);
+}
+__host__ __device__ inline int v_index(int t, int d, int esz) {
+  return piece_index((t >> 2) * 16 + (d & 15), (d >> 5) * 8 + (((d >> 4) & 1) << 2) + (t & 3), esz);
 }
 __host__ __device__ inline int scale_index_np(int t, int b, int np) {
   return ((t >> 2) * np + b) * 4 + (t & 3);

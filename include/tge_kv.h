@@ -86,7 +86,7 @@ const char* tge_backend_arch(void);
  *   fp32)
  * Block (page, kv_head) of a layer is block number page*kv_heads + kv_head.
  * Element (token t, dim d) of a block's part sits at:
- *   K: tge_kv_k_index(t, d, W)      V: tge_kv_v_index(t, d, W)
+ *   K: tge_kv_k_index(t, d, format)  V: tge_kv_v_index(t, d, format)
  *   scale of (t, block b = d/32): tge_kv_scale_index(t, b, W)
  * head_dim: a multiple of 16 up to 256 (F16) or of 32 up to 256 (I8, whose
  * scales cover 32-dim blocks). The reference takes any head_dim > 0
@@ -130,15 +130,21 @@ size_t tge_kv_pool_bytes(const tge_kv_pool* pool);
  * Asynchronous on `stream`. */
 int tge_kv_copy_page(tge_kv_pool* pool, int src_page, int dst_page, void* stream);
 
-/* In-page element index of (token, dim) for K and V blocks, and of the
- * scale of (token, 32-dim block), for blocks of width W (the third
- * argument, 64, 128 or 256; the pool's tge_kv_layer_view.block_dims). With
- * NP = W/32:
- *   K:     ((((d/4)&3)*16 + t)*NP + d/32)*8 + ((d/16)&1)*4 + (d&3)
- *   V:     ((t/4*16 + (d&15))*NP + d/32)*8 + ((d/16)&1)*4 + (t&3)
- *   scale: ((t/4)*NP + b)*4 + (t&3) */
-int tge_kv_k_index(int token, int dim, int head_dim);
-int tge_kv_v_index(int token, int dim, int head_dim);
+/* In-page element index of (token, dim) in a K or V part of the given
+ * format (TGE_KV_F16 or TGE_KV_I8; -1 for another value), and of the scale
+ * of (token, 32-dim block) in blocks of width W (the third argument, 64, 128
+ * or 256; the pool's tge_kv_layer_view.block_dims). A part is a sequence of
+ * 16-byte pieces of PE = 8 (F16) or 16 (I8) elements; piece i of lane l
+ * (l = 0..63) sits at element (i*64 + l)*PE, so a 64-lane wave reads a part
+ * with one 1-KiB contiguous load per piece. Lane l holds elements j = 0 ..
+ * 8*W/32-1 of its matrix-core operand, element j in piece j/PE at position
+ * j%PE:
+ *   K: lane = ((d/4)&3)*16 + t,   j = (d/32)*8 + ((d/16)&1)*4 + (d&3)
+ *   V: lane = (t/4)*16 + (d&15),  j = (d/32)*8 + ((d/16)&1)*4 + (t&3)
+ *   index = ((j/PE)*64 + lane)*PE + j%PE   (the same for every W)
+ *   scale: ((t/4)*NP + b)*4 + (t&3), NP = W/32 */
+int tge_kv_k_index(int token, int dim, int format);
+int tge_kv_v_index(int token, int dim, int format);
 int tge_kv_scale_index(int token, int block, int head_dim);
 
 /* ---------------------------------------------------------------------------

@@ -102,25 +102,31 @@ def test_pool_accepts_head_sizes_between_the_block_widths(tk):
 
 def test_page_layout_is_a_bijection(tk):
     L = tk.lib()
-    for hd in (64, 128):
-        np_ = hd // 32
-        ks = {L.tge_kv_k_index(t, d, hd) for t in range(16) for d in range(hd)}
-        vs = {L.tge_kv_v_index(t, d, hd) for t in range(16) for d in range(hd)}
-        ss = {L.tge_kv_scale_index(t, b, hd) for t in range(16) for b in range(np_)}
-        assert ks == set(range(16 * hd)) and vs == set(range(16 * hd))
-        assert ss == set(range(16 * np_))
-        # operand contiguity: lane (g, t) owns NP*8 consecutive K elements:
-        # per pair p, dims 32p+4g+e then 32p+16+4g+e
-        for g in range(4):
-            for t in range(16):
-                dims = [32 * p + 16 * h + 4 * g + e for p in range(np_) for h in range(2)
-                        for e in range(4)]
-                idx = [L.tge_kv_k_index(t, d, hd) for d in dims]
-                assert idx == list(range((g * 16 + t) * np_ * 8, (g * 16 + t + 1) * np_ * 8))
-                # and of V: tokens 4g..4g+3 of dims 32p+t (h=0), 32p+16+t (h=1)
-                vidx = [L.tge_kv_v_index(4 * g + e, 32 * p + 16 * h + t, hd) for p in range(np_)
-                        for h in range(2) for e in range(4)]
-                assert vidx == list(range((g * 16 + t) * np_ * 8, (g * 16 + t + 1) * np_ * 8))
+    assert L.tge_kv_k_index(0, 0, 0) == -1 and L.tge_kv_v_index(0, 0, 3) == -1
+    for fmt, esz in ((tk.KV_F16, 2), (tk.KV_I8, 1)):
+        pe = 16 // esz
+        for hd in (64, 128, 256):
+            np_ = hd // 32
+            ks = {L.tge_kv_k_index(t, d, fmt) for t in range(16) for d in range(hd)}
+            vs = {L.tge_kv_v_index(t, d, fmt) for t in range(16) for d in range(hd)}
+            ss = {L.tge_kv_scale_index(t, b, hd) for t in range(16) for b in range(np_)}
+            assert ks == set(range(16 * hd)) and vs == set(range(16 * hd)), (fmt, hd)
+            assert ss == set(range(16 * np_))
+            # operand order: lane (g, t) holds, per pair p, K dims 32p+4g+e then
+            # 32p+16+4g+e, and V tokens 4g..4g+3 of dims 32p+t (h=0), 32p+16+t
+            # (h=1); its element j sits in 16-byte piece j // pe at element
+            # (64 * piece + lane) * pe + j % pe, so piece i of the 64 lanes is
+            # one contiguous KiB
+            for g in range(4):
+                for t in range(16):
+                    lane = g * 16 + t
+                    want = [(64 * (j // pe) + lane) * pe + j % pe for j in range(np_ * 8)]
+                    dims = [32 * p + 16 * h + 4 * g + e for p in range(np_) for h in range(2)
+                            for e in range(4)]
+                    assert [L.tge_kv_k_index(t, d, fmt) for d in dims] == want
+                    vidx = [L.tge_kv_v_index(4 * g + e, 32 * p + 16 * h + t, fmt)
+                            for p in range(np_) for h in range(2) for e in range(4)]
+                    assert vidx == want
 
 
 # ---------------------------------------------------------------------------

@@ -45,8 +45,11 @@ def raw_pool_rows(case, layer, s, count):
     t = np.arange(16)[:, None]
     d = np.arange(W)[None, :]
     n = W // 32
-    kidx = ((((d >> 2) & 3) * 16 + t) * n + (d >> 5)) * 8 + (((d >> 4) & 1) << 2) + (d & 3)
-    vidx = (((t >> 2) * 16 + (d & 15)) * n + (d >> 5)) * 8 + (((d >> 4) & 1) << 2) + (t & 3)
+    pe = 16 // esz  # elements per 16-byte piece; piece i of lane l at (64 i + l) pe
+    kl, kj = ((d >> 2) & 3) * 16 + t, (d >> 5) * 8 + (((d >> 4) & 1) << 2) + (d & 3)
+    vl, vj = (t >> 2) * 16 + (d & 15), (d >> 5) * 8 + (((d >> 4) & 1) << 2) + (t & 3)
+    kidx = ((kj // pe) * 64 + kl) * pe + kj % pe
+    vidx = ((vj // pe) * 64 + vl) * pe + vj % pe
     sidx = ((t >> 2) * n + np.arange(n)[None, :]) * 4 + (t & 3)
     k = np.empty((count, case.kv_dim), elem)
     v = np.empty((count, case.kv_dim), elem)
