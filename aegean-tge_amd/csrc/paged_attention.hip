@@ -655,10 +655,6 @@ __device__ __forceinline__ void decode_body(const AttnParams& p,
       int fs = head + count;
       fs = fs >= NB ? fs - NB : fs;
       finalize(fs);
-      if constexpr (MIX) {
-        // (the merge area is free again after finalize)
-        if (p.counters && cw.part >= 0) arrive_and_merge<D, ROWS>(p, cw.red, &sh.flag, sh.merge);
-      }
       next_unit();
     }
   };
@@ -701,6 +697,20 @@ __device__ __forceinline__ void decode_body(const AttnParams& p,
     --count;
     fifo.pop();
     close_units();  // the slot just read is free
+  }
+  if constexpr (MIX) {
+    // The split pieces of the share count in (and the last piece of a
+    // record merges it) once the whole share is done: the ring is empty
+    // then, so waiting for the coherent partial stores drains nothing. (At
+    // the end of each piece instead, the wait drained every wave's ring:
+    // 135 against 131 us for a c5-shaped mixed step.) Only a share's first
+    // and last items can be pieces.
+    if (p.counters) {
+      for (int it = first; it < last; ++it) {
+        const WorkRec w = load_work(work + it);
+        if (w.part >= 0) arrive_and_merge<D, ROWS>(p, w.red, &sh.flag, sh.merge);
+      }
+    }
   }
   if constexpr (kApp) {
     // the rows into the pool (for the launches after this one); the list
@@ -1033,11 +1043,12 @@ void paged_prefill_kernel(AttnParams p) {
 // ---------------------------------------------------------------------------
 // Mixed-step kernel (continuous batching: some sessions decoding, some
 // prefilling a chunk, forward_batch qwen2.cpp:1613-1747): one launch whose
-// first n_dec workgroups run the decode role over the decode plan's
-// persistent shares and whose remaining workgroups are block-prefill tiles
-// of the prefill plan; the tiles take over each CU's slots as its decode
-// workgroups finish, so the decode tail overlaps the prefill. Split pieces of
-// either kind are merged in the same launch by the last piece to arrive.
+// first n_dec workgroups (one per CU) run the decode role over the decode
+// plan's persistent shares and whose remaining workgroups are block-prefill
+// tiles of the prefill plan; the tiles take each CU's other slot from the
+// start and its decode slot once the share is done, so the HBM-bound decode
+// runs under the MFMA-bound tiles. Split pieces of either kind are merged in
+// the same launch by the last piece to arrive.
 // The two roles share the workgroup's LDS (a union) and its register budget.
 // ---------------------------------------------------------------------------
 template <int FMT, bool SF32, int D, int NRG>
@@ -1361,31 +1372,6 @@ hipError_t launch_mixed(int format, int scale_f32, int head_dim, int row_groups,
                       });
 }
 
-template <int FMT, bool SF32, int D>
-int mixed_blocks_d(int row_groups) {
-  int n = 0;
-  hipError_t e = hipErrorInvalidValue;
-  switch (row_groups) {
-#define TGE_MOCC(r)                                                                                    \
-  case r:                                                                                              \
-    if constexpr (r <= max_row_groups<D>())                                                            \
-      e = hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, paged_mixed_kernel<FMT, SF32, D, r>, 256, 0); \
-    break;
-    TGE_MOCC(1)
-    TGE_MOCC(2)
-    TGE_MOCC(3)
-    TGE_MOCC(4)
-#undef TGE_MOCC
-    default: break;
-  }
-  return e == hipSuccess ? n : 0;
-}
-
-int mixed_blocks_per_cu(int format, int scale_f32, int head_dim, int row_groups) {
-  return with_variant(format, scale_f32, head_dim, 0, [&]<int FMT, bool SF32, int D>() {
-    return mixed_blocks_d<FMT, SF32, D>(row_groups);
-  });
-}
 
 int prefill_halves(int format, int head_dim) {
   return with_variant(format, 0, head_dim, 1, [&]<int FMT, bool SF32, int D>() {

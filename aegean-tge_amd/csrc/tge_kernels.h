@@ -147,11 +147,11 @@ hipError_t launch_kv_gather(int format, const GatherParams& p, hipStream_t strea
 hipError_t launch_decode(int format, int scale_f32, int head_dim, int row_groups, int n_groups,
                          const AttnParams& p, hipStream_t stream);
 // Mixed step in one launch (paged_mixed_kernel): n_dec persistent decode
-// workgroups over `dec`'s plan, then n_pf block-prefill tiles of `pf`'s
-// plan; both plans merge their splits in the launch (counters required).
+// workgroups over `dec`'s plan (one per CU), then n_pf block-prefill tiles
+// of `pf`'s plan; both plans merge their splits in the launch (counters
+// required).
 hipError_t launch_mixed(int format, int scale_f32, int head_dim, int row_groups, int n_dec,
                         int n_pf, const AttnParams& dec, const AttnParams& pf, hipStream_t stream);
-int mixed_blocks_per_cu(int format, int scale_f32, int head_dim, int row_groups);
 // Block prefill: one workgroup per work item (tiles of up to 128 rows).
 // Groups of four waves per block-prefill workgroup (1 or 2): with two, an
 // item's pages are shared by both halves and the plan's items may be twice

@@ -154,16 +154,17 @@ bool take_session(const Step& s, const SessionRec& r, int only) {
 // Relative speed of the k-th workgroup that lands on a CU. Workgroups are
 // dispatched one per CU before a CU gets a second, and on a shared SIMD the
 // older wave wins issue, so equal page shares finish far apart. Measured
-// pages per microsecond of the c5 decode kernel by dispatch rank: 1 : 0.75
-// with two workgroups per CU, 1 : 0.775 : 0.54 with three (per-workgroup
-// timestamps over whole launches); more ranks fall off by TGE_DECODE_RANK_WEIGHT.
+// pages per microsecond of the c5 decode kernel by dispatch rank: 1 : 0.79
+// with two workgroups per CU (1 : 0.75 before page loads read whole KiB
+// runs), 1 : 0.775 : 0.54 with three (per-workgroup timestamps over whole
+// launches); more ranks fall off by TGE_DECODE_RANK_WEIGHT.
 #ifndef TGE_DECODE_RANK_WEIGHT
 #define TGE_DECODE_RANK_WEIGHT 0.76
 #endif
 
 namespace {
 double rank_weight(int rank, int per_cu) {
-  if (per_cu == 2 && rank < 2) return rank == 0 ? 1.0 : 0.75;
+  if (per_cu == 2 && rank < 2) return rank == 0 ? 1.0 : 0.79;
   if (per_cu == 3 && rank < 3) return rank == 0 ? 1.0 : rank == 1 ? 0.775 : 0.54;
   return std::pow(TGE_DECODE_RANK_WEIGHT, (double)rank);
 }
