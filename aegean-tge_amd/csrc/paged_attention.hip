@@ -214,7 +214,13 @@ __device__ __forceinline__ void patch_slot(char* slot, const LaneCodes& c, int o
   }
 }
 
-template <int FMT, bool SF32, int D, int NRG, int W, int WPE, bool SP, bool MIX, bool APP = false>
+// SKIP (static sparse, stride > 16 only): pages holding no kept position
+// are never fetched. For strides of 16 or less every page holds one; that
+// variant leaves the kept-page enumeration out of its issue path (with it
+// compiled in, the c5 step at stride 4 took 1.22x the dense kernel's time,
+// without 1.08x).
+template <int FMT, bool SF32, int D, int NRG, int W, int WPE, bool SP, bool MIX, bool APP = false,
+          bool SKIP = false>
 __device__ __forceinline__ void decode_body(const AttnParams& p,
                                             DecodeShared<FMT, SF32, D, NRG, SP, MIX>& sh,
                                             const int group) {
@@ -388,7 +394,8 @@ __device__ __forceinline__ void decode_body(const AttnParams& p,
   // unit's smallest span). The waves split the kept ordinals round-robin
   // (wave w takes w, w+W, ...), so a periodic skip pattern never leaves
   // one wave all the work.
-  const bool skipping = SP && p.sp_stride > 16;
+  static_assert(!SKIP || SP, "page skipping is a static sparse variant");
+  const bool skipping = SKIP && p.sp_stride > 16;
   int ka0 = 0, kna = 0, kk0 = 0, knm = 0, kc0 = 0, knc = 0;  // A start/count, M first k/count, C
   auto kept_geometry = [&](const WorkRec& w) __attribute__((always_inline)) -> void {
     const int pb = w.page_begin, pe = w.page_end;
@@ -740,11 +747,11 @@ __device__ __forceinline__ void decode_body(const AttnParams& p,
 
 // APP: the launch also encodes, attends to and stores the step's new rows
 // (p.app_k, tge_decode_step).
-template <int FMT, bool SF32, int D, int NRG, int W, int WPE, bool SP, bool APP = false>
+template <int FMT, bool SF32, int D, int NRG, int W, int WPE, bool SP, bool APP = false, bool SKIP = false>
 __global__ __launch_bounds__(64 * W) __attribute__((amdgpu_waves_per_eu(WPE, WPE)))
 void paged_decode_kernel(AttnParams p) {
   __shared__ DecodeShared<FMT, SF32, D, NRG, SP> sh;
-  decode_body<FMT, SF32, D, NRG, W, WPE, SP, false, APP>(p, sh, blockIdx.x);
+  decode_body<FMT, SF32, D, NRG, W, WPE, SP, false, APP, SKIP>(p, sh, blockIdx.x);
 }
 
 // ---------------------------------------------------------------------------
@@ -1186,7 +1193,11 @@ hipError_t launch_decode_d(int row_groups, int n_groups, const AttnParams& p, hi
     if constexpr (n <= max_row_groups<D>()) {                                               \
       using C = DecodeCfg<FMT, SF32, D, n, false>;                                          \
       using CS = DecodeCfg<FMT, SF32, D, n, true>;                                          \
-      if (p.sp_stride > 0) {                                                                \
+      if (p.sp_stride > 16) {                                                               \
+        hipLaunchKernelGGL((paged_decode_kernel<FMT, SF32, D, n, CS::W, CS::WPE, true, false,  \
+                                                true>),                                     \
+                           dim3((unsigned)n_groups), dim3(64 * CS::W), 0, stream, p);       \
+      } else if (p.sp_stride > 0) {                                                         \
         hipLaunchKernelGGL((paged_decode_kernel<FMT, SF32, D, n, CS::W, CS::WPE, true>),    \
                            dim3((unsigned)n_groups), dim3(64 * CS::W), 0, stream, p);       \
       } else if (p.app_k) {                                                                 \
