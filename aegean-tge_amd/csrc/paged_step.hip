@@ -144,7 +144,10 @@ __device__ __forceinline__ void load_page(PageRegs<FMT, SF32, D>& r, const char*
   }
 }
 
-template <int FMT, bool SF32, int D, int NRG>
+// SP: the static sparse subset of p.sp_* applies (attention_head_static_sparse,
+// attention_avx2.cpp:263-490: every page is read and the dropped positions
+// are masked per row).
+template <int FMT, bool SF32, int D, int NRG, bool SP = false>
 __global__ __launch_bounds__(64 * kStepWaves) void paged_step_kernel(StepParams p) {
   using C = StepCfg<FMT, SF32, D, NRG>;
   using SH = StepShared<FMT, SF32, D, NRG>;
@@ -307,6 +310,7 @@ __global__ __launch_bounds__(64 * kStepWaves) void paged_step_kernel(StepParams 
 #pragma unroll
     for (int t = 0; t < NT; ++t) u.o[rg][t] = float4_t{0, 0, 0, 0};
   }
+  if constexpr (SP) u.set_sparse(p.sp_sink, p.sp_window, p.sp_stride, rec.ctx + rec.n_new);
   const int unmasked = (rec.ctx + 1) / 16;  // pages every row sees whole
   const half8_t* qt = sh.q + lane;
   auto qf = [&](int rg, int pp) __attribute__((always_inline)) { return qt[(rg * NP + pp) * 64]; };
@@ -322,7 +326,7 @@ __global__ __launch_bounds__(64 * kStepWaves) void paged_step_kernel(StepParams 
 #pragma unroll
     for (int i = 0; i < PB; ++i) {
       const int pi = jb + i * W;
-      if (pi < rec.page_end) u.template consume_with<false>(r[i], pi, grp, pi >= unmasked, qf);
+      if (pi < rec.page_end) u.template consume_with<SP>(r[i], pi, grp, pi >= unmasked, qf);
     }
   }
 
@@ -515,35 +519,46 @@ __global__ __launch_bounds__(64 * kStepWaves) void paged_step_kernel(StepParams 
 
 }  // namespace
 
-template <int FMT, bool SF32, int D>
-hipError_t launch_step_d(int row_groups, int n, const StepParams& p, hipStream_t st) {
+template <int FMT, bool SF32, int D, bool SP>
+hipError_t launch_step_v(int row_groups, int n, const StepParams& p, hipStream_t st) {
   const dim3 grid((unsigned)n), block(64 * kStepWaves);
   // variants that would spill are not built (step_fits keeps the planner
   // from asking for them)
   constexpr bool I8 = FMT == kI8;
   switch (row_groups) {
-    case 1: hipLaunchKernelGGL((paged_step_kernel<FMT, SF32, D, 1>), grid, block, 0, st, p); break;
+    case 1:
+      if constexpr (step_fits(I8, SF32, D, 16, SP)) {
+        hipLaunchKernelGGL((paged_step_kernel<FMT, SF32, D, 1, SP>), grid, block, 0, st, p);
+        break;
+      }
+      return hipErrorInvalidValue;
     case 2:
-      if constexpr (step_fits(I8, SF32, D, 32)) {
-        hipLaunchKernelGGL((paged_step_kernel<FMT, SF32, D, 2>), grid, block, 0, st, p);
+      if constexpr (step_fits(I8, SF32, D, 32, SP)) {
+        hipLaunchKernelGGL((paged_step_kernel<FMT, SF32, D, 2, SP>), grid, block, 0, st, p);
         break;
       }
       return hipErrorInvalidValue;
     case 3:
-      if constexpr (step_fits(I8, SF32, D, 48)) {
-        hipLaunchKernelGGL((paged_step_kernel<FMT, SF32, D, 3>), grid, block, 0, st, p);
+      if constexpr (step_fits(I8, SF32, D, 48, SP)) {
+        hipLaunchKernelGGL((paged_step_kernel<FMT, SF32, D, 3, SP>), grid, block, 0, st, p);
         break;
       }
       return hipErrorInvalidValue;
     case 4:
-      if constexpr (step_fits(I8, SF32, D, 64)) {
-        hipLaunchKernelGGL((paged_step_kernel<FMT, SF32, D, 4>), grid, block, 0, st, p);
+      if constexpr (step_fits(I8, SF32, D, 64, SP)) {
+        hipLaunchKernelGGL((paged_step_kernel<FMT, SF32, D, 4, SP>), grid, block, 0, st, p);
         break;
       }
       return hipErrorInvalidValue;
     default: return hipErrorInvalidValue;
   }
   return hipGetLastError();
+}
+
+template <int FMT, bool SF32, int D>
+hipError_t launch_step_d(int row_groups, int n, const StepParams& p, hipStream_t st) {
+  return p.sp_stride > 0 ? launch_step_v<FMT, SF32, D, true>(row_groups, n, p, st)
+                         : launch_step_v<FMT, SF32, D, false>(row_groups, n, p, st);
 }
 
 hipError_t launch_step(int format, int scale_f32, int head_dim, int row_groups, int n_recs,

@@ -201,6 +201,19 @@ struct tge_batch {
   }
 };
 
+namespace {
+
+// Whether tge_decode_step runs the current plan as one kernel: a small step
+// (its lists built), and with a static sparse subset only where the sparse
+// variant of the kernel fits its registers.
+bool one_kernel_step(const tge_batch* b) {
+  return b->small.built &&
+         (b->sp_stride == 0 || tge::step_fits(b->format == TGE_KV_I8, b->scale_format == TGE_SCALE_F32,
+                                              b->step.block_dims, b->step.max_rows, true));
+}
+
+}  // namespace
+
 extern "C" {
 
 const char* tge_status_string(int status) {
@@ -514,7 +527,7 @@ int tge_batch_info(const tge_batch* b, int* rows, int* work_items, int* max_spli
 
 int tge_batch_step_info(const tge_batch* b, int* workgroups, int* max_pieces) {
   if (!b || !b->planned) return fail(TGE_ERR_INVALID, "batch_step_info: batch not planned");
-  const bool one = b->small.built;
+  const bool one = one_kernel_step(b);
   if (workgroups) *workgroups = one ? (int)b->small.lists.recs.size() : 0;
   if (max_pieces) *max_pieces = one ? b->small.lists.max_pieces : 0;
   return TGE_OK;
@@ -783,9 +796,9 @@ int tge_decode_step(const tge_batch* b, tge_kv_pool* p, int layer, const float* 
   if (!q || !k || !v || !out) return fail(TGE_ERR_INVALID, "decode_step: null q/k/v/out");
   if (!b->decode.built)
     return fail(TGE_ERR_INVALID, "decode_step: n_new * group exceeds a decode unit (64 rows, 48 at head_dim > 128)");
-  if (b->sp_stride > 0) {
-    // a static sparse step: the append, then the sparse decode kernel and
-    // its split merge
+  if (b->sp_stride > 0 && !one_kernel_step(b)) {
+    // a static sparse step the one-launch kernel does not take: the append,
+    // then the sparse decode kernel and its split merge
     s = tge_kv_append(b, p, layer, k, v, stream);
     if (s != TGE_OK) return s;
     return tge_decode_attention(b, p, layer, q, out, stream);
@@ -829,6 +842,9 @@ int tge_decode_step(const tge_batch* b, tge_kv_pool* p, int layer, const float* 
   a.rows_cap = 16 * sp.lists.row_groups;
   a.group = b->step.group;
   a.scale_log2 = (float)(1.4426950408889634 / std::sqrt((double)b->step.head_dim));
+  a.sp_sink = b->sp_sink;
+  a.sp_window = b->sp_window;
+  a.sp_stride = b->sp_stride;
   TGE_HIP(tge::launch_step(p->desc.format, p->desc.scale_format == TGE_SCALE_F32,
                            b->step.block_dims, sp.lists.row_groups, (int)sp.lists.recs.size(), a,
                            static_cast<hipStream_t>(stream)));

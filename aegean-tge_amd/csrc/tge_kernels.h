@@ -111,6 +111,7 @@ struct StepParams {
   int rows_cap;
   int group;              // query heads per KV head
   float scale_log2;
+  int sp_sink, sp_window, sp_stride;  // static sparse subset (stride 0: dense)
 };
 
 // Kernel-level group attention (tge_attention_group): one KV head's query

@@ -107,9 +107,15 @@ constexpr int step_batch_pages(bool i8, bool scale_f32, int head_dim, int row_gr
   return row_groups >= 3 || head_dim > 128 ? 1 : (2 * kw + 2 * sw <= 16 && !i8 ? 4 : 2);
 }
 
-// Steps the one-kernel step takes: rows per unit that fit its registers.
-constexpr bool step_fits(bool i8, bool scale_f32, int head_dim, int rows) {
-  return rows <= kMaxRows && (head_dim <= 64 || rows <= (head_dim > 128 ? 16 : (i8 && scale_f32 ? 32 : 48)));
+// Steps the one-kernel step takes: rows per unit that fit its registers
+// (`sparse`: the variant that applies a static sparse subset, whose extra
+// row state spills with int8 pages and fp32 scales beyond 16 rows at 128
+// dims and at 256 dims).
+constexpr bool step_fits(bool i8, bool scale_f32, int head_dim, int rows, bool sparse = false) {
+  if (rows > kMaxRows) return false;
+  if (head_dim <= 64) return true;
+  if (sparse && i8 && scale_f32) return head_dim <= 128 && rows <= 16;
+  return rows <= (head_dim > 128 ? 16 : (i8 && scale_f32 ? 32 : 48));
 }
 
 // New-row records of a decode launch that stores the step's rows: ints per

@@ -249,9 +249,11 @@ int tge_decode_attention(const tge_batch* batch, const tge_kv_pool* pool,
  * store-then-attend order of forward / forward_batch (qwen2.cpp:2073-2095,
  * 1681-1747). A small step (every session's rows fit a decode unit, at
  * most 48 rows per session at head_dim 128, at most 4096 page blocks in the
- * step, no static sparse subset) runs as one kernel: the workgroup that reads a segment's new positions stores the new
- * rows of its KV head first (the same bits as tge_kv_append), and a context
- * cut into several pieces is merged by the last piece to finish. A larger
+ * step; with a static sparse subset and int8 pages with fp32 scales, at most
+ * 16 rows per session and head_dim 128) runs as one kernel: the workgroup
+ * that reads a segment's new positions stores the new rows of its KV head
+ * first (the same bits as tge_kv_append), and a context cut into several
+ * pieces is merged by the last piece to finish. A larger
  * step runs the decode kernel and its merge, the decode kernel taking the
  * new rows from k and v: each wave encodes the rows of the pages it reads
  * (the same bits as tge_kv_append), writes them into its on-chip copy of

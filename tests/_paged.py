@@ -61,6 +61,8 @@ class PagedCase:
     def step(self, layer=0, kind="decode"):
         """Append the new rows, attend; returns (out rows, batch)."""
         b = tk.Batch().plan(self.pool, self.sessions(True), self.qh)
+        if getattr(self, "sparse", None):
+            b.set_sparse(*self.sparse)
         kk = np.concatenate([k[c:] for k, c in zip(self.k, self.contexts)])
         vv = np.concatenate([v[c:] for v, c in zip(self.v, self.contexts)])
         dk, dv = tk.DeviceArray.from_numpy(kk), tk.DeviceArray.from_numpy(vv)

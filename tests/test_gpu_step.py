@@ -47,6 +47,39 @@ def test_step_matches_oracle(gpu, name):
     case.close()
 
 
+SPARSE_STEP_CASES = {
+    # name: (q_heads, kv_heads, hd, fmt, sf, contexts, n_new, (sink, window, stride), one kernel)
+    "c1_shape_stride4": (14, 2, 64, tk.KV_F16, 0, [1024], 1, (4, 512, 4), True),
+    "c2_shape_i8_stride37": (14, 2, 64, tk.KV_I8, 0, [4096], 1, (4, 512, 37), True),
+    "c3_shape_stride5": (12, 2, 128, tk.KV_F16, 0, [512, 2048, 4096, 8192], 1, (4, 512, 5), True),
+    "verify_i8_sink_straddles": (28, 4, 128, tk.KV_I8, 0, [700, 35, 1500, 3000], 4, (20, 40, 17), True),
+    "verify_i8_f32_scales": (28, 4, 128, tk.KV_I8, 1, [700, 35, 1500], 4, (4, 64, 3), False),
+}
+
+
+@pytest.mark.parametrize("name", list(SPARSE_STEP_CASES))
+def test_sparse_step_matches_oracle(gpu, name):
+    """A static sparse subset (sink + strided middle + window, the kept set
+    of build_sparse_index, qwen2.cpp:192-220) on tge_decode_step: small
+    steps stay one kernel (the sparse variant of the step kernel; int8
+    pages with fp32 scales at 32 rows and more take the append and sparse
+    decode kernels instead), against the oracle's sparse head, pool
+    contents bit for bit."""
+    qh, kvh, hd, fmt, sf, ctx, nn, sparse, one = SPARSE_STEP_CASES[name]
+    say(f"sparse step case {name}")
+    case = PagedCase(qh, kvh, hd, fmt, ctx, nn, scale_format=sf, seed=33, outlier_frac=0.01)
+    case.fill()
+    case.sparse = sparse
+    got, b = case.step(kind="step")
+    assert (b.step_info()[0] > 0) == one, b.step_info()
+    err = assert_attention_close(got, case.oracle_out(), name)
+    say(f"  max abs err {err:.2e}")
+    b.close()
+    case.sparse = None
+    check_contents(case)
+    case.close()
+
+
 def test_step_split_counters_across_layers(gpu):
     """A context cut into the most pieces, run on three layers in a row and
     twice on one layer: every launch's last piece merges and resets its
