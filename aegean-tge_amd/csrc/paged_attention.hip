@@ -1058,31 +1058,34 @@ void paged_prefill_kernel(AttnParams p) {
 // the same launch by the last piece to arrive.
 // The two roles share the workgroup's LDS (a union) and its register budget.
 // ---------------------------------------------------------------------------
-template <int FMT, bool SF32, int D, int NRG>
+// SP: both roles apply the static sparse subset (the decode role reads
+// every page of its units, as the sparse decode kernel does for strides up
+// to 16).
+template <int FMT, bool SF32, int D, int NRG, bool SP = false>
 struct MixCfg {
-  using DC = DecodeCfg<FMT, SF32, D, NRG, false, true>;
+  using DC = DecodeCfg<FMT, SF32, D, NRG, SP, true>;
   static constexpr int WPE = DC::WPE;
 };
 
-template <int FMT, bool SF32, int D, int NRG>
-__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(MixCfg<FMT, SF32, D, NRG>::WPE,
-                                                                     MixCfg<FMT, SF32, D, NRG>::WPE)))
+template <int FMT, bool SF32, int D, int NRG, bool SP = false>
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(MixCfg<FMT, SF32, D, NRG, SP>::WPE,
+                                                                     MixCfg<FMT, SF32, D, NRG, SP>::WPE)))
 void paged_mixed_kernel(AttnParams dec, AttnParams pf, int n_dec) {
-  using DC = typename MixCfg<FMT, SF32, D, NRG>::DC;
-  constexpr int WPE = MixCfg<FMT, SF32, D, NRG>::WPE;
+  using DC = typename MixCfg<FMT, SF32, D, NRG, SP>::DC;
+  constexpr int WPE = MixCfg<FMT, SF32, D, NRG, SP>::WPE;
   static_assert(DC::W == 4, "both roles run 256 threads");
-  static_assert(DecodeShared<FMT, SF32, D, NRG, false, true>::MERGE_FLOATS >= 10 * 16 * NRG,
+  static_assert(DecodeShared<FMT, SF32, D, NRG, SP, true>::MERGE_FLOATS >= 10 * 16 * NRG,
                 "the decode merge area holds the split merge's scratch");
   static_assert(sizeof(PrefillShared<FMT, SF32, D, WPE>::ring) >= 10 * kPrefillRows * sizeof(float),
                 "the prefill ring holds the split merge's scratch");
   __shared__ union {
-    DecodeShared<FMT, SF32, D, NRG, false, true> d;
+    DecodeShared<FMT, SF32, D, NRG, SP, true> d;
     PrefillShared<FMT, SF32, D, WPE> p;
   } sh;
   if ((int)blockIdx.x < n_dec) {
-    decode_body<FMT, SF32, D, NRG, 4, WPE, false, true>(dec, sh.d, blockIdx.x);
+    decode_body<FMT, SF32, D, NRG, 4, WPE, SP, true>(dec, sh.d, blockIdx.x);
   } else {
-    prefill_body<FMT, SF32, D, WPE, false, true>(pf, sh.p, blockIdx.x - n_dec);
+    prefill_body<FMT, SF32, D, WPE, SP, true>(pf, sh.p, blockIdx.x - n_dec);
   }
 }
 
@@ -1357,8 +1360,12 @@ hipError_t launch_mixed_d(int row_groups, int n_dec, int n_pf, const AttnParams&
 #define TGE_MIX(n)                                                                                \
   case n:                                                                                         \
     if constexpr (n <= max_row_groups<D>()) {                                                     \
-      hipLaunchKernelGGL((paged_mixed_kernel<FMT, SF32, D, n>), grid, block, 0, stream, dec, pf,  \
-                         n_dec);                                                                  \
+      if (dec.sp_stride > 0)                                                                      \
+        hipLaunchKernelGGL((paged_mixed_kernel<FMT, SF32, D, n, true>), grid, block, 0, stream, dec, \
+                           pf, n_dec);                                                            \
+      else                                                                                        \
+        hipLaunchKernelGGL((paged_mixed_kernel<FMT, SF32, D, n>), grid, block, 0, stream, dec, pf, \
+                           n_dec);                                                                \
       break;                                                                                      \
     } else {                                                                                      \
       return hipErrorInvalidValue;                                                                \

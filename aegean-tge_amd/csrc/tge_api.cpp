@@ -173,7 +173,6 @@ struct tge_batch {
   // whose rows fit a decode unit, the prefill kernel over the others.
   AttnPlan mix_decode, mix_prefill;
   bool mix_built = false;
-  bool mix_one = false;  // dense: one paged_mixed_kernel launch, splits merged in it
   // arrival counters of the mixed launch: the decode plan's records, then
   // the prefill plan's (zero between launches)
   tge::plan::Scratch mix_counters;
@@ -882,31 +881,21 @@ int tge_batch_attention(const tge_batch* b, const tge_kv_pool* p, int layer, con
   hipStream_t st = static_cast<hipStream_t>(stream);
   const bool sparse = b->sp_stride > 0;
   if (!mb->mix_built || mb->mix_decode.sparse != sparse) {
-    // Built on first use after each plan, reused by every layer. Dense
-    // steps run as one launch (the decode shares balanced for the mixed
-    // kernel); a static sparse subset keeps the two kernels.
-    mb->mix_one = !sparse;
-    s = build_decode_plan(mb, p, mb->mix_decode, 1, st, mb->mix_one);
+    // Built on first use after each plan (and after the sparse setting
+    // changes), reused by every layer: one launch, the decode shares
+    // balanced for the mixed kernel.
+    s = build_decode_plan(mb, p, mb->mix_decode, 1, st, true);
     if (s != TGE_OK) return s;
     tge::plan::build_prefill(mb->step, device_cus(), mb->mix_prefill.lists, 2);
     s = upload_plan(mb->mix_prefill, b->step.block_dims, st);
     if (s != TGE_OK) return s;
-    if (mb->mix_one) {
-      const size_t n = mb->mix_decode.lists.reduce.size() + mb->mix_prefill.lists.reduce.size();
-      const size_t had = mb->mix_counters.bytes;
-      s = mb->mix_counters.reserve(g_mem, std::max<size_t>(n, 1) * sizeof(int), st);
-      if (s != TGE_OK) return s;
-      if (mb->mix_counters.bytes != had)
-        TGE_HIP(hipMemsetAsync(mb->mix_counters.dev, 0, mb->mix_counters.bytes, st));
-    }
-    mb->mix_built = true;
-  }
-  if (!b->mix_one) {
-    // Long chunks first: the prefill tiles are MFMA-bound, the persistent
-    // decode workgroups HBM-bound; both write disjoint rows of `out`.
-    s = run_attention(b, p, layer, q, out, stream, b->mix_prefill, false);
+    const size_t n = mb->mix_decode.lists.reduce.size() + mb->mix_prefill.lists.reduce.size();
+    const size_t had = mb->mix_counters.bytes;
+    s = mb->mix_counters.reserve(g_mem, std::max<size_t>(n, 1) * sizeof(int), st);
     if (s != TGE_OK) return s;
-    return run_attention(b, p, layer, q, out, stream, b->mix_decode, true);
+    if (mb->mix_counters.bytes != had)
+      TGE_HIP(hipMemsetAsync(mb->mix_counters.dev, 0, mb->mix_counters.bytes, st));
+    mb->mix_built = true;
   }
   // One launch: the decode shares first, then the prefill tiles; each
   // plan's split records are merged in the launch (arrival counters).

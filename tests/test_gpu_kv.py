@@ -657,7 +657,9 @@ def test_mixed_one_launch_split_merges_repeat(gpu, fmt):
     (tk.KV_I8, (20, 40, 17), "decode"),    # sink straddles a page; most middle pages kept
     (tk.KV_I8, (0, 48, 3), "decode"),
     (tk.KV_F16, (4, 64, 5), "prefill"),
-    (tk.KV_F16, (2, 80, 24), "mixed"),
+    (tk.KV_F16, (2, 80, 24), "mixed"),     # one launch: the sparse mixed kernel
+    (tk.KV_I8, (4, 64, 4), "mixed"),
+    (tk.KV_F16, (4, 100, 37), "mixed"),
 ])
 def test_static_sparse_attention(gpu, fmt, sparse, kind):
     """Static sparse attention (sink + strided middle + window, the kept set
