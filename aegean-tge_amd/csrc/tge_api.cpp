@@ -130,7 +130,10 @@ struct AttnPlan {
   tge::plan::AttnLists lists;
   bool built = false;
   bool sparse = false;  // decode lists balanced for the static sparse kernel
-  tge::plan::Staged image;  // work | reduce | wg_first
+  tge::plan::Staged image;  // work | reduce | wg_first (plans built after tge_batch_plan)
+  // Device base of the lists: `image`, or the batch image's region for the
+  // plans tge_batch_plan uploads with the step (one copy per step).
+  char* dev = nullptr;
   size_t off_reduce = 0;
   size_t off_first = 0;
   size_t off_app = 0;  // app_first, then app_recs (decode plans that store the new rows)
@@ -149,10 +152,9 @@ struct AttnPlan {
 struct StepPlan {
   tge::plan::StepLists lists;
   bool built = false;
-  tge::plan::Staged image;
+  char* dev = nullptr;  // records | first-batch page ids, in the batch image
   tge::plan::Scratch part_o, part_ml, counters;
   ~StepPlan() {
-    image.release(g_mem);
     part_o.release(g_mem);
     part_ml.release(g_mem);
     counters.release(g_mem);
@@ -347,8 +349,20 @@ void tge_batch_destroy(tge_batch* b) { delete b; }
 
 namespace {
 
-// Uploads an attention plan's lists and sizes its split-K partial buffers
-// (rows of the page blocks' width).
+// Sizes an attention plan's split-K partial buffers (rows of the page
+// blocks' width) once its lists are on the device at pl.dev.
+int finish_plan(AttnPlan& pl, int block_dims, hipStream_t st) {
+  const size_t rows_cap = 16 * (size_t)pl.lists.row_groups;
+  const size_t parts = (size_t)std::max(pl.lists.parts, 1);
+  int s = pl.part_o.reserve(g_mem, parts * rows_cap * block_dims * sizeof(float), st);
+  if (s == TGE_OK) s = pl.part_ml.reserve(g_mem, parts * rows_cap * 2 * sizeof(float), st);
+  if (s != TGE_OK) return s;
+  pl.built = true;
+  return TGE_OK;
+}
+
+// Uploads an attention plan's lists on their own (the plans built after
+// tge_batch_plan) and sizes its partial buffers.
 int upload_plan(AttnPlan& pl, int block_dims, hipStream_t st) {
   pl.built = false;
   const size_t total = tge::plan::image_layout(pl.lists, &pl.off_reduce, &pl.off_first, &pl.off_app);
@@ -356,13 +370,8 @@ int upload_plan(AttnPlan& pl, int block_dims, hipStream_t st) {
     tge::plan::write_image(pl.lists, pl.off_reduce, pl.off_first, h, pl.off_app);
   });
   if (s != TGE_OK) return s;
-  const size_t rows_cap = 16 * (size_t)pl.lists.row_groups;
-  const size_t parts = (size_t)std::max(pl.lists.parts, 1);
-  s = pl.part_o.reserve(g_mem, parts * rows_cap * block_dims * sizeof(float), st);
-  if (s == TGE_OK) s = pl.part_ml.reserve(g_mem, parts * rows_cap * 2 * sizeof(float), st);
-  if (s != TGE_OK) return s;
-  pl.built = true;
-  return TGE_OK;
+  pl.dev = pl.image.dev;
+  return finish_plan(pl, block_dims, st);
 }
 
 int device_cus() {
@@ -406,12 +415,12 @@ tge::plan::Residency resident_groups_mixed() {
   return tge::plan::Residency{cus, cus};
 }
 
-// Builds and uploads a decode plan over the sessions `only` selects
+// Builds the lists of a decode plan over the sessions `only` selects
 // (0 all, 1 those a decode unit holds), balanced for the decode kernel the
 // batch's current sparse setting launches (`mixed`: the decode role of the
 // mixed-step kernel).
-int build_decode_plan(tge_batch* b, const tge_kv_pool* p, AttnPlan& pl, int only, hipStream_t st,
-                      bool mixed = false) {
+void build_decode_lists(tge_batch* b, const tge_kv_pool* p, AttnPlan& pl, int only, bool mixed) {
+  pl.built = false;
   int max_rows = 0;
   for (const auto& sr : b->step.sessions)
     if (tge::plan::take_session(b->step, sr, only))
@@ -430,6 +439,12 @@ int build_decode_plan(tge_batch* b, const tge_kv_pool* p, AttnPlan& pl, int only
                                     tge::decode_app_waves(p->desc.format, sf32, b->step.block_dims, rg),
                                     tge::decode_app_rows(b->step.block_dims));
   pl.sparse = sparse;
+}
+
+// The same, uploaded on its own (a plan built after tge_batch_plan).
+int build_decode_plan(tge_batch* b, const tge_kv_pool* p, AttnPlan& pl, int only, hipStream_t st,
+                      bool mixed = false) {
+  build_decode_lists(b, p, pl, only, mixed);
   return upload_plan(pl, b->step.block_dims, st);
 }
 
@@ -437,24 +452,14 @@ int build_decode_plan(tge_batch* b, const tge_kv_pool* p, AttnPlan& pl, int only
 
 namespace {
 
-// The one-launch lists of a small decode step, uploaded with their partial
-// and counter buffers (counters zeroed when allocated).
-int upload_step_plan(tge_batch* b, const tge_kv_pool* pool, hipStream_t st) {
+// The partial and counter buffers of a small decode step's one-launch
+// lists, once the lists are on the device at sp.dev (counters zeroed when
+// allocated).
+int finish_step_plan(tge_batch* b, hipStream_t st) {
   StepPlan& sp = b->small;
-  sp.built = false;
-  if (!tge::plan::build_step_lists(b->step, pool->desc.format == TGE_KV_I8,
-                                   pool->desc.scale_format == TGE_SCALE_F32, sp.lists))
-    return TGE_OK;
   const auto& L = sp.lists;
-  // [ records | first-batch page ids ]
-  const size_t rbytes = L.recs.size() * sizeof(tge::StepRec);
-  const size_t ibytes = L.first_ids.size() * sizeof(int);
-  int s = sp.image.upload(g_mem, rbytes + ibytes, st, [&](char* h) {
-    std::memcpy(h, L.recs.data(), rbytes);
-    std::memcpy(h + rbytes, L.first_ids.data(), ibytes);
-  });
-  if (s != TGE_OK) return s;
   const size_t rows_cap = 16 * (size_t)L.row_groups;
+  int s = TGE_OK;
   const size_t parts = (size_t)std::max(L.parts, 1);
   s = sp.part_o.reserve(g_mem, parts * rows_cap * b->step.block_dims * sizeof(float), st);
   if (s == TGE_OK) s = sp.part_ml.reserve(g_mem, parts * rows_cap * 2 * sizeof(float), st);
@@ -488,27 +493,52 @@ int tge_batch_plan(tge_batch* b, const tge_kv_pool* pool, const tge_batch_desc* 
   b->mix_built = false;
 
   hipStream_t hs = static_cast<hipStream_t>(stream);
+  // The step's lists are built on the host first and go up in one copy:
+  // [ sessions | tables | rows | decode lists | step records | first-batch
+  // page ids ]. Decode lists are built eagerly when the rows fit a decode
+  // unit (the common case: one upload per step serves every layer).
+  const bool dec = st.max_rows <= tge::max_unit_rows(st.block_dims);
+  if (dec) build_decode_lists(b, pool, b->decode, 0, false);
+  b->small.built = false;
+  const bool small = tge::plan::build_step_lists(st, pool->desc.format == TGE_KV_I8,
+                                                 pool->desc.scale_format == TGE_SCALE_F32,
+                                                 b->small.lists);
+  const auto& SL = b->small.lists;
   const size_t o_sess = 0;
   const size_t o_tab = align_up(o_sess + st.sessions.size() * sizeof(tge::SessionRec));
   const size_t o_rows = align_up(o_tab + st.tables.size() * sizeof(int));
-  const size_t total = o_rows + st.rows.size() * sizeof(tge::RowRec);
+  const size_t o_dec = align_up(o_rows + st.rows.size() * sizeof(tge::RowRec));
+  AttnPlan& dp = b->decode;
+  const size_t dec_bytes =
+      dec ? tge::plan::image_layout(dp.lists, &dp.off_reduce, &dp.off_first, &dp.off_app) : 0;
+  const size_t o_step = align_up(o_dec + dec_bytes);
+  const size_t rbytes = small ? SL.recs.size() * sizeof(tge::StepRec) : 0;
+  const size_t ibytes = small ? SL.first_ids.size() * sizeof(int) : 0;
+  const size_t total = o_step + rbytes + ibytes;
   s = b->image.upload(g_mem, total, hs, [&](char* h) {
     std::memcpy(h + o_sess, st.sessions.data(), st.sessions.size() * sizeof(tge::SessionRec));
     if (!st.tables.empty()) std::memcpy(h + o_tab, st.tables.data(), st.tables.size() * sizeof(int));
     std::memcpy(h + o_rows, st.rows.data(), st.rows.size() * sizeof(tge::RowRec));
+    if (dec) tge::plan::write_image(dp.lists, dp.off_reduce, dp.off_first, h + o_dec, dp.off_app);
+    if (small) {
+      std::memcpy(h + o_step, SL.recs.data(), rbytes);
+      std::memcpy(h + o_step + rbytes, SL.first_ids.data(), ibytes);
+    }
   });
   if (s != TGE_OK) return s;
   b->off_sessions = o_sess;
   b->off_tables = o_tab;
   b->off_rows = o_rows;
-  // Decode lists are built eagerly when the rows fit a decode unit (the
-  // common case: one upload per step serves every layer).
-  if (st.max_rows <= tge::max_unit_rows(st.block_dims)) {
-    s = build_decode_plan(b, pool, b->decode, 0, hs);
+  if (dec) {
+    dp.dev = b->image.dev + o_dec;
+    s = finish_plan(dp, st.block_dims, hs);
     if (s != TGE_OK) return s;
   }
-  s = upload_step_plan(b, pool, hs);
-  if (s != TGE_OK) return s;
+  if (small) {
+    b->small.dev = b->image.dev + o_step;
+    s = finish_step_plan(b, hs);
+    if (s != TGE_OK) return s;
+  }
   b->planned = true;
   return TGE_OK;
 }
@@ -602,8 +632,8 @@ tge::AttnParams attn_params(const tge_batch* b, const tge_kv_pool* p, int layer,
   a.pool = v.k;
   a.block_bytes = (uint32_t)p->geom.block_bytes;
   a.sessions = reinterpret_cast<const tge::SessionRec*>(b->image.dev + b->off_sessions);
-  a.work = reinterpret_cast<const tge::WorkRec*>(pl.image.dev);
-  a.wg_first = pl.lists.wg_first.empty() ? nullptr : reinterpret_cast<const int*>(pl.image.dev + pl.off_first);
+  a.work = reinterpret_cast<const tge::WorkRec*>(pl.dev);
+  a.wg_first = pl.lists.wg_first.empty() ? nullptr : reinterpret_cast<const int*>(pl.dev + pl.off_first);
   a.tables = reinterpret_cast<const int*>(b->image.dev + b->off_tables);
   a.sp_sink = b->sp_sink;
   a.sp_window = b->sp_window;
@@ -653,7 +683,7 @@ int run_attention(const tge_batch* b, const tge_kv_pool* p, int layer, const flo
   if (app_k) {
     a.app_k = app_k;
     a.app_v = app_v;
-    a.app_first = reinterpret_cast<const int*>(pl.image.dev + pl.off_app);
+    a.app_first = reinterpret_cast<const int*>(pl.dev + pl.off_app);
     a.app_recs = a.app_first + pl.lists.app_first.size();
   }
   std::array<hipEvent_t, 3>* ev = nullptr;
@@ -675,7 +705,7 @@ int run_attention(const tge_batch* b, const tge_kv_pool* p, int layer, const flo
   }
   if (merge_kernel) {
     tge::ReduceParams r{};
-    r.items = reinterpret_cast<const tge::ReduceRec*>(pl.image.dev + pl.off_reduce);
+    r.items = reinterpret_cast<const tge::ReduceRec*>(pl.dev + pl.off_reduce);
     r.part_o = reinterpret_cast<const float*>(pl.part_o.dev);
     r.part_ml = reinterpret_cast<const float*>(pl.part_ml.dev);
     r.out = out;
@@ -830,8 +860,8 @@ int tge_decode_step(const tge_batch* b, tge_kv_pool* p, int layer, const float* 
   a.app.dims = b->step.head_dim;
   a.app.scale_f32 = p->desc.scale_format == TGE_SCALE_F32;
   a.app.q_heads = b->step.q_heads;
-  a.recs = reinterpret_cast<const tge::StepRec*>(sp.image.dev);
-  a.first_ids = reinterpret_cast<const int*>(sp.image.dev + sp.lists.recs.size() * sizeof(tge::StepRec));
+  a.recs = reinterpret_cast<const tge::StepRec*>(sp.dev);
+  a.first_ids = reinterpret_cast<const int*>(sp.dev + sp.lists.recs.size() * sizeof(tge::StepRec));
   a.tables = reinterpret_cast<const int*>(b->image.dev + b->off_tables);
   a.q = q;
   a.out = out;
@@ -902,9 +932,9 @@ int tge_batch_attention(const tge_batch* b, const tge_kv_pool* p, int layer, con
   tge::AttnParams dec = attn_params(b, p, layer, q, out, b->mix_decode);
   tge::AttnParams pf = attn_params(b, p, layer, q, out, b->mix_prefill);
   int* counters = reinterpret_cast<int*>(b->mix_counters.dev);
-  dec.reduce = reinterpret_cast<const tge::ReduceRec*>(b->mix_decode.image.dev + b->mix_decode.off_reduce);
+  dec.reduce = reinterpret_cast<const tge::ReduceRec*>(b->mix_decode.dev + b->mix_decode.off_reduce);
   dec.counters = counters;
-  pf.reduce = reinterpret_cast<const tge::ReduceRec*>(b->mix_prefill.image.dev + b->mix_prefill.off_reduce);
+  pf.reduce = reinterpret_cast<const tge::ReduceRec*>(b->mix_prefill.dev + b->mix_prefill.off_reduce);
   pf.counters = counters + b->mix_decode.lists.reduce.size();
   std::array<hipEvent_t, 3>* ev = nullptr;
   s = profile_events(mb, &ev);
