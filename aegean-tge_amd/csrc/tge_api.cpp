@@ -92,15 +92,25 @@ struct HipMem final : tge::plan::MemOps {
     return fail(e == hipErrorOutOfMemory ? TGE_ERR_CAPACITY : TGE_ERR_DEVICE,
                 std::string(what) + ": " + hipGetErrorString(e));
   }
+  // (coherent: the plan upload kernel reads it over the bus)
   int host_alloc(char** p, size_t n) override {
-    return status(hipHostMalloc(reinterpret_cast<void**>(p), n), "hipHostMalloc");
+    return status(hipHostMalloc(reinterpret_cast<void**>(p), n, hipHostMallocCoherent),
+                  "hipHostMalloc");
   }
   void host_free(char* p) override { (void)hipHostFree(p); }
   int dev_alloc(char** p, size_t n) override {
     return status(hipMalloc(reinterpret_cast<void**>(p), n), "hipMalloc");
   }
   void dev_free(char* p) override { (void)hipFree(p); }
+  // A kernel copies the pinned staging buffer (no DMA-engine hand-offs on
+  // the launch stream); where the runtime gives no device address for it,
+  // a DMA copy.
   int copy_to_device(char* d, const char* h, size_t n, void* st) override {
+    void* hd = nullptr;
+    if (hipHostGetDevicePointer(&hd, const_cast<char*>(h), 0) == hipSuccess && hd)
+      return status(tge::launch_upload(d, static_cast<const char*>(hd), n, static_cast<hipStream_t>(st)),
+                    "plan upload");
+    (void)hipGetLastError();  // (clear the failed lookup)
     return status(hipMemcpyAsync(d, h, n, hipMemcpyHostToDevice, static_cast<hipStream_t>(st)),
                   "hipMemcpyAsync");
   }

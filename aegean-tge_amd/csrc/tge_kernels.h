@@ -172,6 +172,9 @@ hipError_t launch_reduce(int head_dim, int n_items, int max_parts, const ReduceP
                          hipStream_t stream);
 // Expiries of the kernels' bounded waits since the process started (a
 // synchronous read of the device counter).
+// Copies n bytes of a pinned host buffer (its device address) to device
+// memory on `stream` with a kernel (system-coherent loads).
+hipError_t launch_upload(char* dst, const char* src_dev, size_t n, hipStream_t stream);
 hipError_t read_wait_expiries(unsigned int* out);
 // Read-only streaming of `bytes` (pattern 0: 4 KiB chunks over the grid;
 // 1: scattered blocks of block_bytes <= 17 KiB, one wave each).
