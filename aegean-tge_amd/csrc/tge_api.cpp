@@ -504,11 +504,21 @@ int tge_batch_plan(tge_batch* b, const tge_kv_pool* pool, const tge_batch_desc* 
 
   hipStream_t hs = static_cast<hipStream_t>(stream);
   // The step's lists are built on the host first and go up in one copy:
-  // [ sessions | tables | rows | decode lists | step records | first-batch
-  // page ids ]. Decode lists are built eagerly when the rows fit a decode
-  // unit (the common case: one upload per step serves every layer).
+  // [ sessions | tables | rows | attention lists | step records |
+  // first-batch page ids ]. The attention lists are the decode lists when
+  // every session's rows fit a decode unit (one upload per step serves every
+  // layer), the block-prefill lists when none does (a prompt chunk); a step
+  // mixing both builds its plans on first use.
   const bool dec = st.max_rows <= tge::max_unit_rows(st.block_dims);
+  bool pre = !dec;
+  for (const auto& sr : st.sessions) pre = pre && !tge::plan::decode_session(st, sr);
   if (dec) build_decode_lists(b, pool, b->decode, 0, false);
+  if (pre) {
+    b->prefill.built = false;
+    tge::plan::build_prefill(st, device_cus(), b->prefill.lists, 0,
+                             tge::prefill_halves(pool->desc.format, st.block_dims),
+                             pool->desc.format == TGE_KV_I8);
+  }
   b->small.built = false;
   const bool small = tge::plan::build_step_lists(st, pool->desc.format == TGE_KV_I8,
                                                  pool->desc.scale_format == TGE_SCALE_F32,
@@ -518,9 +528,10 @@ int tge_batch_plan(tge_batch* b, const tge_kv_pool* pool, const tge_batch_desc* 
   const size_t o_tab = align_up(o_sess + st.sessions.size() * sizeof(tge::SessionRec));
   const size_t o_rows = align_up(o_tab + st.tables.size() * sizeof(int));
   const size_t o_dec = align_up(o_rows + st.rows.size() * sizeof(tge::RowRec));
-  AttnPlan& dp = b->decode;
+  AttnPlan& dp = dec ? b->decode : b->prefill;  // (the eager attention plan, if any)
+  const bool eager = dec || pre;
   const size_t dec_bytes =
-      dec ? tge::plan::image_layout(dp.lists, &dp.off_reduce, &dp.off_first, &dp.off_app) : 0;
+      eager ? tge::plan::image_layout(dp.lists, &dp.off_reduce, &dp.off_first, &dp.off_app) : 0;
   const size_t o_step = align_up(o_dec + dec_bytes);
   const size_t rbytes = small ? SL.recs.size() * sizeof(tge::StepRec) : 0;
   const size_t ibytes = small ? SL.first_ids.size() * sizeof(int) : 0;
@@ -529,7 +540,7 @@ int tge_batch_plan(tge_batch* b, const tge_kv_pool* pool, const tge_batch_desc* 
     std::memcpy(h + o_sess, st.sessions.data(), st.sessions.size() * sizeof(tge::SessionRec));
     if (!st.tables.empty()) std::memcpy(h + o_tab, st.tables.data(), st.tables.size() * sizeof(int));
     std::memcpy(h + o_rows, st.rows.data(), st.rows.size() * sizeof(tge::RowRec));
-    if (dec) tge::plan::write_image(dp.lists, dp.off_reduce, dp.off_first, h + o_dec, dp.off_app);
+    if (eager) tge::plan::write_image(dp.lists, dp.off_reduce, dp.off_first, h + o_dec, dp.off_app);
     if (small) {
       std::memcpy(h + o_step, SL.recs.data(), rbytes);
       std::memcpy(h + o_step + rbytes, SL.first_ids.data(), ibytes);
@@ -539,7 +550,7 @@ int tge_batch_plan(tge_batch* b, const tge_kv_pool* pool, const tge_batch_desc* 
   b->off_sessions = o_sess;
   b->off_tables = o_tab;
   b->off_rows = o_rows;
-  if (dec) {
+  if (eager) {
     dp.dev = b->image.dev + o_dec;
     s = finish_plan(dp, st.block_dims, hs);
     if (s != TGE_OK) return s;
