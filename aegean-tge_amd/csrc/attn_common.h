@@ -82,7 +82,7 @@ struct PageRegs {
 };
 
 // Buffer resource of one page block (64-bit base, so a layer's array may
-// exceed 4 GiB). Loads add the lane's chunk offset (VGPR); offsets past the
+// exceed 4 GiB). Loads add the lane's piece offset (VGPR); offsets past the
 // block read zeros instead of faulting.
 [[maybe_unused]] __device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void* base,
                                                                          uint32_t bytes) {
@@ -167,7 +167,7 @@ __device__ __forceinline__ void fetch_page(char* slot, const char* block, uint32
 #endif
 }
 
-// Read a landed page back into registers (the lane's own chunk and its
+// Read a landed page back into registers (the lane's own pieces and its
 // group's scales): the K half (K codes and scales) and the V half, so a
 // consumer can hold only the half it is using.
 template <int FMT, bool SF32, int D, bool V>

@@ -17,8 +17,9 @@
 // once for the group), prefill packs the query group of consecutive
 // queries. A page block (16 tokens of one KV head: K, V and int8 scales, one
 // contiguous run of HBM) is fetched straight into LDS by 16-byte
-// buffer_load ... lds instructions, one contiguous chunk per lane (layout in
-// tge_common.h), and read back into the lane's MFMA operand registers.
+// buffer_load ... lds instructions, each covering a contiguous KiB (piece i
+// of every lane; layout in tge_common.h), and read back into the lane's MFMA
+// operand registers.
 //
 // Per page, per 16-row group, per wave (lane = group g 0..3, column c 0..15):
 //   S^T[token][row] = K (16 x D) . Q^T: one v_mfma_f32_16x16x32_f16 per 32-dim
