@@ -918,10 +918,10 @@ __device__ __forceinline__ void prefill_body(const AttnParams& p,
 
   // Last tile holding a page of this wave.
   const int t_last = wave < npages ? (npages - 1 - wave) / kWaves : -1;
-  for (int k = 0; k < ntiles; ++k) {
-    // this wave's page of tile k has landed (its pages of up to NB - 2
-    // younger tiles may still be in flight), then every wave's has, and
-    // every wave is done with tile k - 1, whose slot the fetch below refills
+  // Start of tile k: this wave's page of it has landed (its pages of up to
+  // NB - 2 younger tiles may still be in flight), then every wave's has, and
+  // every wave is done with tile k - 1, whose slot the fetch refills.
+  auto tile_sync = [&](int k) __attribute__((always_inline)) {
     if (k <= t_last) {
       const int younger = (k + NB - 2 < t_last ? k + NB - 2 : t_last) - k;
       wait_vmcnt_pages<NB - 2, RG::LOADS>(younger);
@@ -932,7 +932,38 @@ __device__ __forceinline__ void prefill_body(const AttnParams& p,
       lds_barrier();
     }
     if (k + NB - 1 < ntiles) fetch_tile(k + NB - 1);
-    if (has_rows) {
+  };
+  const auto qf = [&](int rg, int pp) __attribute__((always_inline)) { return u.qop(rg, pp); };
+  // Pages j and j + 1 of the tile in LDS at `tile` (logical page pi first).
+  auto pair = [&](const char* tile, int j, int pi) __attribute__((always_inline)) {
+    if constexpr (FMT == kF16) {
+      u.consume2_slots(tile + j * RG::SLOT, tile + (j + 1) * RG::SLOT, lane, pi, pi + 1, grp,
+                       pi >= unmasked, pi + 1 >= unmasked, qf);
+    } else {
+      Regs ra, rb;
+      read_page<FMT, SF32, D>(ra, tile + j * RG::SLOT, lane, grp);
+      read_page<FMT, SF32, D>(rb, tile + (j + 1) * RG::SLOT, lane, grp);
+      u.consume2(ra, rb, pi, pi + 1, grp, pi >= unmasked, pi + 1 >= unmasked, qf);
+    }
+  };
+  // Tiles whose four pages all lie in the range take a straight path with
+  // no per-page range test (the accumulators then keep their registers
+  // from one page pair to the next, with no copies between them); the
+  // last, partial tile and static sparse subsets take the general one.
+  const int nfull = SP ? 0 : npages / kWaves;
+  if (!has_rows) {
+    for (int k = 0; k < ntiles; ++k) tile_sync(k);
+  } else {
+    int k = 0;
+    for (; k < nfull; ++k) {
+      tile_sync(k);
+      const char* tile = ring + (k % NB) * SH::TILE;
+      const int pi = first_page + k * kWaves;
+      pair(tile, 0, pi);
+      pair(tile, 2, pi + 2);
+    }
+    for (; k < ntiles; ++k) {
+      tile_sync(k);
       const char* tile = ring + (k % NB) * SH::TILE;
 #pragma unroll
       for (int j = 0; j < kWaves; j += 2) {
@@ -946,16 +977,7 @@ __device__ __forceinline__ void prefill_body(const AttnParams& p,
                                      first_page + k * kWaves + jj >= unmasked);
           }
         } else if (pg + 1 < npages) {
-          const auto qf = [&](int rg, int pp) __attribute__((always_inline)) { return u.qop(rg, pp); };
-          if constexpr (FMT == kF16) {
-            u.consume2_slots(tile + j * RG::SLOT, tile + (j + 1) * RG::SLOT, lane, pi, pi + 1, grp,
-                             pi >= unmasked, pi + 1 >= unmasked, qf);
-          } else {
-            Regs ra, rb;
-            read_page<FMT, SF32, D>(ra, tile + j * RG::SLOT, lane, grp);
-            read_page<FMT, SF32, D>(rb, tile + (j + 1) * RG::SLOT, lane, grp);
-            u.consume2(ra, rb, pi, pi + 1, grp, pi >= unmasked, pi + 1 >= unmasked, qf);
-          }
+          pair(tile, j, pi);
         } else if (pg < npages) {
           Regs r;
           read_page<FMT, SF32, D>(r, tile + j * RG::SLOT, lane, grp);
