@@ -277,7 +277,7 @@ int tge_kv_pool_create(const tge_kv_pool_desc* desc, tge_kv_pool** out) {
   if (tge::block_dims_for(d.head_dim, d.format) == 0)
     return fail(TGE_ERR_INVALID, d.format == TGE_KV_I8
                                      ? "kv_pool_create: int8 head_dim must be a multiple of 32 up to 256"
-                                     : "kv_pool_create: head_dim must be a multiple of 16 up to 256");
+                                     : "kv_pool_create: head_dim must be a multiple of 8 up to 256");
   if (d.format == TGE_KV_I8 && d.scale_format != TGE_SCALE_F16 &&
       d.scale_format != TGE_SCALE_F32)
     return fail(TGE_ERR_INVALID, "kv_pool_create: unknown scale format");
@@ -770,6 +770,10 @@ int tge_kv_append_rope(const tge_batch* b, tge_kv_pool* p, int layer,
   if (!r || !r->k || !r->v || !r->rope_cos || !r->rope_sin)
     return fail(TGE_ERR_INVALID, "kv_append_rope: null k/v/tables");
   if (r->q && !r->q_out) return fail(TGE_ERR_INVALID, "kv_append_rope: q without q_out");
+  // (a lane rotates 8 dims against the 8 half a head away: the halves must
+  // be whole runs of 8)
+  if (b->step.head_dim % 16 != 0)
+    return fail(TGE_ERR_INVALID, "kv_append_rope: head_dim must be a multiple of 16");
   int max_pos = -1;
   for (const auto& row : b->step.rows) max_pos = std::max(max_pos, row.pos);
   if (max_pos >= r->rope_positions)

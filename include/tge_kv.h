@@ -88,7 +88,7 @@ const char* tge_backend_arch(void);
  * Element (token t, dim d) of a block's part sits at:
  *   K: tge_kv_k_index(t, d, format)  V: tge_kv_v_index(t, d, format)
  *   scale of (t, block b = d/32): tge_kv_scale_index(t, b, W)
- * head_dim: a multiple of 16 up to 256 (F16) or of 32 up to 256 (I8, whose
+ * head_dim: a multiple of 8 up to 256 (F16) or of 32 up to 256 (I8, whose
  * scales cover 32-dim blocks). The reference takes any head_dim > 0
  * (attention_scalar.cpp:11-14; int8 % 32, qwen2.cpp:406-409); heads wider
  * than 256 are not supported here. q, k, v and out rows always have the
@@ -397,7 +397,9 @@ int tge_attention_group(const tge_attention_group_args* args, void* stream);
  * apply_rope(k) (NeoX halves, qwen2.cpp:1196-1230); store k and v. One
  * launch does it for every row of the plan; the rotated q goes to q_out
  * (which may be q itself) for the attention call. Row i's position is its
- * plan position (ctx + j of its session) and indexes the tables.
+ * plan position (ctx + j of its session) and indexes the tables. head_dim
+ * must be a multiple of 16 here (TGE_ERR_INVALID otherwise): each NeoX
+ * half is whole runs of 8 dims.
  * ------------------------------------------------------------------------ */
 typedef struct {
   const float* q;        /* [rows][q_heads*head_dim] or NULL (K/V only) */

@@ -556,7 +556,8 @@ def test_append_rope_bitexact(gpu, fmt, sf, kvh, hd, fma):
 
 def test_append_rope_checks(gpu):
     """Argument checks of the fused append: tables must cover every position
-    of the plan; q needs q_out; no bias and no q are allowed (K/V only)."""
+    of the plan; q needs q_out; no bias and no q are allowed (K/V only); a
+    head size off the 16-dim grid is refused."""
     case = PagedCase(14, 2, 64, tk.KV_F16, [20], [2], seed=3)
     b = tk.Batch().plan(case.pool, case.sessions(True), 14)
     k = tk.DeviceArray.from_numpy(np.ones((2, 128), np.float32))
@@ -572,6 +573,18 @@ def test_append_rope_checks(gpu):
     tk.hip().sync()
     gk, gv, _, _ = b.gather(case.pool, 0, 0, 22)
     assert np.array_equal(gk[20:], O.float_to_half(np.ones((2, 128), np.float32)))
+    b.close()
+    case.close()
+    # a head off the 16-dim grid (a pool takes multiples of 8): the NeoX
+    # halves are not whole runs of 8, so the fused append refuses it
+    case = PagedCase(14, 2, 72, tk.KV_F16, [20], [2], seed=3)
+    b = tk.Batch().plan(case.pool, case.sessions(True), 14)
+    k = tk.DeviceArray.from_numpy(np.ones((2, 144), np.float32))
+    c = tk.DeviceArray.from_numpy(np.ones((22, 36), np.float32))
+    s = tk.DeviceArray.from_numpy(np.zeros((22, 36), np.float32))
+    with pytest.raises(tk.TgeError) as e:
+        b.append_rope(case.pool, 0, tk.rope_args(k, k, c, s, 22))
+    assert e.value.status == tk.ERR_INVALID
     b.close()
     case.close()
 
@@ -754,11 +767,16 @@ HEAD_SIZES = {
     "f16_d112_g4": (16, 4, 112, tk.KV_F16, 0),
     "f16_d48_g8": (8, 1, 48, tk.KV_F16, 0),
     "f16_d16": (4, 2, 16, tk.KV_F16, 0),
+    # off the 16-dim grid (f16 heads are multiples of 8)
+    "f16_d72": (14, 2, 72, tk.KV_F16, 0),
+    "f16_d120_g4": (16, 4, 120, tk.KV_F16, 0),
+    "f16_d8": (4, 2, 8, tk.KV_F16, 0),
     "i8_d96_f16scales": (12, 2, 96, tk.KV_I8, tk.SCALE_F16),
     "i8_d32_f32scales": (8, 4, 32, tk.KV_I8, tk.SCALE_F32),
     # 256-dim blocks (one wave per SIMD in decode and prefill)
     "f16_d256_g8": (16, 2, 256, tk.KV_F16, 0),
     "f16_d192_g4": (8, 2, 192, tk.KV_F16, 0),
+    "f16_d200": (8, 2, 200, tk.KV_F16, 0),
     "i8_d256_f16scales": (8, 2, 256, tk.KV_I8, tk.SCALE_F16),
     "i8_d160_f32scales_g8": (8, 1, 160, tk.KV_I8, tk.SCALE_F32),
 }
