@@ -134,5 +134,16 @@ __device__ __forceinline__ void load8(float (&x)[8], const float* src) {
   x[4] = f1.x; x[5] = f1.y; x[6] = f1.z; x[7] = f1.w;
 }
 
+// Dims d0 .. d0 + 7 of one head's row (d0 a multiple of 8): the dims from
+// `dims` on read as zeros and are never loaded. Head sizes are multiples
+// of 4, so each run of 4 lies wholly inside or outside the head.
+__device__ __forceinline__ void load8_head(float (&x)[8], const float* head_row, int d0, int dims) {
+  const float4 z = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+  const float4 f0 = d0 < dims ? *reinterpret_cast<const float4*>(head_row + d0) : z;
+  const float4 f1 = d0 + 4 < dims ? *reinterpret_cast<const float4*>(head_row + d0 + 4) : z;
+  x[0] = f0.x; x[1] = f0.y; x[2] = f0.z; x[3] = f0.w;
+  x[4] = f1.x; x[5] = f1.y; x[6] = f1.z; x[7] = f1.w;
+}
+
 }  // namespace
 }  // namespace tge

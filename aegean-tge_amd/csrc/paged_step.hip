@@ -219,14 +219,8 @@ __global__ __launch_bounds__(64 * kStepWaves) void paged_step_kernel(StepParams 
     const int pos = rec.ctx + j;
     jb.rr = RowRec{p.tables[rec.table_off + pos / 16], pos % 16, pos};
     const int d0 = jb.b * 32 + jb.quarter * 8;  // (dims past the head's own store zeros)
-    const size_t off = (size_t)(rec.q_row + j) * kv_dim + rec.kv_head * dims + (d0 < dims ? d0 : 0);
-    const float* ks = kbase + off;
-    const float* vs = vbase + off;
-    load8(jb.x, jb.which ? vs : ks);
-    if (d0 >= dims) {
-#pragma unroll
-      for (int i = 0; i < 8; ++i) jb.x[i] = 0.0f;
-    }
+    const size_t off = (size_t)(rec.q_row + j) * kv_dim + rec.kv_head * dims;
+    load8_head(jb.x, (jb.which ? vbase : kbase) + off, d0, dims);
   };
   Job job;
   if (lanes > 0) fetch_job(0, job);

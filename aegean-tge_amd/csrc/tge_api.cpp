@@ -277,7 +277,7 @@ int tge_kv_pool_create(const tge_kv_pool_desc* desc, tge_kv_pool** out) {
   if (tge::block_dims_for(d.head_dim, d.format) == 0)
     return fail(TGE_ERR_INVALID, d.format == TGE_KV_I8
                                      ? "kv_pool_create: int8 head_dim must be a multiple of 32 up to 256"
-                                     : "kv_pool_create: head_dim must be a multiple of 8 up to 256");
+                                     : "kv_pool_create: head_dim must be a multiple of 4 up to 256");
   if (d.format == TGE_KV_I8 && d.scale_format != TGE_SCALE_F16 &&
       d.scale_format != TGE_SCALE_F32)
     return fail(TGE_ERR_INVALID, "kv_pool_create: unknown scale format");

@@ -31,11 +31,12 @@ struct BlockGeom {
 // stored in 64-dim blocks, up to 128 in 128-dim blocks, up to 256 in
 // 256-dim blocks, the dims from head_dim on holding zeros (so scores and
 // values are those of the head's own dims). A head size must be a positive
-// multiple of 8 (int8: of 32, the quantizer's block) of at most 256; 0 for
+// multiple of 4 (int8: of 32, the quantizer's block) of at most 256; 0 for
 // any other. Every kernel reads and writes the head's own dims of q, k, v
-// and out in runs of 4 or 8 that lie wholly inside or outside them.
+// and out in 16-byte runs of 4 that lie wholly inside or outside them (the
+// rows stay 16-byte aligned).
 __host__ __device__ inline int block_dims_for(int head_dim, int format) {
-  if (head_dim <= 0 || head_dim > 256 || head_dim % (format == kI8 ? 32 : 8) != 0) return 0;
+  if (head_dim <= 0 || head_dim > 256 || head_dim % (format == kI8 ? 32 : 4) != 0) return 0;
   return head_dim <= 64 ? 64 : head_dim <= 128 ? 128 : 256;
 }
 

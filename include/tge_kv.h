@@ -88,7 +88,7 @@ const char* tge_backend_arch(void);
  * Element (token t, dim d) of a block's part sits at:
  *   K: tge_kv_k_index(t, d, format)  V: tge_kv_v_index(t, d, format)
  *   scale of (t, block b = d/32): tge_kv_scale_index(t, b, W)
- * head_dim: a multiple of 8 up to 256 (F16) or of 32 up to 256 (I8, whose
+ * head_dim: a multiple of 4 up to 256 (F16) or of 32 up to 256 (I8, whose
  * scales cover 32-dim blocks). The reference takes any head_dim > 0
  * (attention_scalar.cpp:11-14; int8 % 32, qwen2.cpp:406-409); heads wider
  * than 256 are not supported here. q, k, v and out rows always have the

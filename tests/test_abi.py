@@ -70,10 +70,10 @@ def test_kernel_timing_argument_checks(tk):
 def test_pool_argument_checks(tk):
     h = C.c_void_p()
     # (layers, pages, kv_heads, head_dim, format, scale format); head sizes
-    # off the 8-dim grid (f16) or the 32-dim quantizer blocks (int8), or
+    # off the 4-dim grid (f16) or the 32-dim quantizer blocks (int8), or
     # wider than 256 dims, are rejected
-    for desc in [(0, 4, 1, 64, 1, 0), (1, 4, 1, 68, 1, 0), (1, 4, 1, 4, 1, 0),
-                 (1, 4, 1, 252, 1, 0), (1, 4, 1, 72, 2, 0), (1, 4, 1, 264, 1, 0),
+    for desc in [(0, 4, 1, 64, 1, 0), (1, 4, 1, 66, 1, 0), (1, 4, 1, 2, 1, 0),
+                 (1, 4, 1, 254, 1, 0), (1, 4, 1, 72, 2, 0), (1, 4, 1, 264, 1, 0),
                  (1, 4, 1, 272, 1, 0), (1, 4, 1, 512, 1, 0), (1, 4, 1, 0, 1, 0),
                  (1, 4, 1, -16, 1, 0), (1, 4, 1, 80, 2, 0), (1, 4, 1, 48, 2, 1),
                  (1, 4, 1, 240, 2, 0), (1, 4, 1, 64, 7, 0), (1, 4, 1, 64, 2, 9),
@@ -86,11 +86,11 @@ def test_pool_argument_checks(tk):
 
 
 def test_pool_accepts_head_sizes_between_the_block_widths(tk):
-    # f16: any multiple of 8 up to 256; int8: multiples of 32. Without a
+    # f16: any multiple of 4 up to 256; int8: multiples of 32. Without a
     # GPU the call gets past the argument checks and reports the backend.
     h = C.c_void_p()
-    for hd, fmt in [(8, 1), (16, 1), (48, 1), (72, 1), (80, 1), (96, 1), (112, 1), (120, 1),
-                    (144, 1), (200, 1), (248, 1), (256, 1), (32, 2),
+    for hd, fmt in [(4, 1), (8, 1), (16, 1), (48, 1), (68, 1), (72, 1), (80, 1), (96, 1),
+                    (100, 1), (112, 1), (120, 1), (144, 1), (200, 1), (252, 1), (256, 1), (32, 2),
                     (96, 2), (160, 2), (256, 2)]:
         d = tk.PoolDesc(1, 4, 1, hd, fmt, 0)
         st = tk.lib().tge_kv_pool_create(C.byref(d), C.byref(h))

@@ -575,7 +575,7 @@ def test_append_rope_checks(gpu):
     assert np.array_equal(gk[20:], O.float_to_half(np.ones((2, 128), np.float32)))
     b.close()
     case.close()
-    # a head off the 16-dim grid (a pool takes multiples of 8): the NeoX
+    # a head off the 16-dim grid (a pool takes multiples of 4): the NeoX
     # halves are not whole runs of 8, so the fused append refuses it
     case = PagedCase(14, 2, 72, tk.KV_F16, [20], [2], seed=3)
     b = tk.Batch().plan(case.pool, case.sessions(True), 14)
@@ -767,16 +767,18 @@ HEAD_SIZES = {
     "f16_d112_g4": (16, 4, 112, tk.KV_F16, 0),
     "f16_d48_g8": (8, 1, 48, tk.KV_F16, 0),
     "f16_d16": (4, 2, 16, tk.KV_F16, 0),
-    # off the 16-dim grid (f16 heads are multiples of 8)
+    # off the 16-dim grid (f16 heads are multiples of 4; 16-byte runs of q,
+    # k, v and out rows past the head's end are never read or written)
     "f16_d72": (14, 2, 72, tk.KV_F16, 0),
+    "f16_d100": (14, 2, 100, tk.KV_F16, 0),
     "f16_d120_g4": (16, 4, 120, tk.KV_F16, 0),
-    "f16_d8": (4, 2, 8, tk.KV_F16, 0),
+    "f16_d4": (4, 2, 4, tk.KV_F16, 0),
     "i8_d96_f16scales": (12, 2, 96, tk.KV_I8, tk.SCALE_F16),
     "i8_d32_f32scales": (8, 4, 32, tk.KV_I8, tk.SCALE_F32),
     # 256-dim blocks (one wave per SIMD in decode and prefill)
     "f16_d256_g8": (16, 2, 256, tk.KV_F16, 0),
     "f16_d192_g4": (8, 2, 192, tk.KV_F16, 0),
-    "f16_d200": (8, 2, 200, tk.KV_F16, 0),
+    "f16_d252": (8, 2, 252, tk.KV_F16, 0),
     "i8_d256_f16scales": (8, 2, 256, tk.KV_I8, tk.SCALE_F16),
     "i8_d160_f32scales_g8": (8, 1, 160, tk.KV_I8, tk.SCALE_F32),
 }

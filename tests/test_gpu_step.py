@@ -211,6 +211,9 @@ LARGE_STEP_CASES = {
     "i8_f32_group1": (8, 8, 128, tk.KV_I8, 1, [9000, 1, 255, 40, 600], 8, True),
     "short_sessions_first_pages": (28, 4, 128, tk.KV_I8, 0, [17000, 20, 3, 45, 0, 16], 4, True),
     "d256_append_first": (12, 2, 256, tk.KV_F16, 0, [30000, 5000, 8, 100], 8, False),
+    # a head off the 16-dim grid (100 dims in 128-dim blocks): the decode
+    # launch reads and stores the rows' own dims in runs of 4
+    "f16_d100_verify": (28, 4, 100, tk.KV_F16, 0, [9000, 37, 5000, 15, 3000, 300], 4, True),
     # many short sessions: shares of many units; more rows on one wave's
     # pages than it holds, so the append runs first
     "many_short": (28, 4, 128, tk.KV_I8, 0, [int(x) for x in np.random.default_rng(5).integers(0, 60, 160)]
