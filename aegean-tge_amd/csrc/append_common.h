@@ -136,7 +136,8 @@ __device__ __forceinline__ void load8(float (&x)[8], const float* src) {
 
 // Dims d0 .. d0 + 7 of one head's row (d0 a multiple of 8): the dims from
 // `dims` on read as zeros and are never loaded. Head sizes are multiples
-// of 4, so each run of 4 lies wholly inside or outside the head.
+// of 4, so each run of 4 lies wholly inside or outside the head. (Callers
+// keep a single 8-value load for heads that are multiples of 8.)
 __device__ __forceinline__ void load8_head(float (&x)[8], const float* head_row, int d0, int dims) {
   const float4 z = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
   const float4 f0 = d0 < dims ? *reinterpret_cast<const float4*>(head_row + d0) : z;

@@ -37,8 +37,13 @@ __global__ __launch_bounds__(256) void kv_append_kernel(AppendParams p) {
 
   // (dims past the head's own are stored as zeros)
   const int d0 = b * 32 + quarter * 8;
-  float x[8];
-  load8_head(x, (which ? p.v : p.k) + (size_t)row * p.kv_heads * p.dims + h * p.dims, d0, p.dims);
+  float x[8] = {0, 0, 0, 0, 0, 0, 0, 0};
+  const float* head_row = (which ? p.v : p.k) + (size_t)row * p.kv_heads * p.dims + h * p.dims;
+  if ((p.dims & 7) == 0) {
+    if (d0 < p.dims) load8(x, head_row + d0);
+  } else {
+    load8_head(x, head_row, d0, p.dims);
+  }
   store_lane<FMT>(p, x, p.rows[row], which, h, b, quarter, live);
 }
 

@@ -642,7 +642,11 @@ __device__ __forceinline__ void decode_body(const AttnParams& p,
         jobs[a].key = live ? (item << 16) | ((pos >> 4) & 0xffff) : -1;
 #pragma unroll
         for (int i = 0; i < 8; ++i) app_x[a][i] = 0.0f;  // (dims past the head's own store zeros)
-        if (live) load8_head(app_x[a], src + (size_t)kvrow * p.dims, d0, p.dims);
+        if (live && (p.dims & 7) == 0) {
+          if (d0 < p.dims) load8(app_x[a], src + (size_t)kvrow * p.dims + d0);
+        } else if (live) {
+          load8_head(app_x[a], src + (size_t)kvrow * p.dims, d0, p.dims);
+        }
       }
     }
   }

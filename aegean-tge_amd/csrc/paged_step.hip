@@ -220,7 +220,16 @@ __global__ __launch_bounds__(64 * kStepWaves) void paged_step_kernel(StepParams 
     jb.rr = RowRec{p.tables[rec.table_off + pos / 16], pos % 16, pos};
     const int d0 = jb.b * 32 + jb.quarter * 8;  // (dims past the head's own store zeros)
     const size_t off = (size_t)(rec.q_row + j) * kv_dim + rec.kv_head * dims;
-    load8_head(jb.x, (jb.which ? vbase : kbase) + off, d0, dims);
+    if ((dims & 7) == 0) {
+      // (the load is issued for every lane, at dim 0 past the head's end)
+      load8(jb.x, (jb.which ? vbase : kbase) + off + (d0 < dims ? d0 : 0));
+      if (d0 >= dims) {
+#pragma unroll
+        for (int i = 0; i < 8; ++i) jb.x[i] = 0.0f;
+      }
+    } else {
+      load8_head(jb.x, (jb.which ? vbase : kbase) + off, d0, dims);
+    }
   };
   Job job;
   if (lanes > 0) fetch_job(0, job);
