@@ -913,6 +913,10 @@ __device__ __forceinline__ void prefill_body(const AttnParams& p,
         for (int pp = 0; pp < NP; ++pp) u.q[rg][pp] = stage[(rg * NP + pp) * 64 + lane];
       }
     }
+    // Every second-half wave holds its operands before either half's first
+    // in-loop fetch refills the staging slots (the first half's tile
+    // barrier does not wait for the second half's reads).
+    lds_barrier();
   }
   u.set_sparse(p.sp_sink, p.sp_window, p.sp_stride,
                w.ctx + w.row_begin + (w.rows - 1) / w.rows_per_query + 1);
